@@ -1,0 +1,267 @@
+"""Benchmark of the Qwen3 attention hot path on one MI355X.
+
+Headline (the metric line): paged decode attention at the Qwen3-8B shape,
+batch 64, 32 q / 8 kv heads, head_dim 128, page 16, contexts U[512, 4096]
+(seed 2) -- microseconds per layer and achieved HBM bandwidth against the
+8 TB/s MI355X peak. A step is one decode-attention call over the batch
+(one kernel: split-K partials merged in the same launch). Three copies of the
+KV pool are rotated so repeated steps cannot be served from the 256 MB MALL.
+The kernel's own duration is taken with HIP events on the stream it runs on.
+
+Also measured (in "secondary"): the whole decode block (fused QK
+norm+RoPE+store, then attention), the varlen prefill at the Qwen3-8B
+16-sequence shape (TFLOP/s against 2.5 PFLOP/s bf16 dense), the Qwen3-32B
+bs32 32k-context decode, and the Qwen3-4B mixed batch (prefill+store then
+decode). The CPU baseline runs the reference's CPU decode path (per-token
+gather loop + repeat_interleave + SDPA, restated in the oracle) on a bounded
+sample of the same batch on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+METRIC = "paged decode attn µs/layer + achieved HBM TB/s (% peak), Qwen3-8B shape bs64"
+
+
+def _events_time(fn, steps, warmup):
+    """Run fn(i) warmup + steps times; return (wall_s_total, per-step event ms list)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn(warmup + i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def bench_decode(name, steps, warmup, tiles_per_split=0, copies=3, with_block=False):
+    from tinyserver_amd import workloads as W
+    from tinyserver_amd.kernels import paged_attention_forward, qk_norm_rope_store
+
+    dev = torch.device("cuda:0")
+    w = W.make(name, device=dev)
+    B = len(w.ctx_lens)
+    seq_lens = w.ctx_lens.to(torch.int32).to(dev)
+    pools = [(w.k_cache, w.v_cache)] + [(w.k_cache.clone(), w.v_cache.clone()) for _ in range(copies - 1)]
+    cu = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    q_rot, _ = qk_norm_rope_store(w.q, w.k, w.v, w.q_weight, w.k_weight, w.cos, w.sin, w.eps, pools[0][0],
+                                  pools[0][1], w.block_tables, cu, w.positions.to(dev), return_k=False)
+    out = torch.empty_like(q_rot)
+
+    def attn(i):
+        kc, vc = pools[i % copies]
+        paged_attention_forward(q_rot, kc, vc, w.block_tables, W.PAGE, seq_lens, tiles_per_split=tiles_per_split,
+                                out=out)
+
+    wall, ev = _events_time(attn, steps, warmup)
+    nbytes = W.decode_bytes(w.ctx_lens, w.num_heads, w.num_kv_heads)
+    res = {
+        "workload": name,
+        "batch": B,
+        "num_heads": w.num_heads,
+        "num_kv_heads": w.num_kv_heads,
+        "sum_ctx": int(w.ctx_lens.sum()),
+        "bytes_per_call": nbytes,
+        "kernel_us_mean": statistics.mean(ev) * 1e3,
+        "kernel_us_median": statistics.median(ev) * 1e3,
+        "kernel_us_p10": sorted(ev)[len(ev) // 10] * 1e3,
+        "kernel_us_p90": sorted(ev)[(9 * len(ev)) // 10] * 1e3,
+        "wall_ms_per_step": wall / steps * 1e3,
+    }
+    res["achieved_gbs"] = nbytes / (res["kernel_us_mean"] * 1e-6) / 1e9
+    res["pct_peak_hbm"] = 100.0 * res["achieved_gbs"] / HBM_PEAK_GBS
+    res["tokens_per_s"] = B / (res["kernel_us_mean"] * 1e-6)
+    if with_block:
+        qw, kw, cos, sin, pos = w.q_weight, w.k_weight, w.cos, w.sin, w.positions.to(dev)
+
+        def block(i):
+            kc, vc = pools[i % copies]
+            qr, _ = qk_norm_rope_store(w.q, w.k, w.v, qw, kw, cos, sin, w.eps, kc, vc, w.block_tables, cu, pos,
+                                       return_k=False)
+            paged_attention_forward(qr, kc, vc, w.block_tables, W.PAGE, seq_lens, tiles_per_split=tiles_per_split,
+                                    out=out)
+
+        _, evb = _events_time(block, steps, warmup)
+        res["block_us_mean"] = statistics.mean(evb) * 1e3
+    return res, w
+
+
+def bench_prefill(name, steps, warmup):
+    from tinyserver_amd import workloads as W
+    from tinyserver_amd.kernels import flash_attn_varlen_func, qk_norm_rope_store
+
+    dev = torch.device("cuda:0")
+    w = W.make(name, device=dev)
+    T = w.q.shape[0]
+    hq = w.q.shape[1]
+    q_rot, k_rot = qk_norm_rope_store(w.q, w.k, w.v, w.q_weight, w.k_weight, w.cos, w.sin, w.eps, w.k_cache,
+                                      w.v_cache, w.block_tables, w.cu_seqlens)
+    out = torch.empty_like(q_rot)
+
+    def attn(i):
+        flash_attn_varlen_func(q_rot, k_rot, w.v, w.cu_seqlens, w.cu_seqlens, w.max_seqlen, w.max_seqlen, True, out=out)
+
+    _, ev = _events_time(attn, steps, warmup)
+    flops = W.prefill_flops(w.seq_lens, hq)
+    us = statistics.mean(ev) * 1e3
+
+    def block(i):
+        qr, kr = qk_norm_rope_store(w.q, w.k, w.v, w.q_weight, w.k_weight, w.cos, w.sin, w.eps, w.k_cache,
+                                    w.v_cache, w.block_tables, w.cu_seqlens)
+        flash_attn_varlen_func(qr, kr, w.v, w.cu_seqlens, w.cu_seqlens, w.max_seqlen, w.max_seqlen, True, out=out)
+
+    _, evb = _events_time(block, steps, warmup)
+    return {
+        "workload": name,
+        "tokens": T,
+        "gflop": flops / 1e9,
+        "kernel_us_mean": us,
+        "tflops": flops / (us * 1e-6) / 1e12,
+        "pct_peak_mfma": 100.0 * flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
+        "tokens_per_s": T / (us * 1e-6),
+        "block_us_mean": statistics.mean(evb) * 1e3,
+    }
+
+
+def cpu_baseline(w, sample_seqs=8, reps=3):
+    """The reference's CPU decode path (gather loop + repeat_interleave + SDPA) on
+    the first `sample_seqs` sequences of the same batch, timed on this host."""
+    from oracle import paged as op
+
+    n = min(sample_seqs, len(w.ctx_lens))
+    pages = sorted({p for lst in w.block_lists[:n] for p in lst})
+    remap = {p: i for i, p in enumerate(pages)}
+    idx = torch.tensor(pages, device=w.k_cache.device)
+    kc, vc = w.k_cache[idx].cpu(), w.v_cache[idx].cpu()
+    tables = [[remap[p] for p in lst] for lst in w.block_lists[:n]]
+    q = w.q[:n].cpu().transpose(0, 1).unsqueeze(0).contiguous()  # (1, Hq, n, D)
+    positions = [int(x) - 1 for x in w.ctx_lens[:n]]
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        op.decode_cpu_path(q, kc, vc, tables, positions, literal_gather=True)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    from tinyserver_amd import workloads as W
+
+    nbytes = W.decode_bytes(w.ctx_lens[:n], w.num_heads, w.num_kv_heads)
+    return {
+        "value": nbytes / t / 1e12,
+        "unit": "TB/s",
+        "cores": torch.get_num_threads(),
+        "host_cpus": os.cpu_count(),
+        "kind": "port",
+        "sample": f"reference CPU decode path (per-token gather loop + repeat_interleave + SDPA) on the first {n} of "
+                  f"{len(w.ctx_lens)} sequences ({int(w.ctx_lens[:n].sum())} context tokens), median of {reps} runs",
+        "sample_seconds": t,
+        "us_per_layer_full_batch_est": t * 1e6 * float(w.ctx_lens.sum()) / float(w.ctx_lens[:n].sum()),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--tiles-per-split", type=int, default=0)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: the attention path runs on a single MI355X here; --gpus must be 1",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    from tinyserver_amd import _lib
+
+    _lib.load()
+    head, w = bench_decode("qwen3-8b-decode-bs64", args.steps, args.warmup, args.tiles_per_split, with_block=True)
+    line = {
+        "metric": METRIC,
+        "value": round(head["achieved_gbs"] / 1000.0, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["wall_ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 K/V pool, shuffled page-16 block tables)",
+        "config": {
+            "workload": "qwen3-8b-decode-bs64",
+            "batch": head["batch"],
+            "num_heads": head["num_heads"],
+            "num_kv_heads": head["num_kv_heads"],
+            "head_dim": 128,
+            "page": 16,
+            "ctx": "U[512,4096], seed 2",
+            "sum_ctx": head["sum_ctx"],
+            "tiles_per_split": args.tiles_per_split,
+        },
+        "us_per_layer": round(head["kernel_us_mean"], 2),
+        "us_per_layer_median": round(head["kernel_us_median"], 2),
+        "us_per_layer_p10_p90": [round(head["kernel_us_p10"], 2), round(head["kernel_us_p90"], 2)],
+        "pct_peak_hbm": round(head["pct_peak_hbm"], 2),
+        "tokens_per_s": round(head["tokens_per_s"], 1),
+        "decode_block_us_per_layer": round(head["block_us_mean"], 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(head["achieved_gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(head["achieved_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "paged_decode_mfma<bf16,128,page16>",
+            "bytes_per_launch": head["bytes_per_call"],
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(w)
+    del w
+    torch.cuda.empty_cache()
+    if not args.no_secondary:
+        sec = {}
+        s, w2 = bench_decode("qwen3-32b-decode-bs32", max(10, args.steps // 5), 3, copies=1)
+        del w2
+        torch.cuda.empty_cache()
+        sec["qwen3-32b-decode-bs32"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in s.items()}
+        s, w2 = bench_decode("qwen3-4b-mixed-decode", max(10, args.steps // 5), 3)
+        del w2
+        sec["qwen3-4b-mixed-decode"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in s.items()}
+        for name in ("qwen3-8b-prefill-16seq", "qwen3-4b-mixed-prefill"):
+            s = bench_prefill(name, max(10, args.steps // 5), 3)
+            sec[name] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in s.items()}
+        line["secondary"] = sec
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

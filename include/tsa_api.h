@@ -1,0 +1,158 @@
+/*
+ * tsa_api.h -- C ABI of the MI355X (gfx950) Qwen3 attention hot path.
+ *
+ * One shared library, libtsa.so, built with hipcc for gfx950. Every entry
+ * point takes plain views of caller-owned device memory plus a HIP stream
+ * (passed as void*, so no HIP header is needed to bind it) and returns an int
+ * status. The library never allocates device memory: outputs and the decode
+ * workspace are passed in by the caller. Launches are asynchronous on the
+ * given stream; nothing synchronises.
+ *
+ * Status codes: TSA_OK (0); TSA_ERR_INVALID (-1) for an argument that the
+ * reference would reject or that is malformed (message from tsa_last_error);
+ * TSA_ERR_UNSUPPORTED (-2) for a well-formed call outside what the kernels
+ * implement (for example head_dim 96); TSA_ERR_LAUNCH (-3) for a HIP error.
+ * tsa_last_error() is per calling thread.
+ *
+ * Reference interfaces replaced (paths relative to the tinyserver repository):
+ *   tsa_store_kv            server/model/kernels/kv_cache.py:73-119   (store_kv_cache)
+ *   tsa_store_kv_mapped     server/model/kernels/kv_cache.py:194-251  (store_kv_cache_batched)
+ *   tsa_store_kv_paged      server/model/patches/qwen3.py:296-318, 335-357
+ *                           (the per-token mapping loop and per-sequence store
+ *                           loop at the call site, done on the device)
+ *   tsa_qk_norm_rope        server/model/patches/qwen3.py:268-287 (q_norm, k_norm,
+ *                           apply_rotary_pos_emb; transformers
+ *                           models/qwen3/modeling_qwen3.py:59-64, 140-170)
+ *   tsa_qk_norm_rope_store  the same, fused with tsa_store_kv_paged
+ *   tsa_paged_decode        server/model/kernels/paged_attention.py:124-192
+ *                           (paged_attention_forward)
+ *   tsa_varlen_prefill      server/model/kernels/varlen_attention.py:145-218
+ *                           (flash_attn_varlen_func)
+ */
+#ifndef TSA_API_H
+#define TSA_API_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSA_ABI_VERSION 1
+
+enum tsa_status {
+  TSA_OK = 0,
+  TSA_ERR_INVALID = -1,
+  TSA_ERR_UNSUPPORTED = -2,
+  TSA_ERR_LAUNCH = -3,
+};
+
+enum tsa_dtype {
+  TSA_BF16 = 0,
+  TSA_F16 = 1,
+  TSA_F32 = 2,
+  TSA_I32 = 3,
+  TSA_I64 = 4,
+};
+
+/* A strided view of caller-owned device memory: element (i0, i1, ...) sits at
+ * data + sum(i_d * stride[d]) elements. Sizes and strides are in elements,
+ * outermost first; entries past ndim are ignored. */
+typedef struct tsa_view {
+  void* data;
+  int64_t size[4];
+  int64_t stride[4];
+  int32_t ndim;
+  int32_t dtype; /* enum tsa_dtype */
+} tsa_view;
+
+/* ABI version of the loaded library (TSA_ABI_VERSION). */
+int tsa_abi_version(void);
+
+/* Message for the last non-zero status returned on this thread. */
+const char* tsa_last_error(void);
+
+/* store_kv_cache (kv_cache.py:73-119): for one sequence, token i of
+ * k_src/v_src (Hkv, n, D) goes to absolute position start_position + i:
+ * cache[block_table[p / BS], h, p % BS, :] for k_cache/v_cache
+ * (NB, Hkv, BS, D). block_table: (n_blocks,) int32. Positions whose logical
+ * block is past the table, or whose block id is outside [0, NB), are not
+ * written. */
+int tsa_store_kv(const tsa_view* k_src, const tsa_view* v_src, const tsa_view* k_cache,
+                 const tsa_view* v_cache, const tsa_view* block_table, int64_t start_position,
+                 void* stream);
+
+/* store_kv_cache_batched (kv_cache.py:194-251): token t of k_src/v_src
+ * (Hkv, T, D) goes to cache[block_mapping[t], h, slot_mapping[t], :].
+ * block_mapping/slot_mapping: (T,) int32 or int64. Out-of-range ids are
+ * skipped. */
+int tsa_store_kv_mapped(const tsa_view* k_src, const tsa_view* v_src, const tsa_view* k_cache,
+                        const tsa_view* v_cache, const tsa_view* block_mapping,
+                        const tsa_view* slot_mapping, void* stream);
+
+/* Device-side addressing for a whole batch (replaces qwen3.py:296-318 and
+ * :335-357). Tokens of sequence s are k_src[:, cu_seqlens[s]:cu_seqlens[s+1], :];
+ * token t sits at position positions[t] when positions is non-NULL (int32 or
+ * int64, (T,)), else at t - cu_seqlens[s] (prefill). It is written to
+ * cache[block_tables[s, p / BS], h, p % BS, :]. block_tables: (nseq, max_blocks)
+ * int32; cu_seqlens: (nseq + 1,) int32. */
+int tsa_store_kv_paged(const tsa_view* k_src, const tsa_view* v_src, const tsa_view* k_cache,
+                       const tsa_view* v_cache, const tsa_view* block_tables,
+                       const tsa_view* cu_seqlens, const tsa_view* positions, void* stream);
+
+/* Fused Qwen3 per-head RMSNorm + rotate-half RoPE with HF's rounding points:
+ * y = w * round(x * rsqrt(mean(x^2) + eps)); out = round(round(y*cos) +
+ * round(rotate_half(y)*sin)). q: (T, Hq, D), k: (T, Hkv, D) inputs;
+ * q_out/k_out same shapes (may alias the inputs); q_weight/k_weight: (D,);
+ * cos/sin: (T, D) in the model dtype. eps is rounded to fp32 as HF does. */
+int tsa_qk_norm_rope(const tsa_view* q, const tsa_view* k, const tsa_view* q_out,
+                     const tsa_view* k_out, const tsa_view* q_weight, const tsa_view* k_weight,
+                     const tsa_view* cos, const tsa_view* sin, double eps, void* stream);
+
+/* tsa_qk_norm_rope plus the paged store of the rotated K and of v (T, Hkv, D)
+ * into k_cache/v_cache with tsa_store_kv_paged's addressing. k_out may have
+ * data == NULL when the caller needs the rotated K only in the cache. */
+int tsa_qk_norm_rope_store(const tsa_view* q, const tsa_view* k, const tsa_view* v,
+                           const tsa_view* q_out, const tsa_view* k_out,
+                           const tsa_view* q_weight, const tsa_view* k_weight,
+                           const tsa_view* cos, const tsa_view* sin, double eps,
+                           const tsa_view* k_cache, const tsa_view* v_cache,
+                           const tsa_view* block_tables, const tsa_view* cu_seqlens,
+                           const tsa_view* positions, void* stream);
+
+/* Bytes of partial-result workspace tsa_paged_decode needs for this shape and
+ * split size (tiles_per_split 0 = the library's choice; a tile is 16 tokens).
+ * 0 when every sequence fits one split. */
+size_t tsa_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads,
+                                        int64_t head_dim, int64_t max_blocks_per_seq,
+                                        int64_t block_size, int32_t tiles_per_split);
+
+/* paged_attention_forward (paged_attention.py:124-192):
+ * out[s, h] = softmax(query[s, h] . K_s^T * softmax_scale) V_s over the first
+ * seq_lens[s] tokens gathered through block_tables[s], kv head h / (Hq/Hkv).
+ * query/out: (B, Hq, D); caches (NB, Hkv, BS, D); block_tables (B, max_blocks)
+ * int32; seq_lens (B,) int32. workspace holds split-K partial results (no
+ * initialisation needed; calls that share one must be ordered on one stream).
+ * Two launches when a sequence spans several splits: the split kernel and a
+ * merge kernel. */
+int tsa_paged_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache,
+                     const tsa_view* v_cache, const tsa_view* block_tables,
+                     const tsa_view* seq_lens, double softmax_scale, void* workspace,
+                     size_t workspace_bytes, int32_t tiles_per_split, void* stream);
+
+/* flash_attn_varlen_func (varlen_attention.py:145-218): per sequence b and
+ * q-head h, softmax(q k^T * softmax_scale) v over keys cu_seqlens_k[b] ..
+ * cu_seqlens_k[b+1], kv head h / (Hq/Hkv); causal masks key j > query i
+ * (positions within the sequence, top-left aligned). q/out: (Tq, Hq, D);
+ * k/v: (Tk, Hkv, D); cu_seqlens_*: (b + 1,) int32. */
+int tsa_varlen_prefill(const tsa_view* out, const tsa_view* q, const tsa_view* k,
+                       const tsa_view* v, const tsa_view* cu_seqlens_q,
+                       const tsa_view* cu_seqlens_k, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                       int32_t causal, double softmax_scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TSA_API_H */

@@ -1,0 +1,190 @@
+"""Paged decode attention on the GPU vs the oracle.
+
+The oracle restates the reference kernel (paged_attention.py:8-121) in fp32.
+Cases: the reference's own three configurations, query not mutated, shape and
+dtype, the poisoned partial last block (tests/model/test_paged_attention_kernel.py:
+109-222); the Qwen3-0.6B-shaped decode step end to end (norm+RoPE+store then
+attend); GQA groups 1..16, head_dim 64/128, page sizes 4..64; split-K with
+forced small splits, called twice to show the merge counters reset; seq_len 1
+(output = the V row); the full Qwen3-8B bs64 and Qwen3-32B bs32 shapes checked
+on sampled sequences. Tolerance for bf16/fp16: max-abs 2e-2, mean-abs 2e-3;
+fp32 (generic kernel): the reference test's 1e-3.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import kv_store as ok
+from oracle import norm_rope as onr
+from oracle import paged as op
+from tests.helpers import assert_close
+from tinyserver_amd import workloads as W
+from tinyserver_amd.kernels import paged_attention_forward, qk_norm_rope_store
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _random_paged_inputs(seq_lens, num_heads, num_kv_heads, head_dim, block_size, dtype, seed):
+    """The reference test's generator (test_paged_attention_kernel.py:67-106): disjoint
+    shuffled physical blocks plus 3 spare ones, zero-padded tables."""
+    gen = torch.Generator().manual_seed(seed)
+    blocks_per_seq = [max(1, math.ceil(n / block_size)) for n in seq_lens]
+    num_blocks = sum(blocks_per_seq) + 3
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=gen).to(dtype)
+
+    query = randn(len(seq_lens), num_heads, head_dim)
+    k_cache = randn(num_blocks, num_kv_heads, block_size, head_dim)
+    v_cache = randn(num_blocks, num_kv_heads, block_size, head_dim)
+    phys = torch.randperm(num_blocks, generator=gen)[: sum(blocks_per_seq)]
+    bt = torch.zeros(len(seq_lens), max(blocks_per_seq), dtype=torch.int32)
+    cur = 0
+    for s, n in enumerate(blocks_per_seq):
+        bt[s, :n] = phys[cur : cur + n].to(torch.int32)
+        cur += n
+    return query, k_cache, v_cache, bt, torch.tensor(seq_lens, dtype=torch.int32)
+
+
+def _run(query, k_cache, v_cache, bt, bs, sl, **kw):
+    out = paged_attention_forward(query.to(DEV), k_cache.to(DEV), v_cache.to(DEV), bt.to(DEV), bs, sl.to(DEV), **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+REF_CONFIGS = [
+    (4, 4, 64, 16, [10]),
+    (8, 2, 64, 16, [7, 16, 40]),
+    (16, 4, 128, 32, [1, 33, 64]),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cfg", range(len(REF_CONFIGS)))
+def test_reference_configs(cfg, dtype):
+    hq, hkv, d, bs, lens = REF_CONFIGS[cfg]
+    args = _random_paged_inputs(lens, hq, hkv, d, bs, dtype, seed=0)
+    out = _run(*args[:4], bs, args[4])
+    ref = op.paged_attention_forward(*args[:4], bs, args[4])
+    tol = dict(max_abs=1e-3, mean_abs=1e-3) if dtype == torch.float32 else {}
+    assert out.dtype == dtype and out.shape == args[0].shape
+    assert_close(out, ref, what=f"cfg{cfg} {dtype}", **tol)
+
+
+def test_query_not_mutated():
+    q, kc, vc, bt, sl = _random_paged_inputs([12, 5], 8, 2, 64, 16, torch.bfloat16, seed=1)
+    qd = q.to(DEV)
+    before = qd.clone()
+    paged_attention_forward(qd, kc.to(DEV), vc.to(DEV), bt.to(DEV), 16, sl.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(qd, before)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_partial_last_block_masked(dtype):
+    q, kc, vc, bt, sl = _random_paged_inputs([5], 8, 2, 64, 16, dtype, seed=3)
+    blk = int(bt[0, 0])
+    kc[blk, :, 5:, :] = 1e4
+    vc[blk, :, 5:, :] = 1e4
+    out = _run(q, kc, vc, bt, 16, sl)
+    ref = op.paged_attention_forward(q, kc, vc, bt, 16, sl)
+    tol = dict(max_abs=1e-3, mean_abs=1e-3) if dtype == torch.float32 else {}
+    assert_close(out, ref, what="poison", **tol)
+
+
+def test_nonfinite_unused_slots_do_not_leak():
+    q, kc, vc, bt, sl = _random_paged_inputs([21], 8, 2, 128, 16, torch.bfloat16, seed=4)
+    blk = int(bt[0, 1])
+    kc[blk, :, 5:, :] = float("nan")
+    vc[blk, :, 5:, :] = float("inf")
+    out = _run(q, kc, vc, bt, 16, sl)
+    ref = op.paged_attention_forward(q, kc, vc, bt, 16, sl)
+    assert_close(out, ref, what="nan/inf slots")
+
+
+@pytest.mark.parametrize("group", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_gqa_groups(group, head_dim):
+    hkv = 2
+    q, kc, vc, bt, sl = _random_paged_inputs([1, 17, 300, 64], hkv * group, hkv, head_dim, 16, torch.bfloat16,
+                                             seed=group)
+    out = _run(q, kc, vc, bt, 16, sl)
+    ref = op.paged_attention_forward(q, kc, vc, bt, 16, sl)
+    assert_close(out, ref, what=f"G={group} D={head_dim}")
+
+
+@pytest.mark.parametrize("block_size", [4, 8, 32, 64])
+def test_page_sizes(block_size):
+    q, kc, vc, bt, sl = _random_paged_inputs([3, 50, 129, 16], 16, 4, 128, block_size, torch.bfloat16, seed=7)
+    out = _run(q, kc, vc, bt, block_size, sl)
+    ref = op.paged_attention_forward(q, kc, vc, bt, block_size, sl)
+    assert_close(out, ref, what=f"BS={block_size}")
+
+
+@pytest.mark.parametrize("tiles_per_split", [4, 8, 16])
+def test_split_k_merge(tiles_per_split):
+    """Many splits per sequence; the second call checks the counters reset."""
+    q, kc, vc, bt, sl = _random_paged_inputs([2000, 1, 777, 4096, 64], 32, 8, 128, 16, torch.bfloat16, seed=9)
+    ref = op.paged_attention_forward(q, kc, vc, bt, 16, sl)
+    for call in range(2):
+        out = _run(q, kc, vc, bt, 16, sl, tiles_per_split=tiles_per_split)
+        assert_close(out, ref, what=f"tps={tiles_per_split} call {call}")
+
+
+def test_seq_len_one_returns_v_row():
+    q, kc, vc, bt, sl = _random_paged_inputs([1, 1], 8, 2, 128, 16, torch.bfloat16, seed=5)
+    out = _run(q, kc, vc, bt, 16, sl).cpu()
+    for s in range(2):
+        for h in range(8):
+            assert torch.equal(out[s, h], vc[int(bt[s, 0]), h // 4, 0]), (s, h)
+
+
+def test_decode_step_qwen3_0p6b():
+    """Norm+RoPE+store, then attend (the decode branch, qwen3.py:328-409), vs the oracle."""
+    w = W.make("qwen3-0.6b-decode-bs4", poison=True)
+    b = len(w.ctx_lens)
+    # oracle
+    qr, kr = onr.qk_norm_rope(w.q[None], w.k[None], w.q_weight, w.k_weight, w.cos[None], w.sin[None], w.eps)
+    kc_ref, vc_ref = w.k_cache.clone(), w.v_cache.clone()
+    for i in range(b):
+        ok.store_kv_cache(int(w.positions[i]), torch.tensor(w.block_lists[i]), kr[0][:, i : i + 1],
+                          w.v[i][:, None], kc_ref, vc_ref)
+    ref = op.paged_attention_forward(qr[0].transpose(0, 1).contiguous(), kc_ref, vc_ref, w.block_tables, 16,
+                                     w.ctx_lens.to(torch.int32))
+    # GPU
+    g = w.to(DEV)
+    qg, _ = qk_norm_rope_store(g.q, g.k, g.v, g.q_weight, g.k_weight, g.cos, g.sin, g.eps, g.k_cache, g.v_cache,
+                               g.block_tables, torch.arange(b + 1, dtype=torch.int32, device=DEV), g.positions,
+                               return_k=False)
+    out = paged_attention_forward(qg, g.k_cache, g.v_cache, g.block_tables, 16, g.ctx_lens.to(torch.int32))
+    torch.cuda.synchronize()
+    assert_close(out, ref, what="decode step")
+
+
+def _sampled_check(w, seqs, tiles_per_split=0):
+    """w lives on the GPU; each sampled sequence is checked against the oracle on
+    a compact CPU copy of just its pages."""
+    out = paged_attention_forward(w.q, w.k_cache, w.v_cache, w.block_tables, 16, w.ctx_lens.to(torch.int32).to(DEV),
+                                  tiles_per_split=tiles_per_split)
+    torch.cuda.synchronize()
+    for s in seqs:
+        pages = torch.tensor(w.block_lists[s], device=DEV)
+        kc, vc = w.k_cache[pages].cpu(), w.v_cache[pages].cpu()
+        bt = torch.arange(len(pages), dtype=torch.int32)[None]
+        sl = w.ctx_lens[s : s + 1].to(torch.int32).cpu()
+        ref = op.paged_attention_forward(w.q[s : s + 1].cpu(), kc, vc, bt, 16, sl)
+        assert_close(out[s : s + 1], ref, what=f"{w.name} seq {s} ctx {int(sl)}")
+
+
+def test_qwen3_8b_bs64_sampled():
+    w = W.make("qwen3-8b-decode-bs64", device=DEV)
+    order = torch.argsort(w.ctx_lens.cpu())
+    _sampled_check(w, [int(order[0]), int(order[len(order) // 2]), int(order[-1]), 7])
+
+
+def test_qwen3_32b_bs32_sampled():
+    w = W.make("qwen3-32b-decode-bs32", device=DEV)
+    _sampled_check(w, [0, 31])

@@ -1,0 +1,121 @@
+"""Varlen causal prefill on the GPU vs the oracle.
+
+The oracle restates the reference kernel (varlen_attention.py:8-142): 32-key
+online softmax, top-left causal mask, P rounded to the V dtype before P.V.
+Cases: the reference's self-test configuration (varlen_attention.py:257-307:
+fp16, seed 42, 4 sequences of U[32,256] tokens, 16/4 heads, D 64, causal and
+not), bf16/fp16/fp32, GQA groups, q_len != k_len, length-1 sequences, the
+call site's strided (T, H, D) views (qwen3.py:199-201), and the full
+Qwen3-8B-shaped 16-sequence prefill checked on sampled sequences and heads.
+Tolerance: max-abs 2e-2, mean-abs 2e-3 for 16-bit dtypes (the reference's
+own fp16 check is max 5e-2, mean 1e-3); fp32 1e-4.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import varlen as ov
+from tests.helpers import assert_close
+from tinyserver_amd import workloads as W
+from tinyserver_amd.kernels import flash_attn_varlen_func
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _cu(lens):
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+    return cu
+
+
+def _inputs(lens_q, lens_k, hq, hkv, d, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(sum(lens_q), hq, d, generator=g).to(dtype)
+    k = torch.randn(sum(lens_k), hkv, d, generator=g).to(dtype)
+    v = torch.randn(sum(lens_k), hkv, d, generator=g).to(dtype)
+    return q, k, v, _cu(lens_q), _cu(lens_k)
+
+
+def _tol(dtype):
+    return dict(max_abs=1e-4, mean_abs=1e-5) if dtype == torch.float32 else {}
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_reference_selftest_config(causal):
+    torch.manual_seed(42)
+    lens = torch.randint(32, 257, (4,)).tolist()
+    q, k, v, cu, _ = _inputs(lens, lens, 16, 4, 64, torch.float16, seed=42)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV), cu.to(DEV), max(lens), max(lens),
+                                 causal=causal, softmax_scale=1.0 / math.sqrt(64))
+    torch.cuda.synchronize()
+    ref = ov.flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), causal, 1.0 / math.sqrt(64))
+    assert_close(out, ref, what=f"selftest causal={causal}")
+    # and the reference's own looser check against its naive restatement
+    naive = ov.reference_attn_varlen(q.float(), k.float(), v.float(), cu, cu, causal, 1.0 / math.sqrt(64))
+    assert_close(out, naive, max_abs=5e-2, mean_abs=1e-3, what="vs naive")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("group", [1, 4, 8])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_matches_oracle(dtype, group, head_dim):
+    lens = [1, 31, 32, 33, 100, 257]
+    q, k, v, cu, _ = _inputs(lens, lens, 2 * group, 2, head_dim, dtype, seed=group)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV), cu.to(DEV), max(lens), max(lens), True)
+    torch.cuda.synchronize()
+    ref = ov.flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), True)
+    assert_close(out, ref, what=f"{dtype} G={group} D={head_dim}", **_tol(dtype))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_q_len_differs_from_k_len(causal):
+    lq, lk = [5, 40, 64], [9, 33, 100]
+    q, k, v, cq, ck = _inputs(lq, lk, 8, 2, 128, torch.bfloat16, seed=3)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cq.to(DEV), ck.to(DEV), max(lq), max(lk), causal)
+    torch.cuda.synchronize()
+    ref = ov.flash_attn_varlen_func(q, k, v, cq, ck, max(lq), max(lk), causal)
+    assert_close(out, ref, what=f"lq!=lk causal={causal}")
+
+
+def test_single_token_sequences_return_v():
+    lens = [1, 1, 1]
+    q, k, v, cu, _ = _inputs(lens, lens, 8, 2, 128, torch.bfloat16, seed=5)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV), cu.to(DEV), 1, 1, True).cpu()
+    for t in range(3):
+        for h in range(8):
+            assert torch.equal(out[t, h], v[t, h // 4])
+
+
+def test_call_site_strided_views():
+    """q/k/v as (1, H, T, D) tensors squeezed and transposed, as qwen3.py:199-201 passes them."""
+    lens = [70, 129, 3]
+    q, k, v, cu, _ = _inputs(lens, lens, 16, 8, 128, torch.bfloat16, seed=6)
+    qh = q.transpose(0, 1).contiguous()[None].to(DEV)  # (1, Hq, T, D)
+    kh = k.transpose(0, 1).contiguous()[None].to(DEV)
+    vh = v.transpose(0, 1).contiguous()[None].to(DEV)
+    out = flash_attn_varlen_func(qh.squeeze(0).transpose(0, 1), kh.squeeze(0).transpose(0, 1),
+                                 vh.squeeze(0).transpose(0, 1), cu.to(DEV), cu.to(DEV), max(lens), max(lens),
+                                 causal=True, softmax_scale=128**-0.5)
+    torch.cuda.synchronize()
+    ref = ov.flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), True, 128**-0.5)
+    assert_close(out, ref, what="strided views")
+
+
+def test_qwen3_8b_prefill_sampled():
+    w = W.make("qwen3-8b-prefill-16seq", device=DEV)
+    out = flash_attn_varlen_func(w.q, w.k, w.v, w.cu_seqlens, w.cu_seqlens, w.max_seqlen, w.max_seqlen, True)
+    torch.cuda.synchronize()
+    cu = w.cu_seqlens.tolist()
+    order = sorted(range(len(cu) - 1), key=lambda s: cu[s + 1] - cu[s])
+    for s in (order[0], order[-1]):
+        a, b = cu[s], cu[s + 1]
+        heads = [0, 13, 31]
+        sub_q = w.q[a:b, heads].cpu()
+        sub_k = w.k[a:b, [h // 4 for h in heads]].cpu()
+        sub_v = w.v[a:b, [h // 4 for h in heads]].cpu()
+        c1 = torch.tensor([0, b - a], dtype=torch.int32)
+        ref = ov.flash_attn_varlen_func(sub_q, sub_k, sub_v, c1, c1, b - a, b - a, True)
+        assert_close(out[a:b, heads], ref, what=f"seq {s} len {b - a}")

@@ -1,0 +1,134 @@
+"""ctypes binding of libtsa.so (include/tsa_api.h).
+
+Tensors cross the boundary as ``tsa_view`` structs (data pointer, sizes,
+element strides, dtype); the HIP stream is torch's current stream on the
+tensor's device. There is no CPU fallback: a missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_double, c_int, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libtsa.so"
+
+TSA_OK, TSA_ERR_INVALID, TSA_ERR_UNSUPPORTED, TSA_ERR_LAUNCH = 0, -1, -2, -3
+TSA_BF16, TSA_F16, TSA_F32, TSA_I32, TSA_I64 = 0, 1, 2, 3, 4
+_DTYPES = {
+    torch.bfloat16: TSA_BF16,
+    torch.float16: TSA_F16,
+    torch.float32: TSA_F32,
+    torch.int32: TSA_I32,
+    torch.int64: TSA_I64,
+}
+
+
+class TsaView(ctypes.Structure):
+    _fields_ = [
+        ("data", c_void_p),
+        ("size", c_int64 * 4),
+        ("stride", c_int64 * 4),
+        ("ndim", c_int32),
+        ("dtype", c_int32),
+    ]
+
+
+_V = POINTER(TsaView)
+
+# name -> (restype, argtypes); mirrors include/tsa_api.h.
+SIGNATURES = {
+    "tsa_abi_version": (c_int, []),
+    "tsa_last_error": (ctypes.c_char_p, []),
+    "tsa_store_kv": (c_int, [_V, _V, _V, _V, _V, c_int64, c_void_p]),
+    "tsa_store_kv_mapped": (c_int, [_V, _V, _V, _V, _V, _V, c_void_p]),
+    "tsa_store_kv_paged": (c_int, [_V, _V, _V, _V, _V, _V, _V, c_void_p]),
+    "tsa_qk_norm_rope": (c_int, [_V, _V, _V, _V, _V, _V, _V, _V, c_double, c_void_p]),
+    "tsa_qk_norm_rope_store": (
+        c_int,
+        [_V, _V, _V, _V, _V, _V, _V, _V, _V, c_double, _V, _V, _V, _V, _V, c_void_p],
+    ),
+    "tsa_paged_decode_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int32]),
+    "tsa_paged_decode": (
+        c_int,
+        [_V, _V, _V, _V, _V, _V, c_double, c_void_p, c_size_t, c_int32, c_void_p],
+    ),
+    "tsa_varlen_prefill": (c_int, [_V, _V, _V, _V, _V, _V, c_int64, c_int64, c_int32, c_double, c_void_p]),
+}
+
+ABI_VERSION = 1
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libtsa.so once. Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build the HIP library first "
+                "(python -m tinyserver_amd._build or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.tsa_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"libtsa.so ABI {lib.tsa_abi_version()} != expected {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def view(t: torch.Tensor | None) -> TsaView | None:
+    """Describe a tensor for the C ABI (None stays None -> NULL)."""
+    if t is None:
+        return None
+    if t.dim() > 4:
+        raise ValueError(f"tensors of rank > 4 are not supported (got {t.dim()})")
+    if t.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {t.dtype}")
+    v = TsaView()
+    v.data = t.data_ptr() if t.numel() else None
+    for i, (n, s) in enumerate(zip(t.shape, t.stride())):
+        v.size[i] = n
+        v.stride[i] = s
+    v.ndim = t.dim()
+    v.dtype = _DTYPES[t.dtype]
+    return v
+
+
+def ref(v: TsaView | None):
+    return ctypes.byref(v) if v is not None else None
+
+
+def check(rc: int, what: str) -> None:
+    if rc == TSA_OK:
+        return
+    msg = (load().tsa_last_error() or b"").decode(errors="replace")
+    if rc == TSA_ERR_INVALID:
+        raise ValueError(f"{what}: {msg}")
+    if rc == TSA_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg} (status {rc})")
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors must live on one GPU; the kernels have no CPU path."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("tinyserver_amd kernels run on a ROCm GPU; got a CPU tensor")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,306 @@
+// Fused Qwen3 per-head QK RMSNorm + rotate-half RoPE (+ optional paged K/V
+// store).
+//
+// Replaces the eager sequence at server/model/patches/qwen3.py:268-287:
+// q_norm/k_norm (transformers models/qwen3/modeling_qwen3.py:59-64) followed by
+// apply_rotary_pos_emb (modeling_qwen3.py:140-170), about 15 element-wise
+// launches per tensor, with one pass over q and k. The rounding points are
+// HF's, in the model dtype T:
+//   y   = T(x * (1 / sqrt(mean(x^2) + eps)))      statistics in fp32
+//   z   = T(w * y)
+//   out = T( T(z * cos) + T(rotate_half(z) * sin) )
+// where rotate_half(z)_i = -z_{i+D/2} for i < D/2 and z_{i-D/2} otherwise.
+// Products of two 16-bit values are exact in fp32, so every T(.) above is a
+// single rounding exactly as torch does it; fp32 arithmetic uses the _rn
+// intrinsics so no multiply-add is contracted across a rounding point.
+//
+// Layout: one lane owns 8 consecutive elements of a (token, head) row, so a
+// D=128 row is 16 lanes and the RoPE partner elements (i +- D/2) sit in lane
+// c ^ (D/16), one cross-lane exchange away. Rows are ordered token-major
+// (all Hq + Hkv heads of a token are adjacent) so a token's cos/sin and its
+// block-table lookup are shared by neighbouring lanes.
+#include "kv_store.h"
+
+namespace tsa {
+
+template <typename T>
+struct NormRopeArgs {
+  const T* q; const T* k;
+  T* q_out; T* k_out;
+  const T* qw; const T* kw;
+  const T* cos; const T* sin;
+  const T* v;                 // raw V rows, (T, Hkv, D); only when storing
+  int64_t q_st, q_sh, q_sd, k_st, k_sh, k_sd;
+  int64_t qo_st, qo_sh, qo_sd, ko_st, ko_sh, ko_sd;
+  int64_t qw_s, kw_s, cos_st, cos_sd, sin_st, sin_sd;
+  int64_t v_st, v_sh, v_sd;
+  int64_t T_, Hq, Hkv;
+  float eps;
+  // Paged store target (k_cache == nullptr: no store).
+  T* k_cache; T* v_cache;
+  int64_t kc_b, kc_h, kc_s, kc_d, vc_b, vc_h, vc_s, vc_d, NB, BS;
+  PagedAddr addr;
+};
+
+template <typename T, bool VEC>
+__device__ __forceinline__ void load8(const T* p, int64_t stride, float (&out)[8]) {
+  if constexpr (VEC && sizeof(T) == 2) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = lo_f<T>(w[i]);
+      out[2 * i + 1] = hi_f<T>(w[i]);
+    }
+  } else if constexpr (VEC) {
+    const f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
+    const f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { out[i] = a[i]; out[4 + i] = b[i]; }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = to_float(p[i * stride]);
+  }
+}
+
+// Values are already representable in T, so the conversion here is exact.
+template <typename T, bool VEC>
+__device__ __forceinline__ void store8(T* p, int64_t stride, const float (&v)[8]) {
+  if constexpr (VEC && sizeof(T) == 2) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack2<T>(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(p) = w;
+  } else if constexpr (VEC) {
+    f32x4 a, b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { a[i] = v[i]; b[i] = v[4 + i]; }
+    reinterpret_cast<f32x4*>(p)[0] = a;
+    reinterpret_cast<f32x4*>(p)[1] = b;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i * stride] = from_float<T>(v[i]);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float round_t(float x) { return to_float(from_float<T>(x)); }
+
+template <typename T, int D, bool VEC>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs<T> a) {
+  constexpr int LANES = D / 8;  // lanes per (token, head) row
+  constexpr int ROWS = 256 / LANES;
+  const int lane_in_row = threadIdx.x % LANES;
+  const int64_t heads = a.Hq + a.Hkv;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * ROWS + threadIdx.x / LANES;
+  const bool live = row < a.T_ * heads;
+  // Dead lanes still join the cross-lane exchanges below (they read row 0).
+  const int64_t r = live ? row : 0;
+  const int64_t t = r / heads;
+  const int64_t hh = r - t * heads;
+  const bool is_k = hh >= a.Hq;
+  const int64_t h = is_k ? hh - a.Hq : hh;
+  const int d0 = lane_in_row * 8;
+
+  const T* src = is_k ? a.k + t * a.k_st + h * a.k_sh + d0 * a.k_sd : a.q + t * a.q_st + h * a.q_sh + d0 * a.q_sd;
+  const T* w = is_k ? a.kw + d0 * a.kw_s : a.qw + d0 * a.qw_s;
+  float x[8], wf[8], cs[8], sn[8];
+  load8<T, VEC>(src, is_k ? a.k_sd : a.q_sd, x);
+  load8<T, VEC>(w, is_k ? a.kw_s : a.qw_s, wf);
+  load8<T, VEC>(a.cos + t * a.cos_st + d0 * a.cos_sd, a.cos_sd, cs);
+  load8<T, VEC>(a.sin + t * a.sin_st + d0 * a.sin_sd, a.sin_sd, sn);
+
+  // mean(x^2) in fp32, summed in the order of the CPU reduction the model's
+  // RMSNorm runs through (four 8-wide accumulators over 32-element strides,
+  // added in order, then the 8 lanes in order), so the rounded sum -- and the
+  // bf16 results downstream of it -- match it bit for bit. Element 8c + e of
+  // the row lives in lane c: accumulator k = c % 4 collects lanes k, k+4, ...
+  float sq[8], acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = sq[e] = __fmul_rn(x[e], x[e]);
+#pragma unroll
+  for (int step = 4; step < LANES; step += 4)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = __fadd_rn(acc[e], __shfl_down(sq[e], step, LANES));
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float v = acc[e];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) v = __fadd_rn(v, __shfl_down(acc[e], k, LANES));
+    ss = __fadd_rn(ss, v);  // meaningful in lane 0 of the row
+  }
+  ss = __shfl(ss, 0, LANES);
+  const float var = __fdiv_rn(ss, static_cast<float>(D));
+  const float rinv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, a.eps)));
+
+  float z[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = round_t<T>(__fmul_rn(wf[i], round_t<T>(__fmul_rn(x[i], rinv))));
+
+  // Partner half: lane c holds dims 8c..8c+7, dims +- D/2 are in lane c ^ (LANES/2).
+  float zp[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) zp[i] = __shfl_xor(z[i], LANES / 2, 64);
+  const bool first_half = lane_in_row < LANES / 2;
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float rot = first_half ? -zp[i] : zp[i];
+    o[i] = round_t<T>(__fadd_rn(round_t<T>(__fmul_rn(z[i], cs[i])), round_t<T>(__fmul_rn(rot, sn[i]))));
+  }
+  if (!live) return;
+
+  if (!is_k) {
+    store8<T, VEC>(a.q_out + t * a.qo_st + h * a.qo_sh + d0 * a.qo_sd, a.qo_sd, o);
+    return;
+  }
+  if (a.k_out) store8<T, VEC>(a.k_out + t * a.ko_st + h * a.ko_sh + d0 * a.ko_sd, a.ko_sd, o);
+  if (a.k_cache) {
+    int64_t blk, slot;
+    if (!a.addr.locate(t, a.BS, a.NB, blk, slot)) return;
+    store8<T, VEC>(a.k_cache + blk * a.kc_b + h * a.kc_h + slot * a.kc_s + d0 * a.kc_d, a.kc_d, o);
+    float vv[8];
+    load8<T, VEC>(a.v + t * a.v_st + h * a.v_sh + d0 * a.v_sd, a.v_sd, vv);
+    store8<T, VEC>(a.v_cache + blk * a.vc_b + h * a.vc_h + slot * a.vc_s + d0 * a.vc_d, a.vc_d, vv);
+  }
+}
+
+static bool vec_ok(const tsa_view* v) { return v == nullptr || v->data == nullptr || rows_vec16(v); }
+
+template <typename T, int D>
+static int launch_norm_rope(const NormRopeArgs<T>& a, bool vec, hipStream_t stream) {
+  constexpr int ROWS = 256 / (D / 8);
+  const int64_t rows = a.T_ * (a.Hq + a.Hkv);
+  if (rows == 0) return TSA_OK;
+  const dim3 grid((rows + ROWS - 1) / ROWS);
+  if (vec) qk_norm_rope_kernel<T, D, true><<<grid, dim3(256), 0, stream>>>(a);
+  else qk_norm_rope_kernel<T, D, false><<<grid, dim3(256), 0, stream>>>(a);
+  return check_launch("tsa_qk_norm_rope");
+}
+
+template <typename T>
+static int run_norm_rope(NormRopeArgs<T>& a, int64_t D, bool vec, hipStream_t stream) {
+  switch (D) {
+    case 64: return launch_norm_rope<T, 64>(a, vec, stream);
+    case 128: return launch_norm_rope<T, 128>(a, vec, stream);
+    case 256: return launch_norm_rope<T, 256>(a, vec, stream);
+  }
+  set_error("tsa_qk_norm_rope: head_dim %lld is not implemented (64, 128, 256)", (long long)D);
+  return TSA_ERR_UNSUPPORTED;
+}
+
+template <typename T>
+static int norm_rope_entry(const tsa_view* q, const tsa_view* k, const tsa_view* v, const tsa_view* q_out,
+                           const tsa_view* k_out, const tsa_view* qw, const tsa_view* kw, const tsa_view* cos,
+                           const tsa_view* sin, double eps, const tsa_view* k_cache, const tsa_view* v_cache,
+                           const PagedAddr* addr, hipStream_t stream) {
+  NormRopeArgs<T> a{};
+  a.q = static_cast<const T*>(q->data);
+  a.k = static_cast<const T*>(k->data);
+  a.q_out = static_cast<T*>(q_out->data);
+  a.k_out = k_out ? static_cast<T*>(k_out->data) : nullptr;
+  a.qw = static_cast<const T*>(qw->data);
+  a.kw = static_cast<const T*>(kw->data);
+  a.cos = static_cast<const T*>(cos->data);
+  a.sin = static_cast<const T*>(sin->data);
+  a.q_st = q->stride[0]; a.q_sh = q->stride[1]; a.q_sd = q->stride[2];
+  a.k_st = k->stride[0]; a.k_sh = k->stride[1]; a.k_sd = k->stride[2];
+  a.qo_st = q_out->stride[0]; a.qo_sh = q_out->stride[1]; a.qo_sd = q_out->stride[2];
+  if (a.k_out) { a.ko_st = k_out->stride[0]; a.ko_sh = k_out->stride[1]; a.ko_sd = k_out->stride[2]; }
+  a.qw_s = qw->stride[0]; a.kw_s = kw->stride[0];
+  a.cos_st = cos->stride[0]; a.cos_sd = cos->stride[1];
+  a.sin_st = sin->stride[0]; a.sin_sd = sin->stride[1];
+  a.T_ = q->size[0]; a.Hq = q->size[1]; a.Hkv = k->size[1];
+  a.eps = static_cast<float>(eps);
+  bool vec = vec_ok(q) && vec_ok(k) && vec_ok(q_out) && vec_ok(k_out) && vec_ok(cos) && vec_ok(sin) &&
+             (qw->stride[0] == 1 && reinterpret_cast<uintptr_t>(qw->data) % 16 == 0) &&
+             (kw->stride[0] == 1 && reinterpret_cast<uintptr_t>(kw->data) % 16 == 0);
+  if (k_cache) {
+    a.v = static_cast<const T*>(v->data);
+    a.v_st = v->stride[0]; a.v_sh = v->stride[1]; a.v_sd = v->stride[2];
+    a.k_cache = static_cast<T*>(k_cache->data);
+    a.v_cache = static_cast<T*>(v_cache->data);
+    a.kc_b = k_cache->stride[0]; a.kc_h = k_cache->stride[1]; a.kc_s = k_cache->stride[2]; a.kc_d = k_cache->stride[3];
+    a.vc_b = v_cache->stride[0]; a.vc_h = v_cache->stride[1]; a.vc_s = v_cache->stride[2]; a.vc_d = v_cache->stride[3];
+    a.NB = k_cache->size[0];
+    a.BS = k_cache->size[2];
+    a.addr = *addr;
+    vec = vec && vec_ok(v) && vec_ok(k_cache) && vec_ok(v_cache);
+  }
+  return run_norm_rope<T>(a, q->size[2], vec, stream);
+}
+
+static int check_norm_rope(const tsa_view* q, const tsa_view* k, const tsa_view* q_out, const tsa_view* k_out,
+                           const tsa_view* qw, const tsa_view* kw, const tsa_view* cos, const tsa_view* sin) {
+  TSA_REQUIRE(view_ok(q, 3) && view_ok(k, 3), "q and k must be 3D tensors (num_tokens, num_heads, head_dim)");
+  TSA_REQUIRE(view_ok(q_out, 3), "q_out must be a 3D tensor shaped like q");
+  TSA_REQUIRE(view_ok(qw, 1) && view_ok(kw, 1), "q_weight and k_weight must be 1D tensors (head_dim)");
+  TSA_REQUIRE(view_ok(cos, 2) && view_ok(sin, 2), "cos and sin must be 2D tensors (num_tokens, head_dim)");
+  const int dt = q->dtype;
+  TSA_REQUIRE(is_float_dtype(dt), "q must be bf16, f16 or f32 (got %s)", dtype_name(dt));
+  TSA_REQUIRE(k->dtype == dt && q_out->dtype == dt && qw->dtype == dt && kw->dtype == dt && cos->dtype == dt &&
+                  sin->dtype == dt,
+              "q, k, outputs, norm weights and cos/sin must share the model dtype %s", dtype_name(dt));
+  const int64_t T = q->size[0], D = q->size[2];
+  TSA_REQUIRE(k->size[0] == T && k->size[2] == D, "k must be (num_tokens=%lld, Hkv, head_dim=%lld)", (long long)T,
+              (long long)D);
+  for (int d = 0; d < 3; ++d) TSA_REQUIRE(q_out->size[d] == q->size[d], "q_out must have q's shape");
+  if (k_out && k_out->data) {
+    TSA_REQUIRE(view_ok(k_out, 3) && k_out->dtype == dt, "k_out must be a 3D tensor shaped like k");
+    for (int d = 0; d < 3; ++d) TSA_REQUIRE(k_out->size[d] == k->size[d], "k_out must have k's shape");
+  }
+  TSA_REQUIRE(qw->size[0] == D && kw->size[0] == D, "norm weights must have head_dim (%lld) entries", (long long)D);
+  TSA_REQUIRE(cos->size[0] == T && cos->size[1] == D && sin->size[0] == T && sin->size[1] == D,
+              "cos and sin must be (num_tokens=%lld, head_dim=%lld)", (long long)T, (long long)D);
+  TSA_REQUIRE(D % 16 == 0, "head_dim must be a multiple of 16 (got %lld)", (long long)D);
+  return TSA_OK;
+}
+
+}  // namespace tsa
+
+using namespace tsa;
+
+template <typename... Args>
+static int dispatch_dtype(int dt, Args&&... args) {
+  switch (dt) {
+    case TSA_BF16: return norm_rope_entry<bf16_t>(args...);
+    case TSA_F16: return norm_rope_entry<f16_t>(args...);
+    case TSA_F32: return norm_rope_entry<float>(args...);
+  }
+  set_error("unsupported dtype %d", dt);
+  return TSA_ERR_UNSUPPORTED;
+}
+
+extern "C" int tsa_qk_norm_rope(const tsa_view* q, const tsa_view* k, const tsa_view* q_out, const tsa_view* k_out,
+                                const tsa_view* q_weight, const tsa_view* k_weight, const tsa_view* cos,
+                                const tsa_view* sin, double eps, void* stream) {
+  if (int rc = check_norm_rope(q, k, q_out, k_out, q_weight, k_weight, cos, sin)) return rc;
+  TSA_REQUIRE(k_out && k_out->data, "k_out is required when K is not stored into a cache");
+  return dispatch_dtype(q->dtype, q, k, nullptr, q_out, k_out, q_weight, k_weight, cos, sin, eps, nullptr, nullptr,
+                        nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tsa_qk_norm_rope_store(const tsa_view* q, const tsa_view* k, const tsa_view* v,
+                                      const tsa_view* q_out, const tsa_view* k_out, const tsa_view* q_weight,
+                                      const tsa_view* k_weight, const tsa_view* cos, const tsa_view* sin, double eps,
+                                      const tsa_view* k_cache, const tsa_view* v_cache,
+                                      const tsa_view* block_tables, const tsa_view* cu_seqlens,
+                                      const tsa_view* positions, void* stream) {
+  if (int rc = check_norm_rope(q, k, q_out, k_out, q_weight, k_weight, cos, sin)) return rc;
+  TSA_REQUIRE(view_ok(v, 3), "v must be a 3D tensor (num_tokens, Hkv, head_dim)");
+  for (int d = 0; d < 3; ++d) TSA_REQUIRE(v->size[d] == k->size[d], "v must have k's shape");
+  TSA_REQUIRE(view_ok(k_cache, 4) && view_ok(v_cache, 4),
+              "k_cache and v_cache must be 4D tensors (num_blocks, num_kv_heads, block_size, head_dim)");
+  for (int d = 0; d < 4; ++d) TSA_REQUIRE(k_cache->size[d] == v_cache->size[d], "k_cache and v_cache must match");
+  TSA_REQUIRE(v->dtype == q->dtype && k_cache->dtype == q->dtype && v_cache->dtype == q->dtype,
+              "v and the caches must share the model dtype %s", dtype_name(q->dtype));
+  TSA_REQUIRE(k_cache->size[1] == k->size[1] && k_cache->size[3] == k->size[2],
+              "cache (NB, %lld, BS, %lld) does not match k (T, %lld, %lld)", (long long)k_cache->size[1],
+              (long long)k_cache->size[3], (long long)k->size[1], (long long)k->size[2]);
+  TSA_REQUIRE(k_cache->size[2] > 0, "block_size must be positive");
+  PagedAddr addr;
+  if (int rc = make_paged_addr(block_tables, cu_seqlens, positions, k->size[0], addr)) return rc;
+  const tsa_view* ko = (k_out && k_out->data) ? k_out : nullptr;
+  return dispatch_dtype(q->dtype, q, k, v, q_out, ko, q_weight, k_weight, cos, sin, eps, k_cache, v_cache, &addr,
+                        static_cast<hipStream_t>(stream));
+}

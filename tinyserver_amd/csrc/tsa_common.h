@@ -1,0 +1,166 @@
+// Shared device/host helpers for the gfx950 attention-path kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "tsa_api.h"
+
+namespace tsa {
+
+// ---------------------------------------------------------------- errors --
+// Per-thread last-error message (the library keeps no other host state).
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+const char* last_error();
+
+#define TSA_REQUIRE(cond, ...)        \
+  do {                                \
+    if (!(cond)) {                    \
+      ::tsa::set_error(__VA_ARGS__);  \
+      return TSA_ERR_INVALID;         \
+    }                                 \
+  } while (0)
+
+#define TSA_UNSUPPORTED(cond, ...)    \
+  do {                                \
+    if (!(cond)) {                    \
+      ::tsa::set_error(__VA_ARGS__);  \
+      return TSA_ERR_UNSUPPORTED;     \
+    }                                 \
+  } while (0)
+
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return TSA_ERR_LAUNCH;
+  }
+  return TSA_OK;
+}
+
+// ----------------------------------------------------------------- views --
+inline bool is_float_dtype(int dt) { return dt == TSA_BF16 || dt == TSA_F16 || dt == TSA_F32; }
+inline bool is_index_dtype(int dt) { return dt == TSA_I32 || dt == TSA_I64; }
+inline int dtype_bytes(int dt) { return dt == TSA_F32 || dt == TSA_I32 ? 4 : dt == TSA_I64 ? 8 : 2; }
+inline const char* dtype_name(int dt) {
+  switch (dt) {
+    case TSA_BF16: return "bf16";
+    case TSA_F16: return "f16";
+    case TSA_F32: return "f32";
+    case TSA_I32: return "i32";
+    case TSA_I64: return "i64";
+  }
+  return "?";
+}
+
+// A view is usable when it is non-NULL, has the expected rank, a sane dtype
+// and non-negative sizes. Data may be NULL only for an empty view.
+inline bool view_ok(const tsa_view* v, int ndim) {
+  if (!v || v->ndim != ndim) return false;
+  if (v->dtype < TSA_BF16 || v->dtype > TSA_I64) return false;
+  int64_t n = 1;
+  for (int d = 0; d < ndim; ++d) {
+    if (v->size[d] < 0) return false;
+    n *= v->size[d];
+  }
+  return n == 0 || v->data != nullptr;
+}
+inline int64_t numel(const tsa_view* v) {
+  int64_t n = 1;
+  for (int d = 0; d < v->ndim; ++d) n *= v->size[d];
+  return n;
+}
+// Innermost dimension is unit-stride and every row starts 16-byte aligned, so
+// rows can be moved with 128-bit accesses.
+inline bool rows_vec16(const tsa_view* v) {
+  const int eb = dtype_bytes(v->dtype);
+  const int nd = v->ndim;
+  if (v->stride[nd - 1] != 1 && v->size[nd - 1] > 1) return false;
+  if ((v->size[nd - 1] * eb) % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(v->data) % 16 != 0) return false;
+  for (int d = 0; d < nd - 1; ++d)
+    if (v->size[d] > 1 && (v->stride[d] * eb) % 16 != 0) return false;
+  return true;
+}
+
+// ------------------------------------------------------- element helpers --
+struct bf16_t { uint16_t x; };
+struct f16_t { uint16_t x; };
+
+__device__ __forceinline__ float to_float(bf16_t v) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(v.x) << 16);
+}
+__device__ __forceinline__ float to_float(f16_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, v.x));
+}
+__device__ __forceinline__ float to_float(float v) { return v; }
+
+// Round-to-nearest-even conversions (gfx950 has a hardware bf16 convert).
+template <typename T> __device__ __forceinline__ T from_float(float f);
+template <> __device__ __forceinline__ bf16_t from_float<bf16_t>(float f) {
+  return bf16_t{__builtin_bit_cast(uint16_t, static_cast<__bf16>(f))};
+}
+template <> __device__ __forceinline__ f16_t from_float<f16_t>(float f) {
+  return f16_t{__builtin_bit_cast(uint16_t, static_cast<_Float16>(f))};
+}
+template <> __device__ __forceinline__ float from_float<float>(float f) { return f; }
+
+// Low/high 16-bit element of a packed dword, as float.
+template <typename T> __device__ __forceinline__ float lo_f(uint32_t w);
+template <typename T> __device__ __forceinline__ float hi_f(uint32_t w);
+template <> __device__ __forceinline__ float lo_f<bf16_t>(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+template <> __device__ __forceinline__ float hi_f<bf16_t>(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+template <> __device__ __forceinline__ float lo_f<f16_t>(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w)));
+}
+template <> __device__ __forceinline__ float hi_f<f16_t>(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return static_cast<uint32_t>(from_float<T>(a).x) | (static_cast<uint32_t>(from_float<T>(b).x) << 16);
+}
+
+// ------------------------------------------------------------ MFMA types --
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// D(16x16 f32) += A(16x32) * B(32x16). Lane i supplies A[i%16][8(i/16)..+8]
+// and B[8(i/16)..+8][i%16] as 8 packed 16-bit values; lane i receives
+// D[4(i/16)+r][i%16] in element r.
+template <typename T> __device__ __forceinline__ f32x4 mfma_k32(u32x4 a, u32x4 b, f32x4 c);
+template <> __device__ __forceinline__ f32x4 mfma_k32<bf16_t>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mfma_k32<f16_t>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+// D(16x16 f32) += A(16x16) * B(16x16). Lane i supplies A[i%16][4(i/16)..+4]
+// and B[4(i/16)..+4][i%16]; lane i receives D[4(i/16)+r][i%16].
+template <typename T> __device__ __forceinline__ f32x4 mfma_k16(u32x2 a, u32x2 b, f32x4 c);
+template <> __device__ __forceinline__ f32x4 mfma_k16<bf16_t>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mfma_k16<f16_t>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+}
+
+// Select 16-bit halves: result = (lo16 of a | lo16 of b << 16) or the high
+// halves, via v_perm_b32.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace tsa

@@ -1,0 +1,93 @@
+"""Paged decode attention -- drop-in for server/model/kernels/paged_attention.py.
+
+``paged_attention_forward`` keeps the reference signature and its "3D"
+ValueError (paged_attention.py:124-192). The output is allocated with
+``torch.empty_like(query)`` as the reference does. The split-K partial-result
+workspace is cached per (device, stream) and grown on demand.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _key(device: torch.device, stream: int) -> tuple[int, int]:
+    return (device.index if device.index is not None else torch.cuda.current_device(), stream)
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    ws = _workspaces.get(_key(device, stream))
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[_key(device, stream)] = ws
+    return ws
+
+
+def decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks, block_size, tiles_per_split=0):
+    lib = _lib.load()
+    return int(lib.tsa_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks,
+                                                    block_size, tiles_per_split))
+
+
+def paged_attention_forward(
+    query: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    block_size: int,
+    seq_lens: torch.Tensor,
+    *,
+    tiles_per_split: int = 0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Decode-phase paged attention, one new token per sequence.
+
+    ``out[s, h] = softmax(query[s, h] . K_s^T / sqrt(D)) V_s`` over the first
+    ``seq_lens[s]`` tokens gathered through ``block_tables[s]``; q-head h reads
+    kv head ``h // (Hq / Hkv)``. query: (B, Hq, D); caches (NB, Hkv, BS, D);
+    block_tables (B, max_blocks) int32; seq_lens (B,) int32.
+    ``tiles_per_split`` (16-token tiles per workgroup, 0 = automatic) and
+    ``out`` are extensions; the defaults reproduce the reference call.
+    """
+    if query.dim() != 3:
+        raise ValueError(f"query must be a 3D tensor, but got shape {query.shape}")
+    if k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise ValueError("k_cache and v_cache must be 4D tensors (num_blocks, num_kv_heads, block_size, head_dim)")
+    if block_tables.dim() != 2:
+        raise ValueError(f"block_tables must be a 2D tensor, but got shape {block_tables.shape}")
+    if int(block_size) != k_cache.shape[2]:
+        raise ValueError(f"block_size {block_size} does not match the cache's {k_cache.shape[2]}")
+    dev = _lib.require_device(query, k_cache, v_cache, block_tables, seq_lens)
+    if block_tables.dtype != torch.int32:
+        block_tables = block_tables.to(torch.int32)
+    if seq_lens.dtype != torch.int32:
+        seq_lens = seq_lens.to(torch.int32)
+    num_seqs, num_heads, head_dim = query.shape
+    num_kv_heads = k_cache.shape[1]
+    if out is None:
+        out = torch.empty_like(query)
+    softmax_scale = 1.0 / math.sqrt(head_dim)
+    lib = _lib.load()
+    stream = _lib.stream_of(dev)
+    nbytes = int(lib.tsa_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim,
+                                                      block_tables.shape[1], k_cache.shape[2], tiles_per_split))
+    ws = _workspace(dev, stream, nbytes)
+    views = [_lib.view(t) for t in (out, query, k_cache, v_cache, block_tables, seq_lens)]
+    rc = lib.tsa_paged_decode(
+        *map(_lib.ref, views),
+        softmax_scale,
+        ws.data_ptr() if ws is not None else None,
+        ws.numel() if ws is not None else 0,
+        int(tiles_per_split),
+        stream,
+    )
+    _lib.check(rc, "paged_attention_forward")
+    return out
