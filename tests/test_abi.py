@@ -1,0 +1,129 @@
+"""The C ABI of libtsa.so, checked without a GPU (no compute calls).
+
+* every entry point declared in include/tsa_api.h is exported by the library
+  and bound by the Python shim;
+* the ABI version matches;
+* malformed arguments are rejected before anything touches a device, with
+  TSA_ERR_INVALID and a message (NULL views, wrong ranks, dtype mismatches,
+  GQA divisibility, mapping lengths), and unimplemented shapes with
+  TSA_ERR_UNSUPPORTED;
+* the decode workspace size follows the split plan.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from tinyserver_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tsa_api.h"
+
+
+def declared_symbols():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(tsa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_are_exported_and_bound():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), f"{name} missing from libtsa.so"
+        assert name in _lib.SIGNATURES, f"{name} not bound in tinyserver_amd._lib"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_abi_version():
+    assert _lib.load().tsa_abi_version() == _lib.ABI_VERSION
+
+
+def _v(shape, dtype=torch.bfloat16, data=0x10000):
+    """A view of a fake device address (never dereferenced: validation fails first)."""
+    v = _lib.TsaView()
+    v.data = data
+    st = 1
+    strides = []
+    for n in reversed(shape):
+        strides.append(st)
+        st *= n
+    for i, (n, s) in enumerate(zip(shape, reversed(strides))):
+        v.size[i] = n
+        v.stride[i] = s
+    v.ndim = len(shape)
+    v.dtype = _lib._DTYPES[dtype]
+    return v
+
+
+def _call(name, *args):
+    lib = _lib.load()
+    return getattr(lib, name)(*args), lib.tsa_last_error().decode()
+
+
+R = ctypes.byref
+
+
+def test_store_validation():
+    rc, msg = _call("tsa_store_kv_mapped", None, None, None, None, None, None, None)
+    assert rc == _lib.TSA_ERR_INVALID and "3D" in msg
+    k2d = _v((2, 8))
+    rc, msg = _call("tsa_store_kv_mapped", R(k2d), R(_v((2, 1, 8))), R(_v((1, 2, 4, 8))), R(_v((1, 2, 4, 8))),
+                    R(_v((1,), torch.int32)), R(_v((1,), torch.int32)), None)
+    assert rc == _lib.TSA_ERR_INVALID and "3D" in msg
+    rc, msg = _call("tsa_store_kv_mapped", R(_v((2, 4, 8))), R(_v((2, 4, 8))), R(_v((2, 2, 4, 8))),
+                    R(_v((2, 2, 4, 8))), R(_v((3,), torch.int32)), R(_v((4,), torch.int32)), None)
+    assert rc == _lib.TSA_ERR_INVALID and "num_tokens" in msg
+    rc, msg = _call("tsa_store_kv_mapped", R(_v((2, 4, 8))), R(_v((2, 4, 8), torch.float16)), R(_v((2, 2, 4, 8))),
+                    R(_v((2, 2, 4, 8))), R(_v((4,), torch.int32)), R(_v((4,), torch.int32)), None)
+    assert rc == _lib.TSA_ERR_INVALID and "dtype" in msg
+    rc, msg = _call("tsa_store_kv_paged", R(_v((2, 4, 8))), R(_v((2, 4, 8))), R(_v((2, 2, 4, 8))),
+                    R(_v((2, 2, 4, 8))), R(_v((2, 3), torch.int32)), R(_v((2,), torch.int32)), None, None)
+    assert rc == _lib.TSA_ERR_INVALID and "cu_seqlens" in msg
+
+
+def test_decode_validation():
+    q = _v((4, 8, 128))
+    kc = _v((10, 3, 16, 128))
+    bt = _v((4, 2), torch.int32)
+    sl = _v((4,), torch.int32)
+    rc, msg = _call("tsa_paged_decode", R(q), R(q), R(kc), R(kc), R(bt), R(sl), 0.1, None, 0, 0, None)
+    assert rc == _lib.TSA_ERR_INVALID and "multiple" in msg
+    rc, msg = _call("tsa_paged_decode", R(_v((4, 128))), R(_v((4, 128))), R(kc), R(kc), R(bt), R(sl), 0.1, None, 0, 0,
+                    None)
+    assert rc == _lib.TSA_ERR_INVALID and "3D" in msg
+    big = _v((4, 8, 1024))
+    kcb = _v((10, 2, 16, 1024))
+    rc, msg = _call("tsa_paged_decode", R(big), R(big), R(kcb), R(kcb), R(bt), R(sl), 0.1, None, 0, 0, None)
+    assert rc == _lib.TSA_ERR_UNSUPPORTED
+
+
+def test_prefill_validation():
+    q, k = _v((10, 6, 64)), _v((10, 4, 64))
+    cu = _v((3,), torch.int32)
+    rc, msg = _call("tsa_varlen_prefill", R(q), R(q), R(k), R(k), R(cu), R(cu), 5, 5, 1, 0.1, None)
+    assert rc == _lib.TSA_ERR_INVALID and "divisible" in msg
+
+
+def test_norm_rope_validation():
+    q, k = _v((5, 4, 128)), _v((5, 2, 128))
+    w, cs = _v((128,)), _v((5, 128))
+    bad_w = _v((64,))
+    rc, msg = _call("tsa_qk_norm_rope", R(q), R(k), R(q), R(k), R(bad_w), R(w), R(cs), R(cs), 1e-6, None)
+    assert rc == _lib.TSA_ERR_INVALID and "head_dim" in msg
+    rc, msg = _call("tsa_qk_norm_rope", R(q), R(k), R(q), R(k), R(w), R(w), R(_v((5, 128), torch.float32)), R(cs),
+                    1e-6, None)
+    assert rc == _lib.TSA_ERR_INVALID and "dtype" in msg
+
+
+def test_workspace_plan():
+    lib = _lib.load()
+    # Everything fits one split -> no workspace.
+    assert lib.tsa_paged_decode_workspace_bytes(4, 16, 8, 128, 2, 16, 0) == 0
+    # Forced 4-tile splits over 64 tiles: 16 splits of partial (acc, m, l) per (seq, q-head).
+    n = lib.tsa_paged_decode_workspace_bytes(2, 8, 2, 128, 64, 16, 4)
+    assert n >= 2 * 8 * 16 * (128 + 2) * 4
+    assert lib.tsa_paged_decode_workspace_bytes(0, 8, 2, 128, 64, 16, 4) == 0
