@@ -57,7 +57,7 @@ def _events_time(fn, steps, warmup):
     return wall, [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
-def bench_decode(name, steps, warmup, tiles_per_split=0, copies=3, with_block=False):
+def bench_decode(name, steps, warmup, num_workgroups=0, copies=3, with_block=False):
     from tinyserver_amd import workloads as W
     from tinyserver_amd.kernels import paged_attention_forward, qk_norm_rope_store
 
@@ -73,7 +73,7 @@ def bench_decode(name, steps, warmup, tiles_per_split=0, copies=3, with_block=Fa
 
     def attn(i):
         kc, vc = pools[i % copies]
-        paged_attention_forward(q_rot, kc, vc, w.block_tables, W.PAGE, seq_lens, tiles_per_split=tiles_per_split,
+        paged_attention_forward(q_rot, kc, vc, w.block_tables, W.PAGE, seq_lens, num_workgroups=num_workgroups,
                                 out=out)
 
     wall, ev = _events_time(attn, steps, warmup)
@@ -101,7 +101,7 @@ def bench_decode(name, steps, warmup, tiles_per_split=0, copies=3, with_block=Fa
             kc, vc = pools[i % copies]
             qr, _ = qk_norm_rope_store(w.q, w.k, w.v, qw, kw, cos, sin, w.eps, kc, vc, w.block_tables, cu, pos,
                                        return_k=False)
-            paged_attention_forward(qr, kc, vc, w.block_tables, W.PAGE, seq_lens, tiles_per_split=tiles_per_split,
+            paged_attention_forward(qr, kc, vc, w.block_tables, W.PAGE, seq_lens, num_workgroups=num_workgroups,
                                     out=out)
 
         _, evb = _events_time(block, steps, warmup)
@@ -186,7 +186,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--tiles-per-split", type=int, default=0)
+    ap.add_argument("--num-workgroups", type=int, default=0)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -201,7 +201,7 @@ def main():
     from tinyserver_amd import _lib
 
     _lib.load()
-    head, w = bench_decode("qwen3-8b-decode-bs64", args.steps, args.warmup, args.tiles_per_split, with_block=True)
+    head, w = bench_decode("qwen3-8b-decode-bs64", args.steps, args.warmup, args.num_workgroups, with_block=True)
     line = {
         "metric": METRIC,
         "value": round(head["achieved_gbs"] / 1000.0, 4),
@@ -224,7 +224,7 @@ def main():
             "page": 16,
             "ctx": "U[512,4096], seed 2",
             "sum_ctx": head["sum_ctx"],
-            "tiles_per_split": args.tiles_per_split,
+            "num_workgroups": args.num_workgroups,
         },
         "us_per_layer": round(head["kernel_us_mean"], 2),
         "us_per_layer_median": round(head["kernel_us_median"], 2),

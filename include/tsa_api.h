@@ -121,25 +121,25 @@ int tsa_qk_norm_rope_store(const tsa_view* q, const tsa_view* k, const tsa_view*
                            const tsa_view* block_tables, const tsa_view* cu_seqlens,
                            const tsa_view* positions, void* stream);
 
-/* Bytes of partial-result workspace tsa_paged_decode needs for this shape and
- * split size (tiles_per_split 0 = the library's choice; a tile is 16 tokens).
- * 0 when every sequence fits one split. */
+/* Bytes of workspace tsa_paged_decode needs: two partial-result slots per
+ * workgroup (num_workgroups 0 = the library's choice, two per CU). */
 size_t tsa_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads,
                                         int64_t head_dim, int64_t max_blocks_per_seq,
-                                        int64_t block_size, int32_t tiles_per_split);
+                                        int64_t block_size, int32_t num_workgroups);
 
 /* paged_attention_forward (paged_attention.py:124-192):
  * out[s, h] = softmax(query[s, h] . K_s^T * softmax_scale) V_s over the first
  * seq_lens[s] tokens gathered through block_tables[s], kv head h / (Hq/Hkv).
  * query/out: (B, Hq, D); caches (NB, Hkv, BS, D); block_tables (B, max_blocks)
- * int32; seq_lens (B,) int32. workspace holds split-K partial results (no
- * initialisation needed; calls that share one must be ordered on one stream).
- * Two launches when a sequence spans several splits: the split kernel and a
- * merge kernel. */
+ * int32; seq_lens (B,) int32. The 16-token tiles of all sequences are split
+ * evenly over num_workgroups workgroups (0 = two per CU); a second launch
+ * merges the sequences cut between workgroups. workspace holds their partial
+ * results (no initialisation needed; calls that share one must be ordered on
+ * one stream). */
 int tsa_paged_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache,
                      const tsa_view* v_cache, const tsa_view* block_tables,
                      const tsa_view* seq_lens, double softmax_scale, void* workspace,
-                     size_t workspace_bytes, int32_t tiles_per_split, void* stream);
+                     size_t workspace_bytes, int32_t num_workgroups, void* stream);
 
 /* flash_attn_varlen_func (varlen_attention.py:145-218): per sequence b and
  * q-head h, softmax(q k^T * softmax_scale) v over keys cu_seqlens_k[b] ..

@@ -121,9 +121,7 @@ def test_norm_rope_validation():
 
 def test_workspace_plan():
     lib = _lib.load()
-    # Everything fits one split -> no workspace.
-    assert lib.tsa_paged_decode_workspace_bytes(4, 16, 8, 128, 2, 16, 0) == 0
-    # Forced 4-tile splits over 64 tiles: 16 splits of partial (acc, m, l) per (seq, q-head).
-    n = lib.tsa_paged_decode_workspace_bytes(2, 8, 2, 128, 64, 16, 4)
-    assert n >= 2 * 8 * 16 * (128 + 2) * 4
-    assert lib.tsa_paged_decode_workspace_bytes(0, 8, 2, 128, 64, 16, 4) == 0
+    # Two partial slots of (acc[G][D], m[G], l[G]) per workgroup.
+    n = lib.tsa_paged_decode_workspace_bytes(2, 8, 2, 128, 64, 16, 10)
+    assert n >= 10 * 2 * 4 * (128 + 2) * 4
+    assert lib.tsa_paged_decode_workspace_bytes(0, 8, 2, 128, 64, 16, 10) == 0

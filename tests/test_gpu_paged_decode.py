@@ -124,14 +124,18 @@ def test_page_sizes(block_size):
     assert_close(out, ref, what=f"BS={block_size}")
 
 
-@pytest.mark.parametrize("tiles_per_split", [4, 8, 16])
-def test_split_k_merge(tiles_per_split):
-    """Many splits per sequence; the second call checks the counters reset."""
-    q, kc, vc, bt, sl = _random_paged_inputs([2000, 1, 777, 4096, 64], 32, 8, 128, 16, torch.bfloat16, seed=9)
+@pytest.mark.parametrize("num_workgroups", [1, 3, 7, 64, 333, 4096])
+def test_stream_partition(num_workgroups):
+    """Sequences cut between workgroups at every kind of boundary (one workgroup,
+    a few, more workgroups than tiles); a second call reuses the workspace."""
+    q, kc, vc, bt, sl = _random_paged_inputs([2000, 1, 777, 4096, 64, 0, 16], 32, 8, 128, 16, torch.bfloat16,
+                                             seed=9)
     ref = op.paged_attention_forward(q, kc, vc, bt, 16, sl)
     for call in range(2):
-        out = _run(q, kc, vc, bt, 16, sl, tiles_per_split=tiles_per_split)
-        assert_close(out, ref, what=f"tps={tiles_per_split} call {call}")
+        out = _run(q, kc, vc, bt, 16, sl, num_workgroups=num_workgroups).cpu()
+        assert torch.isnan(out[5]).all(), "empty sequence must give NaN (0/0) like the reference"
+        keep = [0, 1, 2, 3, 4, 6]
+        assert_close(out[keep], ref[keep], what=f"W={num_workgroups} call {call}")
 
 
 def test_seq_len_one_returns_v_row():
@@ -164,11 +168,11 @@ def test_decode_step_qwen3_0p6b():
     assert_close(out, ref, what="decode step")
 
 
-def _sampled_check(w, seqs, tiles_per_split=0):
+def _sampled_check(w, seqs, num_workgroups=0):
     """w lives on the GPU; each sampled sequence is checked against the oracle on
     a compact CPU copy of just its pages."""
     out = paged_attention_forward(w.q, w.k_cache, w.v_cache, w.block_tables, 16, w.ctx_lens.to(torch.int32).to(DEV),
-                                  tiles_per_split=tiles_per_split)
+                                  num_workgroups=num_workgroups)
     torch.cuda.synchronize()
     for s in seqs:
         pages = torch.tensor(w.block_lists[s], device=DEV)

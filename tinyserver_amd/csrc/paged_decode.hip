@@ -5,10 +5,16 @@
 // each K/V page is re-read Hq/Hkv times and a 32k-token context is one long
 // serial program. Here:
 //
-// * One workgroup (4 waves) per (sequence, kv head, context split). Every
-//   K/V byte is read once and shared by the G = Hq/Hkv query heads of the
-//   group. A split is `tiles_per_split` 16-token tiles; the waves of a
-//   workgroup take its tiles round-robin.
+// * Work is the list of 16-token tiles of every (sequence, kv head) "unit",
+//   unit-major. A fixed grid of workgroups (by default two per CU, all
+//   resident at once) splits that list into equal contiguous shares, so every
+//   workgroup streams the same number of K/V bytes whatever the mix of
+//   context lengths, and the whole call is a single wave of workgroups.
+//   Every K/V byte is read once and shared by the G = Hq/Hkv query heads of
+//   its kv head. Each workgroup derives the tile prefix over seq_lens itself
+//   (a block scan in LDS), so nothing is precomputed on the host.
+// * Within a unit's segment the 4 waves of a workgroup take its tiles
+//   round-robin.
 // * Scores on the matrix cores: S^T(16 tok x 16 head) = K(16 tok x D) Q^T with
 //   v_mfma_f32_16x16x32_{bf16,f16}. The K operand wants token = lane%16 and 8
 //   consecutive dims per lane, which is a plain 128-bit global load (lane
@@ -26,24 +32,25 @@
 //   cross-lane exchanges; the accumulator is rescaled only when a head's max
 //   grows, which a wave-uniform branch detects. P is rounded to the cache
 //   dtype to feed the MFMA (the reference's P.V is fp32); l sums the fp32 p.
-// * Each wave keeps two tiles in registers (ping-pong): the loads of tile
-//   i+1 are in flight while tile i is on the matrix cores. Loads are issued
-//   unconditionally (the tile index is clamped to the wave's last tile, whose
-//   repeat hits the cache) so the compiler can wait for exactly one tile.
-// * Split-K: each workgroup merges its waves in LDS; a sequence that fits one
-//   split writes its output directly, otherwise each split writes (m, l, acc)
-//   to the workspace and a small second kernel merges the splits with a
-//   log-sum-exp reduce. The kernel boundary orders the two, so no cache
-//   flushes or atomics are needed; no host sync, no memset.
+// * Each wave keeps a ring of RING tiles in registers: the loads of the next
+//   RING-1 tiles are in flight while one is on the matrix cores. Loads are
+//   unconditional (the tile index is clamped to the wave's last tile, whose
+//   repeat hits the cache) so the compiler waits for exactly one tile.
+// * A unit wholly inside one workgroup's share is finished there. Only the
+//   first and last unit of a share can be cut; their (m, l, acc) partials go
+//   to two workspace slots per workgroup and a small second kernel merges
+//   them with a log-sum-exp reduce. The kernel boundary orders the two, so no
+//   cache flushes or atomics are needed; no host sync, no memset.
 //
 // Tokens past seq_len are scored -inf and their V rows zeroed (the
 // reference's masked loads, :88-105). seq_len is clamped to the block table's
-// capacity and block ids outside [0, num_blocks) read as zeros, so a malformed
-// table cannot fault. seq_len == 0 yields NaN, as the reference's 0/0 does.
+// capacity, and a tile whose block id is outside [0, num_blocks) is masked
+// (the reference would read out of bounds), so a malformed table cannot
+// fault. seq_len == 0 yields NaN, as the reference's 0/0 does.
 //
 // A generic kernel (one wave per (sequence, q-head), fp32 VALU math) covers
-// what the MFMA path does not: fp32 caches, head_dim other than 64/128,
-// non-unit innermost strides.
+// what the MFMA path does not: fp32 caches, head_dim other than 64/128, GQA
+// groups over 16, non-unit innermost strides.
 #include <cmath>
 
 #include "tsa_common.h"
@@ -64,16 +71,18 @@ struct DecodeArgs {
   int64_t bt_s0, bt_s1, sl_s;
   int64_t NB;
   int32_t B, Hq, Hkv, G, BS, max_blocks, D;
-  int32_t tiles_per_split, max_splits;
+  int32_t W;        // workgroups sharing the tile list
   float scale_log2;
-  float* ws_o;         // [B][Hq][max_splits][D]
-  float* ws_ml;        // [B][Hq][max_splits][2]
+  float* part_o;    // [W][2][G][D]   unnormalised acc of a cut unit
+  float* part_ml;   // [W][2][G][2]   its running max (log2 domain) and sum
+  int64_t* cut;     // [W][4]         unit cut at workgroup w's first tile:
+                    //                {start tile P or -1, tiles n, unit, share}
 };
 
 constexpr int kWaves = 4;
 constexpr float kNegInf = -INFINITY;
 
-// Minimum waves per SIMD the split kernel is compiled for (register budget:
+// Minimum waves per SIMD the stream kernel is compiled for (register budget:
 // 512 / waves VGPRs per lane), and the number of tiles each wave keeps in
 // registers (RING - 1 in flight while one computes).
 #ifndef TSA_DECODE_WAVES_PER_EU
@@ -90,267 +99,356 @@ __device__ __forceinline__ int64_t clamp_len(const DecodeArgs& a, int s) {
   return L < 0 ? 0 : (L > cap ? cap : L);
 }
 
+__device__ __forceinline__ int tiles_of(const DecodeArgs& a, int s) {
+  return static_cast<int>((clamp_len(a, s) + 15) >> 4);
+}
+
+// Exclusive prefix of tiles per sequence into pref[0..B] (pref[B] = total),
+// computed by the whole 256-thread workgroup; tmp holds 256 ints of scratch.
+__device__ void tile_prefix(const DecodeArgs& a, int* pref, int* tmp) {
+  const int tid = threadIdx.x;
+  const int per = (a.B + 255) / 256;
+  int local = 0;
+  for (int i = 0; i < per; ++i) {
+    const int s = tid * per + i;
+    if (s < a.B) {
+      const int n = tiles_of(a, s);
+      pref[s] = local;
+      local += n;
+    }
+  }
+  tmp[tid] = local;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {  // inclusive Hillis-Steele scan
+    const int v = tid >= off ? tmp[tid - off] : 0;
+    __syncthreads();
+    tmp[tid] += v;
+    __syncthreads();
+  }
+  const int base = tid > 0 ? tmp[tid - 1] : 0;
+  for (int i = 0; i < per; ++i) {
+    const int s = tid * per + i;
+    if (s < a.B) pref[s] += base;
+  }
+  if (tid == 255) pref[a.B] = tmp[255];
+  __syncthreads();
+}
+
 template <typename T, int D, bool PAGE16, bool CONTIG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TSA_DECODE_WAVES_PER_EU)))
-void paged_decode_mfma(DecodeArgs a) {
+void paged_decode_stream(DecodeArgs a) {
   constexpr int KJ = D / 32;  // k-steps of the score MFMA
   extern __shared__ float lds[];
-  // Workgroups are numbered kv-head fastest, then sequence, then split. The
-  // hardware deals consecutive workgroup ids to the 8 XCDs round-robin, so
-  // every XCD gets an even share of each split index (split-major order would
-  // leave the XCDs that draw the late, mostly empty splits idle), and the
-  // always-populated first splits are dispatched first.
-  const int id = blockIdx.x;
-  const int kvh = id % a.Hkv;
-  const int s = (id / a.Hkv) % a.B;
-  const int split = id / (a.Hkv * a.B);
+  const int G = a.G, Hkv = a.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
   // Wave-uniform (scalar) so tile indices, block-table reads and page bases
   // stay in SGPRs and the table lookups are scalar loads.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int G = a.G;
-  const int64_t L = clamp_len(a, s);
-  const int ntiles = static_cast<int>((L + 15) >> 4);
-  const int nsplit = (ntiles + a.tiles_per_split - 1) / a.tiles_per_split;
+  const int w = blockIdx.x;
 
-  if (split >= nsplit) {
-    if (L == 0 && split == 0) {  // empty sequence: 0/0 like the reference
-      for (int idx = tid; idx < G * D; idx += 256) {
-        T* o = static_cast<T*>(a.out) + s * a.o_ss + (kvh * G + idx / D) * a.o_sh + (idx % D);
-        *o = from_float<T>(NAN);
+  float* s_o = lds;                          // [kWaves][G][D]
+  float* s_m = s_o + kWaves * G * D;         // [kWaves][G]
+  float* s_l = s_m + kWaves * G;             // [kWaves][G]
+  int* pref = reinterpret_cast<int*>(s_l + kWaves * G);  // [B + 1]
+  int* tmp = pref + a.B + 1;                 // [256]
+  tile_prefix(a, pref, tmp);
+
+  const int64_t total = static_cast<int64_t>(Hkv) * pref[a.B];
+  const int64_t share = (total + a.W - 1) / a.W;
+  const int64_t lo = w * share;
+  const int64_t hi = min(total, lo + share);
+  if (w == 0) {  // empty sequences: 0/0 like the reference
+    for (int sq = 0; sq < a.B; ++sq) {
+      if (pref[sq + 1] != pref[sq]) continue;
+      for (int idx = tid; idx < a.Hq * D; idx += 256) {
+        T* op = static_cast<T*>(a.out) + sq * a.o_ss + (idx / D) * a.o_sh + (idx % D) * a.o_sd;
+        *op = from_float<T>(NAN);
       }
     }
+  }
+  if (lo >= hi) {
+    if (tid == 0) a.cut[w * 4] = -1;
     return;
   }
-  const int t_begin = split * a.tiles_per_split;
-  const int t_end = min(ntiles, t_begin + a.tiles_per_split);
 
-  // Q^T operand: lane (g, c) holds head c, dims 8(g + 4j)..+8 for k-step j.
-  u32x4 qop[KJ];
+  // First unit: the last sequence with Hkv * pref[s] <= lo (that skips empty
+  // sequences), then the kv head inside it.
+  int s;
   {
-    const T* qrow = static_cast<const T*>(a.q) + s * a.q_ss + (kvh * G + c) * a.q_sh;
-#pragma unroll
-    for (int j = 0; j < KJ; ++j)
-      qop[j] = c < G ? *reinterpret_cast<const u32x4*>(qrow + 8 * (g + 4 * j)) : u32x4{0, 0, 0, 0};
+    int l0 = 0, h0 = a.B;  // answer in [l0, h0)
+    while (h0 - l0 > 1) {
+      const int mid = (l0 + h0) >> 1;
+      if (static_cast<int64_t>(Hkv) * pref[mid] <= lo) l0 = mid; else h0 = mid;
+    }
+    s = l0;
+  }
+  int kvh = static_cast<int>((lo - static_cast<int64_t>(Hkv) * pref[s]) / (pref[s + 1] - pref[s]));
+  const bool v_lane = 8 * c < D;
+  if (tid == 0) {  // tell the merge kernel whether a unit is cut at this share's start
+    const int n0 = pref[s + 1] - pref[s];
+    const int64_t P0 = static_cast<int64_t>(Hkv) * pref[s] + static_cast<int64_t>(kvh) * n0;
+    int64_t* rec = a.cut + w * 4;
+    rec[0] = P0 < lo ? P0 : -1;
+    rec[1] = n0;
+    rec[2] = static_cast<int64_t>(s) * Hkv + kvh;
+    rec[3] = share;
   }
 
-  const int32_t* bt_row = a.bt + s * a.bt_s0;
-  const T* kbase = static_cast<const T*>(a.kc) + kvh * a.kc_h;
-  const T* vbase = static_cast<const T*>(a.vc) + kvh * a.vc_h;
-  const bool v_lane = 8 * c < D;
+  for (bool first_unit = true;; first_unit = false) {
+    const int n_s = pref[s + 1] - pref[s];
+    const int64_t P = static_cast<int64_t>(Hkv) * pref[s] + static_cast<int64_t>(kvh) * n_s;
+    if (P >= hi) break;
+    const int t_begin = static_cast<int>(max(lo, P) - P);
+    const int t_end = static_cast<int>(min(hi, P + n_s) - P);
+    const bool whole = t_begin == 0 && t_end == n_s;
+    const int64_t L = clamp_len(a, s);
 
-  auto page_of = [&](int64_t tok, int64_t& phys, int64_t& slot) -> bool {
-    const int64_t lb = tok / a.BS;
-    phys = bt_row[lb * a.bt_s1];
-    slot = tok - lb * a.BS;
-    return phys >= 0 && phys < a.NB;
-  };
-
-  // Slot strides: the contiguous pool layout makes them the compile-time D.
-  const int64_t ks = CONTIG ? D : a.kc_s;
-  const int64_t vs = CONTIG ? D : a.vc_s;
-
-  // K operand (token c of the tile) and V rows (tokens 4g..4g+3) of one tile.
-  // With 16-token pages the whole tile is one page: the loads are
-  // unconditional (an invalid page id reads page 0 and the tile is masked in
-  // compute_tile), so nothing waits on the data until it is consumed.
-  auto load_tile = [&](int t, u32x4 (&ko)[KJ], u32x4 (&vo)[4]) {
-    const int64_t tok0 = static_cast<int64_t>(t) * 16;
-    if constexpr (PAGE16) {
-      int64_t phys, slot0;
-      if (!page_of(tok0, phys, slot0)) phys = 0;
-      const T* kp = kbase + phys * a.kc_b + (slot0 + c) * ks + 8 * g;
-#pragma unroll
-      for (int j = 0; j < KJ; ++j) ko[j] = *reinterpret_cast<const u32x4*>(kp + 32 * j);
-      const T* vp = vbase + phys * a.vc_b + (slot0 + 4 * g) * vs + (v_lane ? 8 * c : 0);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) vo[r] = *reinterpret_cast<const u32x4*>(vp + r * vs);
-    } else {
-      int64_t phys, slot;
-      const int64_t tk = tok0 + c;
-      const bool okk = tk < L && page_of(tk, phys, slot);
-      const T* kp = kbase + (okk ? phys * a.kc_b + slot * ks : 0);
+    // Q^T operand: lane (g, c) holds head c, dims 8(g + 4j)..+8 for k-step j.
+    u32x4 qop[KJ];
+    {
+      const T* qrow = static_cast<const T*>(a.q) + s * a.q_ss + (kvh * G + c) * a.q_sh;
 #pragma unroll
       for (int j = 0; j < KJ; ++j)
-        ko[j] = okk ? *reinterpret_cast<const u32x4*>(kp + 8 * (g + 4 * j)) : u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t tv = tok0 + 4 * g + r;
-        const bool okv = v_lane && tv < L && page_of(tv, phys, slot);
-        vo[r] = okv ? *reinterpret_cast<const u32x4*>(vbase + phys * a.vc_b + slot * vs + 8 * c)
-                    : u32x4{0, 0, 0, 0};
-      }
+        qop[j] = c < G ? *reinterpret_cast<const u32x4*>(qrow + 8 * (g + 4 * j)) : u32x4{0, 0, 0, 0};
     }
-  };
 
-  float m = kNegInf;  // running max of head c (log2 domain), same in all 4 row-groups
-  float l = 0.f;      // this lane's share of head c's softmax denominator
-  f32x4 acc[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int32_t* bt_row = a.bt + s * a.bt_s0;
+    const T* kbase = static_cast<const T*>(a.kc) + kvh * a.kc_h;
+    const T* vbase = static_cast<const T*>(a.vc) + kvh * a.vc_h;
+    // Slot strides: the contiguous pool layout makes them the compile-time D.
+    const int64_t ks = CONTIG ? D : a.kc_s;
+    const int64_t vs = CONTIG ? D : a.vc_s;
 
-  auto compute_tile = [&](int t, const u32x4 (&ko)[KJ], u32x4 (&vo)[4]) {
-    const int64_t tok0 = static_cast<int64_t>(t) * 16;
-    // Tokens past seq_len, and (page-16 path) tiles whose block id is out of
-    // range, are masked: score -inf and V rows zeroed so 0 * (inf/nan) cannot
-    // leak into the accumulator. Only the last tile of a sequence (or a bad
-    // page) takes this wave-uniform branch.
-    int64_t lim = L;
-    if constexpr (PAGE16) {
-      int64_t phys, slot0;
-      if (!page_of(tok0, phys, slot0)) lim = tok0;
-    }
-    if (tok0 + 16 > lim) {
+    auto page_of = [&](int64_t tok, int64_t& phys, int64_t& slot) -> bool {
+      const int64_t lb = tok / a.BS;
+      phys = bt_row[lb * a.bt_s1];
+      slot = tok - lb * a.BS;
+      return phys >= 0 && phys < a.NB;
+    };
+
+    // K operand (token c of the tile) and V rows (tokens 4g..4g+3) of one
+    // tile. With 16-token pages the whole tile is one page: the loads are
+    // unconditional (an invalid page id reads page 0 and the tile is masked in
+    // compute_tile), so nothing waits on the data until it is consumed.
+    auto load_tile = [&](int t, u32x4 (&ko)[KJ], u32x4 (&vo)[4]) {
+      const int64_t tok0 = static_cast<int64_t>(t) * 16;
+      if constexpr (PAGE16) {
+        int64_t phys, slot0;
+        if (!page_of(tok0, phys, slot0)) phys = 0;
+        const T* kp = kbase + phys * a.kc_b + (slot0 + c) * ks + 8 * g;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (tok0 + 4 * g + r >= lim) vo[r] = u32x4{0, 0, 0, 0};
-    }
-    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < KJ; ++j) ko[j] = *reinterpret_cast<const u32x4*>(kp + 32 * j);
+        const T* vp = vbase + phys * a.vc_b + (slot0 + 4 * g) * vs + (v_lane ? 8 * c : 0);
 #pragma unroll
-    for (int j = 0; j < KJ; ++j) sc = mfma_k32<T>(ko[j], qop[j], sc);
-    // sc[r] = q_c . k_{tok0 + 4g + r}
-    const int64_t tb = tok0 + 4 * g;
-    float sv[4];
-    float tmax = kNegInf;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sv[r] = tb + r < lim ? sc[r] * a.scale_log2 : kNegInf;
-      tmax = fmaxf(tmax, sv[r]);
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m, tmax);
-    if (__any(m_new > m)) {
-      const float alpha = fast_exp2(m - m_new);  // 0 on the first tile (m = -inf)
-      l *= alpha;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float ar = __shfl(alpha, 4 * g + r, 64);  // alpha of head 4g + r
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc[u][r] *= ar;
-      }
-      m = m_new;
-    }
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = fast_exp2(sv[r] - m);
-      l += p[r];
-    }
-    const u32x2 pop = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int w = u >> 1;
-      u32x2 bop;
-      if (u & 1) {
-        bop[0] = pack_hi(vo[0][w], vo[1][w]);
-        bop[1] = pack_hi(vo[2][w], vo[3][w]);
+        for (int r = 0; r < 4; ++r) vo[r] = *reinterpret_cast<const u32x4*>(vp + r * vs);
       } else {
-        bop[0] = pack_lo(vo[0][w], vo[1][w]);
-        bop[1] = pack_lo(vo[2][w], vo[3][w]);
-      }
-      acc[u] = mfma_k16<T>(pop, bop, acc[u]);  // acc[u][r] = O[head 4g + r][dim 8c + u]
-    }
-  };
-
-  // Ring of RING tile buffers over this wave's tiles t_begin + wave + 4i,
-  // i < nw: while one tile is on the matrix cores the loads of the next
-  // RING-1 are in flight. The scheduling barriers keep every buffer's loads in
-  // ring order on all paths, so a compute waits for its own tile only.
-  const int first = t_begin + wave;
-  const int nw = first < t_end ? (t_end - first + kWaves - 1) / kWaves : 0;
-  if (nw > 0) {
-    auto tile = [&](int i) { return first + kWaves * min(i, nw - 1); };
-    u32x4 kbuf[RING][KJ], vbuf[RING][4];
+        int64_t phys, slot;
+        const int64_t tk = tok0 + c;
+        const bool okk = tk < L && page_of(tk, phys, slot);
+        const T* kp = kbase + (okk ? phys * a.kc_b + slot * ks : 0);
 #pragma unroll
-    for (int d = 0; d < RING; ++d) {
-      load_tile(tile(d), kbuf[d], vbuf[d]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    for (int i = 0; i < nw; i += RING) {
+        for (int j = 0; j < KJ; ++j)
+          ko[j] = okk ? *reinterpret_cast<const u32x4*>(kp + 8 * (g + 4 * j)) : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t tv = tok0 + 4 * g + r;
+          const bool okv = v_lane && tv < L && page_of(tv, phys, slot);
+          vo[r] = okv ? *reinterpret_cast<const u32x4*>(vbase + phys * a.vc_b + slot * vs + 8 * c)
+                      : u32x4{0, 0, 0, 0};
+        }
+      }
+    };
+
+    float m = kNegInf;  // running max of head c (log2 domain), same in all 4 row-groups
+    float l = 0.f;      // this lane's share of head c's softmax denominator
+    f32x4 acc[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute_tile = [&](int t, const u32x4 (&ko)[KJ], u32x4 (&vo)[4]) {
+      const int64_t tok0 = static_cast<int64_t>(t) * 16;
+      // Tokens past seq_len, and (page-16 path) tiles whose block id is out of
+      // range, are masked: score -inf and V rows zeroed so 0 * (inf/nan) cannot
+      // leak into the accumulator. Only the last tile of a sequence (or a bad
+      // page) takes this wave-uniform branch.
+      int64_t lim = L;
+      if constexpr (PAGE16) {
+        int64_t phys, slot0;
+        if (!page_of(tok0, phys, slot0)) lim = tok0;
+      }
+      if (tok0 + 16 > lim) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (tok0 + 4 * g + r >= lim) vo[r] = u32x4{0, 0, 0, 0};
+      }
+      f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) sc = mfma_k32<T>(ko[j], qop[j], sc);
+      // sc[r] = q_c . k_{tok0 + 4g + r}
+      const int64_t tb = tok0 + 4 * g;
+      float sv[4];
+      float tmax = kNegInf;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sv[r] = tb + r < lim ? sc[r] * a.scale_log2 : kNegInf;
+        tmax = fmaxf(tmax, sv[r]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m, tmax);
+      if (__any(m_new > m)) {
+        const float alpha = m_new == kNegInf ? 1.f : fast_exp2(m - m_new);  // 0 on the first tile
+        l *= alpha;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float ar = __shfl(alpha, 4 * g + r, 64);  // alpha of head 4g + r
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc[u][r] *= ar;
+        }
+        m = m_new;
+      }
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = m == kNegInf ? 0.f : fast_exp2(sv[r] - m);
+        l += p[r];
+      }
+      const u32x2 pop = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int wd = u >> 1;
+        u32x2 bop;
+        if (u & 1) {
+          bop[0] = pack_hi(vo[0][wd], vo[1][wd]);
+          bop[1] = pack_hi(vo[2][wd], vo[3][wd]);
+        } else {
+          bop[0] = pack_lo(vo[0][wd], vo[1][wd]);
+          bop[1] = pack_lo(vo[2][wd], vo[3][wd]);
+        }
+        acc[u] = mfma_k16<T>(pop, bop, acc[u]);  // acc[u][r] = O[head 4g + r][dim 8c + u]
+      }
+    };
+
+    // Ring of RING tile buffers over this wave's tiles t_begin + wave + 4i,
+    // i < nw. The scheduling barriers keep every buffer's loads in ring order
+    // on all paths, so a compute waits for its own tile only.
+    const int first = t_begin + wave;
+    const int nw = first < t_end ? (t_end - first + kWaves - 1) / kWaves : 0;
+    if (nw > 0) {
+      auto tile = [&](int i) { return first + kWaves * min(i, nw - 1); };
+      u32x4 kbuf[RING][KJ], vbuf[RING][4];
 #pragma unroll
       for (int d = 0; d < RING; ++d) {
-        if (i + d < nw) compute_tile(tile(i + d), kbuf[d], vbuf[d]);
-        __builtin_amdgcn_sched_barrier(0);
-        load_tile(tile(i + d + RING), kbuf[d], vbuf[d]);
+        load_tile(tile(d), kbuf[d], vbuf[d]);
         __builtin_amdgcn_sched_barrier(0);
       }
-    }
-  }
-
-  // Head c's denominator: sum the four row-groups.
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-
-  // Merge the waves through LDS: [wave][head][D] acc, then [wave][head] m and l.
-  float* s_o = lds;
-  float* s_m = lds + kWaves * G * D;
-  float* s_l = s_m + kWaves * G;
+      for (int i = 0; i < nw; i += RING) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int hd = 4 * g + r;
-    if (hd < G && v_lane) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) s_o[(wave * G + hd) * D + 8 * c + u] = acc[u][r];
-    }
-  }
-  if (g == 0 && c < G) {
-    s_m[wave * G + c] = m;
-    s_l[wave * G + c] = l;
-  }
-  __syncthreads();
-
-  const int64_t head0 = static_cast<int64_t>(s) * a.Hq + kvh * G;  // row of (s, first head of the group)
-  for (int idx = tid; idx < G * D; idx += 256) {
-    const int hd = idx / D, d = idx - hd * D;
-    float M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w * G + hd]);
-    float o = 0.f, den = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float e = fast_exp2(s_m[w * G + hd] - M);
-      o += e * s_o[(w * G + hd) * D + d];
-      den += e * s_l[w * G + hd];
-    }
-    if (nsplit == 1) {
-      T* op = static_cast<T*>(a.out) + s * a.o_ss + (kvh * G + hd) * a.o_sh + d * a.o_sd;
-      *op = from_float<T>(o / den);
-    } else {
-      const int64_t slot = (head0 + hd) * a.max_splits + split;
-      a.ws_o[slot * D + d] = o;
-      if (d == 0) {
-        a.ws_ml[slot * 2] = M;
-        a.ws_ml[slot * 2 + 1] = den;
+        for (int d = 0; d < RING; ++d) {
+          if (i + d < nw) compute_tile(tile(i + d), kbuf[d], vbuf[d]);
+          __builtin_amdgcn_sched_barrier(0);
+          load_tile(tile(i + d + RING), kbuf[d], vbuf[d]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
+    }
+
+    // Head c's denominator: sum the four row-groups.
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+
+    // Merge the waves through LDS.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int hd = 4 * g + r;
+      if (hd < G && v_lane) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s_o[(wave * G + hd) * D + 8 * c + u] = acc[u][r];
+      }
+    }
+    if (g == 0 && c < G) {
+      s_m[wave * G + c] = m;
+      s_l[wave * G + c] = l;
+    }
+    __syncthreads();
+    const int slot = first_unit ? 0 : 1;
+    for (int idx = tid; idx < G * D; idx += 256) {
+      const int hd = idx / D, d = idx - hd * D;
+      float M = kNegInf;
+#pragma unroll
+      for (int wv = 0; wv < kWaves; ++wv) M = fmaxf(M, s_m[wv * G + hd]);
+      float o = 0.f, den = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < kWaves; ++wv) {
+        const float mw = s_m[wv * G + hd];
+        const float e = mw == kNegInf ? 0.f : fast_exp2(mw - M);
+        o += e * s_o[(wv * G + hd) * D + d];
+        den += e * s_l[wv * G + hd];
+      }
+      if (whole) {
+        T* op = static_cast<T*>(a.out) + s * a.o_ss + (kvh * G + hd) * a.o_sh + d * a.o_sd;
+        *op = from_float<T>(o / den);
+      } else {
+        const int64_t sl = (static_cast<int64_t>(w) * 2 + slot) * G + hd;
+        a.part_o[sl * D + d] = o;
+        if (d == 0) {
+          a.part_ml[sl * 2] = M;
+          a.part_ml[sl * 2 + 1] = den;
+        }
+      }
+    }
+    __syncthreads();  // the LDS is reused by the next unit
+
+    // Next unit: next kv head, then the next non-empty sequence.
+    if (++kvh == Hkv) {
+      kvh = 0;
+      do {
+        ++s;
+      } while (s < a.B && pref[s + 1] == pref[s]);
+      if (s >= a.B) break;
     }
   }
 }
 
-// Merge the splits of one (sequence, kv head): out = sum_s 2^(m_s - M) acc_s /
-// sum_s 2^(m_s - M) l_s. Sequences that fit one split were written directly.
+// Finish the units that were cut between workgroups: out = sum_w 2^(m_w - M)
+// acc_w / sum_w 2^(m_w - M) l_w over the contributing workgroups' slots.
+// Merge workgroup w reads the cut record of stream workgroup w; the unit is
+// merged by the first boundary inside it (w == w0 + 1, w0 the workgroup whose
+// share it starts in), every other workgroup returns at once. The unit is
+// w0's last unit (slot 1) unless it starts exactly at w0's share (slot 0);
+// in every later workgroup it is the first unit (slot 0).
 template <typename T>
-__global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
-  const int kvh = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
+__global__ __launch_bounds__(256) void paged_decode_stream_merge(DecodeArgs a) {
+  const int w = blockIdx.x, tid = threadIdx.x;
+  const int64_t* rec = a.cut + w * 4;
+  const int64_t P = rec[0];
+  if (P < 0) return;
+  const int64_t n = rec[1], share = rec[3];
+  const int w0 = static_cast<int>(P / share);
+  if (w != w0 + 1) return;
+  const int w1 = static_cast<int>((P + n - 1) / share);
+  const int u = static_cast<int>(rec[2]);
+  const int s = u / a.Hkv, kvh = u - s * a.Hkv;
   const int G = a.G, D = a.D;
-  const int64_t L = clamp_len(a, s);
-  const int ntiles = static_cast<int>((L + 15) >> 4);
-  const int nsplit = (ntiles + a.tiles_per_split - 1) / a.tiles_per_split;
-  if (nsplit <= 1) return;
-  const int64_t head0 = static_cast<int64_t>(s) * a.Hq + kvh * G;
+  T* orow = static_cast<T*>(a.out) + s * a.o_ss + (kvh * G) * a.o_sh;
+  const int slot0 = P == static_cast<int64_t>(w0) * share ? 0 : 1;
   for (int idx = tid; idx < G * D; idx += 256) {
     const int hd = idx / D, d = idx - hd * D;
-    const int64_t base = (head0 + hd) * a.max_splits;
     float M = kNegInf;
-    for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, a.ws_ml[(base + sp) * 2]);
-    float o = 0.f, den = 0.f;
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const float e = fast_exp2(a.ws_ml[(base + sp) * 2] - M);
-      o += e * a.ws_o[(base + sp) * D + d];
-      den += e * a.ws_ml[(base + sp) * 2 + 1];
+    for (int v = w0; v <= w1; ++v) {
+      const int slot = v == w0 ? slot0 : 0;
+      M = fmaxf(M, a.part_ml[((static_cast<int64_t>(v) * 2 + slot) * G + hd) * 2]);
     }
-    T* op = static_cast<T*>(a.out) + s * a.o_ss + (kvh * G + hd) * a.o_sh + d * a.o_sd;
-    *op = from_float<T>(o / den);
+    float o = 0.f, den = 0.f;
+    for (int v = w0; v <= w1; ++v) {
+      const int slot = v == w0 ? slot0 : 0;
+      const int64_t sl = (static_cast<int64_t>(v) * 2 + slot) * G + hd;
+      const float mw = a.part_ml[sl * 2];
+      const float e = mw == kNegInf ? 0.f : fast_exp2(mw - M);
+      o += e * a.part_o[sl * D + d];
+      den += e * a.part_ml[sl * 2 + 1];
+    }
+    orow[hd * a.o_sh + d * a.o_sd] = from_float<T>(o / den);
   }
 }
 
@@ -380,18 +478,18 @@ __global__ __launch_bounds__(64) void paged_decode_generic(DecodeArgs a) {
       const int64_t lb = tok / a.BS;
       phys = bt_row[lb * a.bt_s1];
       slot = tok - lb * a.BS;
-      float dot = 0.f;
       if (phys >= 0 && phys < a.NB) {
+        float dot = 0.f;
         const T* kr = kbase + phys * a.kc_b + slot * a.kc_s;
         for (int d = 0; d < D; ++d) dot += to_float(qrow[d * a.q_sd]) * to_float(kr[d * a.kc_d]);
+        sc = dot * a.scale_log2;
       }
-      sc = dot * a.scale_log2;
     }
     float cmax = sc;
     for (int off = 32; off >= 1; off >>= 1) cmax = fmaxf(cmax, __shfl_xor(cmax, off, 64));
     const float m_new = fmaxf(m, cmax);
-    const float alpha = fast_exp2(m - m_new);
-    const float p = fast_exp2(sc - m_new);
+    const float alpha = m_new == kNegInf ? 1.f : fast_exp2(m - m_new);
+    const float p = m_new == kNegInf ? 0.f : fast_exp2(sc - m_new);
     float psum = p;
     for (int off = 32; off >= 1; off >>= 1) psum += __shfl_xor(psum, off, 64);
     l = l * alpha + psum;
@@ -420,35 +518,31 @@ __global__ __launch_bounds__(64) void paged_decode_generic(DecodeArgs a) {
   }
 }
 
-struct DecodePlan {
-  int tiles_per_split;
-  int max_splits;
-  size_t ws_o_bytes, ws_ml_bytes, total;
-};
-
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-static DecodePlan make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_blocks, int64_t BS,
-                            int32_t tiles_per_split) {
+// Workgroups of the stream kernel: two per CU (the register budget lets two
+// 4-wave workgroups share a CU), so all of them are resident at once.
+static int default_workgroups() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return 2 * cus;
+}
+
+struct DecodePlan {
+  int W;
+  size_t part_o_bytes, part_ml_bytes, cut_bytes, total;
+};
+
+static DecodePlan make_plan(int64_t Hq, int64_t Hkv, int64_t D, int32_t num_workgroups) {
   DecodePlan p{};
-  const int64_t max_tiles = (max_blocks * BS + 15) / 16;
-  int64_t tps = tiles_per_split;
-  if (tps <= 0) {
-    // Aim for ~4096 workgroup slots over the longest sequence's tiles.
-    const int64_t units = B * Hkv;
-    tps = (units * max_tiles + 4095) / 4096;
-    if (tps < 8) tps = 8;
-  }
-  tps = (tps + kWaves - 1) / kWaves * kWaves;
-  if (tps > 1 << 20) tps = 1 << 20;
-  p.tiles_per_split = static_cast<int>(tps);
-  p.max_splits = static_cast<int>(max_tiles > 0 ? (max_tiles + tps - 1) / tps : 1);
-  if (p.max_splits < 1) p.max_splits = 1;
-  if (p.max_splits > 1) {
-    p.ws_o_bytes = align256(static_cast<size_t>(B * Hq) * p.max_splits * D * sizeof(float));
-    p.ws_ml_bytes = align256(static_cast<size_t>(B * Hq) * p.max_splits * 2 * sizeof(float));
-  }
-  p.total = p.ws_o_bytes + p.ws_ml_bytes;
+  p.W = num_workgroups > 0 ? num_workgroups : default_workgroups();
+  const int64_t G = Hq / Hkv;
+  p.part_o_bytes = align256(static_cast<size_t>(p.W) * 2 * G * D * sizeof(float));
+  p.part_ml_bytes = align256(static_cast<size_t>(p.W) * 2 * G * 2 * sizeof(float));
+  p.cut_bytes = align256(static_cast<size_t>(p.W) * 4 * sizeof(int64_t));
+  p.total = p.part_o_bytes + p.part_ml_bytes + p.cut_bytes;
   return p;
 }
 
@@ -460,12 +554,13 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream) {
     return check_launch("tsa_paged_decode");
   }
   if constexpr (sizeof(T) == 2) {
-    const dim3 grid(static_cast<uint32_t>(a.max_splits) * a.Hkv * a.B);
-    const size_t lds = static_cast<size_t>(kWaves) * a.G * (a.D + 2) * sizeof(float);
+    const size_t prefix_lds = static_cast<size_t>(a.B + 1 + 256) * sizeof(int);
+    const size_t lds = static_cast<size_t>(kWaves) * a.G * (a.D + 2) * sizeof(float) + prefix_lds;
     const bool page16 = a.BS % 16 == 0;
     const bool contig = a.kc_s == a.D && a.vc_s == a.D;
+    const dim3 grid(a.W);
 #define TSA_DECODE_LAUNCH(DD, P16, CT) \
-  paged_decode_mfma<T, DD, P16, CT><<<grid, dim3(256), lds, stream>>>(a)
+  paged_decode_stream<T, DD, P16, CT><<<grid, dim3(256), lds, stream>>>(a)
     if (a.D == 128) {
       if (page16 && contig) TSA_DECODE_LAUNCH(128, true, true);
       else if (page16) TSA_DECODE_LAUNCH(128, true, false);
@@ -476,10 +571,8 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream) {
       else TSA_DECODE_LAUNCH(64, false, false);
     }
 #undef TSA_DECODE_LAUNCH
-    if (a.max_splits > 1) {
-      if (int rc = check_launch("tsa_paged_decode")) return rc;
-      paged_decode_merge<T><<<dim3(a.Hkv, a.B), dim3(256), 0, stream>>>(a);
-    }
+    if (int rc = check_launch("tsa_paged_decode")) return rc;
+    paged_decode_stream_merge<T><<<dim3(a.W), dim3(256), 0, stream>>>(a);
   }
   return check_launch("tsa_paged_decode");
 }
@@ -490,15 +583,17 @@ using namespace tsa;
 
 extern "C" size_t tsa_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads,
                                                    int64_t head_dim, int64_t max_blocks_per_seq, int64_t block_size,
-                                                   int32_t tiles_per_split) {
-  if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0) return 0;
-  return make_plan(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size, tiles_per_split).total;
+                                                   int32_t num_workgroups) {
+  (void)max_blocks_per_seq;
+  (void)block_size;
+  if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || num_heads % num_kv_heads) return 0;
+  return make_plan(num_heads, num_kv_heads, head_dim, num_workgroups).total;
 }
 
 extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache,
                                 const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
                                 double softmax_scale, void* workspace, size_t workspace_bytes,
-                                int32_t tiles_per_split, void* stream) {
+                                int32_t num_workgroups, void* stream) {
   TSA_REQUIRE(view_ok(query, 3), "query must be a 3D tensor (num_seqs, num_heads, head_dim)");
   TSA_REQUIRE(view_ok(out, 3), "out must be a 3D tensor shaped like query");
   TSA_REQUIRE(view_ok(k_cache, 4) && view_ok(v_cache, 4),
@@ -520,7 +615,10 @@ extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, cons
   TSA_REQUIRE(BS > 0, "block_size must be positive");
   TSA_REQUIRE(block_tables->size[0] == B && seq_lens->size[0] == B,
               "block_tables and seq_lens must have num_seqs (%lld) rows", (long long)B);
+  TSA_REQUIRE(B < 65536 && Hq < 65536, "num_seqs and num_heads must be below 65536");
+  TSA_REQUIRE(block_tables->size[1] * BS < (int64_t(1) << 31) / 16, "block table too long");
   TSA_UNSUPPORTED(D <= 512, "head_dim %lld > 512 is not implemented", (long long)D);
+  TSA_REQUIRE(num_workgroups >= 0, "num_workgroups must be non-negative");
 
   DecodeArgs a{};
   a.out = out->data; a.q = query->data; a.kc = k_cache->data; a.vc = v_cache->data;
@@ -540,18 +638,15 @@ extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, cons
   const bool mfma = (dt == TSA_BF16 || dt == TSA_F16) && (D == 64 || D == 128) && a.G <= 16 &&
                     rows_vec16(query) && rows_vec16(k_cache) && rows_vec16(v_cache) && out->stride[2] == 1;
   if (mfma) {
-    const DecodePlan plan = make_plan(B, Hq, Hkv, D, a.max_blocks, BS, tiles_per_split);
-    a.tiles_per_split = plan.tiles_per_split;
-    a.max_splits = plan.max_splits;
-    TSA_REQUIRE(plan.max_splits < 65536, "context too long for one launch (%d splits)", plan.max_splits);
-    if (plan.total > 0) {
-      TSA_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total,
-                  "workspace of %zu bytes is too small: %zu needed", workspace_bytes, plan.total);
-      TSA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
-      char* w = static_cast<char*>(workspace);
-      a.ws_o = reinterpret_cast<float*>(w);
-      a.ws_ml = reinterpret_cast<float*>(w + plan.ws_o_bytes);
-    }
+    const DecodePlan plan = make_plan(Hq, Hkv, D, num_workgroups);
+    a.W = plan.W;
+    TSA_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total,
+                "workspace of %zu bytes is too small: %zu needed", workspace_bytes, plan.total);
+    TSA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
+    char* ws = static_cast<char*>(workspace);
+    a.part_o = reinterpret_cast<float*>(ws);
+    a.part_ml = reinterpret_cast<float*>(ws + plan.part_o_bytes);
+    a.cut = reinterpret_cast<int64_t*>(ws + plan.part_o_bytes + plan.part_ml_bytes);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dt) {

@@ -31,10 +31,10 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor |
     return ws
 
 
-def decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks, block_size, tiles_per_split=0):
+def decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks, block_size, num_workgroups=0):
     lib = _lib.load()
     return int(lib.tsa_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks,
-                                                    block_size, tiles_per_split))
+                                                    block_size, num_workgroups))
 
 
 def paged_attention_forward(
@@ -45,7 +45,7 @@ def paged_attention_forward(
     block_size: int,
     seq_lens: torch.Tensor,
     *,
-    tiles_per_split: int = 0,
+    num_workgroups: int = 0,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Decode-phase paged attention, one new token per sequence.
@@ -54,7 +54,7 @@ def paged_attention_forward(
     ``seq_lens[s]`` tokens gathered through ``block_tables[s]``; q-head h reads
     kv head ``h // (Hq / Hkv)``. query: (B, Hq, D); caches (NB, Hkv, BS, D);
     block_tables (B, max_blocks) int32; seq_lens (B,) int32.
-    ``tiles_per_split`` (16-token tiles per workgroup, 0 = automatic) and
+    ``num_workgroups`` (workgroups sharing the tile list, 0 = two per CU) and
     ``out`` are extensions; the defaults reproduce the reference call.
     """
     if query.dim() != 3:
@@ -78,7 +78,7 @@ def paged_attention_forward(
     lib = _lib.load()
     stream = _lib.stream_of(dev)
     nbytes = int(lib.tsa_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim,
-                                                      block_tables.shape[1], k_cache.shape[2], tiles_per_split))
+                                                      block_tables.shape[1], k_cache.shape[2], num_workgroups))
     ws = _workspace(dev, stream, nbytes)
     views = [_lib.view(t) for t in (out, query, k_cache, v_cache, block_tables, seq_lens)]
     rc = lib.tsa_paged_decode(
@@ -86,7 +86,7 @@ def paged_attention_forward(
         softmax_scale,
         ws.data_ptr() if ws is not None else None,
         ws.numel() if ws is not None else 0,
-        int(tiles_per_split),
+        int(num_workgroups),
         stream,
     )
     _lib.check(rc, "paged_attention_forward")
