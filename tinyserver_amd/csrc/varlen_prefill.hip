@@ -23,6 +23,7 @@
 // A generic kernel (one wave per (query, q-head), fp32 VALU) covers fp32 and
 // head_dims other than 64/128 and non-unit innermost strides.
 #include <cmath>
+#include <type_traits>
 
 #include "tsa_common.h"
 
@@ -200,6 +201,260 @@ __global__ __launch_bounds__(256) void varlen_prefill_mfma(PrefillArgs a) {
   }
 }
 
+// LDS-staged GQA flash attention. A workgroup owns one kv head of one
+// sequence and 256/G queries: its 4 waves each hold 4 row tiles of 16 rows,
+// a row being a (query, q-head) pair of the group, so all 16 row tiles read
+// the same K/V. 32-key K/V blocks are staged once per workgroup in
+// double-buffered, padded LDS (row stride D+8 elements: the 16 lanes of a
+// 128-bit read hit 16 distinct bank quads), the next block's global loads in
+// flight while the current one is on the matrix cores. Per block a wave reads
+// the K operands once, runs the 4 tiles' scores, then builds the P.V B
+// operands from the V rows once and runs the 4 tiles' P.V. Causal tiles whose
+// first query precedes the block are skipped. Workgroup ids put the kv head
+// fastest (so a kv head's query blocks share one XCD's L2) and the heaviest
+// query blocks first.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void varlen_prefill_lds(PrefillArgs a) {
+  constexpr int KJ = D / 32;
+  constexpr int CPR = D / 8;            // 16-byte chunks per K/V row
+  constexpr int ROW = D + 8;            // padded LDS row, elements
+  constexpr int NCH = 32 * CPR / 256;   // chunks per thread per tensor per block
+  // A row's running max only moves when it grows by more than this (log2
+  // units): p = 2^(s - m) then stays below 2^8, and the accumulator is
+  // rescaled rarely. l uses the same m, so the result is unchanged.
+  constexpr float kRescale = 8.0f;
+  __shared__ __align__(16) uint16_t kl[2][32 * ROW];
+  __shared__ __align__(16) uint16_t vl[2][32 * ROW];
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = a.G, QB = 256 / G;
+  const int id = blockIdx.x;
+  const int kvh = id % a.Hkv;
+  const int rest = id / a.Hkv;
+  const int b = rest % a.nseq;
+  const int qblk = a.nqb - 1 - rest / a.nseq;
+  int64_t q_start64, q_len64, k_start64, k_len64;
+  seq_range(a.cu_q, a.cuq_s, b, a.total_q, q_start64, q_len64);
+  seq_range(a.cu_k, a.cuk_s, b, a.total_k, k_start64, k_len64);
+  // Positions inside one sequence fit 32 bits (cu_seqlens are int32).
+  const int q_len = static_cast<int>(q_len64), k_len = static_cast<int>(k_len64);
+  const int row0 = qblk * QB;
+  if (row0 >= q_len) return;
+
+  const T* kb_ptr = static_cast<const T*>(a.k) + k_start64 * a.k_st + kvh * a.k_sh;
+  const T* vb_ptr = static_cast<const T*>(a.v) + k_start64 * a.v_st + kvh * a.v_sh;
+  const bool v_lane = 8 * c < D;
+  const float cs = a.scale_log2;  // > 0 on this path
+
+  // Row tiles of this wave: rt = 4 wave + t -> query subtile rt / G, head rt % G.
+  int q0[4], head[4];
+  u32x4 qop[4][KJ];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int rt = 4 * wave + t;
+    q0[t] = row0 + 16 * (rt / G);
+    head[t] = kvh * G + rt % G;
+    const int row = q0[t] + c;
+    const T* qp = static_cast<const T*>(a.q) + (q_start64 + row) * a.q_st + head[t] * a.q_sh;
+#pragma unroll
+    for (int j = 0; j < KJ; ++j)
+      qop[t][j] = row < q_len ? *reinterpret_cast<const u32x4*>(qp + 8 * (g + 4 * j)) : u32x4{0, 0, 0, 0};
+  }
+
+  float m[4], l[4];
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    m[t] = kNegInfP;
+    l[t] = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int q_last = row0 + QB < q_len ? row0 + QB : q_len;  // one past the block's last query
+  const int kend = a.causal ? (k_len < q_last ? k_len : q_last) : k_len;
+  const int nblk = (kend + 31) / 32;
+
+  // Two register stages of global loads: block i+2 is in flight while block
+  // i is computed and block i+1 sits in LDS.
+  u32x4 kr[2][NCH], vr[2][NCH];
+  auto gload = [&](int blk, int st) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int qc = tid + 256 * i;
+      const int key = qc / CPR, ch = qc % CPR;
+      const int kk = blk * 32 + key;
+      const bool ok = kk < k_len;
+      kr[st][i] = ok ? *reinterpret_cast<const u32x4*>(kb_ptr + static_cast<int64_t>(kk) * a.k_st + 8 * ch)
+                     : u32x4{0, 0, 0, 0};
+      vr[st][i] = ok ? *reinterpret_cast<const u32x4*>(vb_ptr + static_cast<int64_t>(kk) * a.v_st + 8 * ch)
+                     : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto swrite = [&](int buf, int st) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int qc = tid + 256 * i;
+      const int key = qc / CPR, ch = qc % CPR;
+      *reinterpret_cast<u32x4*>(&kl[buf][key * ROW + 8 * ch]) = kr[st][i];
+      *reinterpret_cast<u32x4*>(&vl[buf][key * ROW + 8 * ch]) = vr[st][i];
+    }
+  };
+
+  // Block blk computes from LDS buffer blk & 1 while block blk + 2's global
+  // loads are in flight into register stage blk & 1 and block blk + 1 (stage
+  // (blk + 1) & 1) is written to the other LDS buffer. The loop is unrolled by
+  // two so the stages are compile-time registers, and the loads are
+  // unconditional (the block index is clamped; a repeated block hits the
+  // cache) so each wait covers exactly the stage it needs.
+  auto clampb = [&](int blk) { return blk < nblk ? blk : nblk - 1; };
+  auto block_step = [&](int blk, auto stage) {
+    constexpr int st = decltype(stage)::value;
+    const int buf = st;
+    gload(clampb(blk + 2), st);
+    __builtin_amdgcn_sched_barrier(0);
+    const int kb0 = blk * 32;
+
+    // Skip the block only when none of the wave's tiles sees it (a single
+    // wave-uniform branch): per-tile branches around the MFMAs would force the
+    // accumulators through VGPR copies and serialise the matrix pipe. A tile
+    // that is dead for this block is masked to p = 0 instead.
+    bool any_live = false;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) any_live |= q0[t] < q_len && !(a.causal && kb0 > q0[t] + 15);
+    if (any_live) {
+    // K operands of the block: lane (g, c) holds key 16ks + c, dims 8(g+4j)..+8.
+    u32x4 kop[2][KJ];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int j = 0; j < KJ; ++j)
+        kop[ks][j] = *reinterpret_cast<const u32x4*>(&kl[buf][(16 * ks + c) * ROW + 8 * (g + 4 * j)]);
+
+    // Scores of all live tiles first, so the softmax VALU work of one tile
+    // overlaps the score MFMAs of the next.
+    f32x4 sc[4][2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        sc[t][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) sc[t][ks] = mfma_k32<T>(kop[ks][j], qop[t][j], sc[t][ks]);
+      }
+    }
+
+    u32x4 pop[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      // Keys past k_len, and (causal) keys after the row's query, only occur in
+      // a sequence's last block or on the diagonal: a wave-uniform branch.
+      if (kb0 + 32 > k_len || (a.causal && kb0 + 31 > q0[t])) {
+        const int qq = q0[t] + c;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int kk = kb0 + 16 * ks + 4 * g + r;
+            if (!(kk < k_len && (!a.causal || kk <= qq))) sc[t][ks][r] = kNegInfP;
+          }
+      }
+      float tmax = kNegInfP;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[t][ks][r]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float mt = tmax * cs;
+      if (__any(mt > m[t] + kRescale)) {
+        const float m_new = fmaxf(m[t], mt);
+        const float alpha = m_new == kNegInfP ? 1.f : fast_exp2(m[t] - m_new);
+        l[t] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float ar = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc[t][u][r] *= ar;
+        }
+        m[t] = m_new;
+      }
+      const float mm = m[t] == kNegInfP ? 0.f : m[t];
+      float p[2][4];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[ks][r] = fast_exp2(fmaf(sc[t][ks][r], cs, -mm));
+          l[t] += p[ks][r];
+        }
+      pop[t] = u32x4{pack2<T>(p[0][0], p[0][1]), pack2<T>(p[0][2], p[0][3]), pack2<T>(p[1][0], p[1][1]),
+                     pack2<T>(p[1][2], p[1][3])};
+    }
+
+    // P.V: B operand for dims 8c+u from the V rows of keys 4g+e / 16+4g+e-4.
+    u32x4 vrow[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = e < 4 ? 4 * g + e : 16 + 4 * g + e - 4;
+      vrow[e] = v_lane ? *reinterpret_cast<const u32x4*>(&vl[buf][key * ROW + 8 * c]) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int wd = u >> 1;
+      u32x4 bop;
+      if (u & 1) {
+        bop[0] = pack_hi(vrow[0][wd], vrow[1][wd]);
+        bop[1] = pack_hi(vrow[2][wd], vrow[3][wd]);
+        bop[2] = pack_hi(vrow[4][wd], vrow[5][wd]);
+        bop[3] = pack_hi(vrow[6][wd], vrow[7][wd]);
+      } else {
+        bop[0] = pack_lo(vrow[0][wd], vrow[1][wd]);
+        bop[1] = pack_lo(vrow[2][wd], vrow[3][wd]);
+        bop[2] = pack_lo(vrow[4][wd], vrow[5][wd]);
+        bop[3] = pack_lo(vrow[6][wd], vrow[7][wd]);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t][u] = mfma_k32<T>(pop[t], bop, acc[t][u]);  // O[query q0+4g+r][dim 8c+u]
+    }
+    }  // any_live
+
+    __builtin_amdgcn_sched_barrier(0);
+    swrite(buf ^ 1, st ^ 1);
+    lds_barrier();
+  };
+  if (nblk > 0) {
+    gload(0, 0);
+    gload(clampb(1), 1);
+    swrite(0, 0);
+    lds_barrier();
+    for (int blk = 0; blk < nblk; blk += 2) {
+      block_step(blk, std::integral_constant<int, 0>{});
+      if (blk + 1 < nblk) block_step(blk + 1, std::integral_constant<int, 1>{});
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (q0[t] >= q_len) continue;
+    float lt = l[t];
+    lt += __shfl_xor(lt, 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float lr = __shfl(lt, 4 * g + r, 64);
+      const int row = q0[t] + 4 * g + r;
+      if (row < q_len && v_lane) {
+        T* op = static_cast<T*>(a.out) + (q_start64 + row) * a.o_st + head[t] * a.o_sh + 8 * c;
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = pack2<T>(acc[t][2 * i][r] / lr, acc[t][2 * i + 1][r] / lr);
+        *reinterpret_cast<u32x4*>(op) = w;
+      }
+    }
+  }
+}
+
 // Generic path: one wave per (query row, q-head), fp32 VALU.
 template <typename T>
 __global__ __launch_bounds__(64) void varlen_prefill_generic(PrefillArgs a, int64_t total_q) {
@@ -274,11 +529,20 @@ static int launch_prefill(PrefillArgs& a, bool mfma, int64_t total_q, int64_t ma
     return check_launch("tsa_varlen_prefill");
   }
   if constexpr (sizeof(T) == 2) {
-    a.nqb = static_cast<int32_t>((max_seqlen_q + 31) / 32);
-    if (a.nqb == 0) return TSA_OK;
-    const dim3 grid(a.nqb, a.nseq, (a.Hq + 3) / 4);
-    if (a.D == 128) varlen_prefill_mfma<T, 128><<<grid, dim3(256), 0, stream>>>(a);
-    else varlen_prefill_mfma<T, 64><<<grid, dim3(256), 0, stream>>>(a);
+    if (a.G <= 16 && a.scale_log2 > 0.f) {
+      const int QB = 256 / a.G;
+      a.nqb = static_cast<int32_t>((max_seqlen_q + QB - 1) / QB);
+      if (a.nqb == 0) return TSA_OK;
+      const dim3 grid(static_cast<uint32_t>(a.nqb) * a.nseq * a.Hkv);
+      if (a.D == 128) varlen_prefill_lds<T, 128><<<grid, dim3(256), 0, stream>>>(a);
+      else varlen_prefill_lds<T, 64><<<grid, dim3(256), 0, stream>>>(a);
+    } else {
+      a.nqb = static_cast<int32_t>((max_seqlen_q + 31) / 32);
+      if (a.nqb == 0) return TSA_OK;
+      const dim3 grid(a.nqb, a.nseq, (a.Hq + 3) / 4);
+      if (a.D == 128) varlen_prefill_mfma<T, 128><<<grid, dim3(256), 0, stream>>>(a);
+      else varlen_prefill_mfma<T, 64><<<grid, dim3(256), 0, stream>>>(a);
+    }
   }
   return check_launch("tsa_varlen_prefill");
 }
