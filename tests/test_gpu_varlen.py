@@ -70,6 +70,19 @@ def test_matches_oracle(dtype, group, head_dim):
     assert_close(out, ref, what=f"{dtype} G={group} D={head_dim}", **_tol(dtype))
 
 
+@pytest.mark.parametrize("group,head_dim", [(2, 64), (3, 128), (16, 128), (32, 64)])
+def test_other_group_sizes(group, head_dim):
+    """Groups that divide 16 take the LDS-staged kernel; others the per-head kernel."""
+    lens = [17, 64, 200, 5]
+    q, k, v, cu, _ = _inputs(lens, lens, 2 * group, 2, head_dim, torch.bfloat16, seed=10 + group)
+    for causal in (True, False):
+        out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV), cu.to(DEV), max(lens), max(lens),
+                                     causal)
+        torch.cuda.synchronize()
+        ref = ov.flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), causal)
+        assert_close(out, ref, what=f"G={group} D={head_dim} causal={causal}")
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_q_len_differs_from_k_len(causal):
     lq, lk = [5, 40, 64], [9, 33, 100]

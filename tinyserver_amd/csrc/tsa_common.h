@@ -119,8 +119,17 @@ template <> __device__ __forceinline__ float lo_f<f16_t>(uint32_t w) {
 template <> __device__ __forceinline__ float hi_f<f16_t>(uint32_t w) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
 }
-template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return static_cast<uint32_t>(from_float<T>(a).x) | (static_cast<uint32_t>(from_float<T>(b).x) << 16);
+// Two floats rounded to nearest-even and packed (a in the low half): one
+// v_cvt_pk_{bf16,f16}_f32.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
 }
 
 // ------------------------------------------------------------ MFMA types --

@@ -201,30 +201,47 @@ __global__ __launch_bounds__(256) void varlen_prefill_mfma(PrefillArgs a) {
   }
 }
 
-// LDS-staged GQA flash attention. A workgroup owns one kv head of one
-// sequence and 256/G queries: its 4 waves each hold 4 row tiles of 16 rows,
-// a row being a (query, q-head) pair of the group, so all 16 row tiles read
-// the same K/V. 32-key K/V blocks are staged once per workgroup in
-// double-buffered, padded LDS (row stride D+8 elements: the 16 lanes of a
-// 128-bit read hit 16 distinct bank quads), the next block's global loads in
-// flight while the current one is on the matrix cores. Per block a wave reads
-// the K operands once, runs the 4 tiles' scores, then builds the P.V B
-// operands from the V rows once and runs the 4 tiles' P.V. Causal tiles whose
-// first query precedes the block are skipped. Workgroup ids put the kv head
-// fastest (so a kv head's query blocks share one XCD's L2) and the heaviest
-// query blocks first.
+// LDS-staged GQA flash attention, two waves per SIMD. A workgroup of 8 waves
+// owns one kv head of one sequence and 256/G queries (G = q heads per kv head,
+// a divisor of 16): each wave holds 2 row tiles of 16 rows, a row being a
+// (query, q-head) pair of the group, so all 16 row tiles read the same K/V.
+// 32-key K/V blocks are staged once per workgroup in double-buffered LDS, the
+// global loads of block i+2 in flight while block i is computed. Per block a
+// wave
+//   * reads its K operands (row-major K, row stride D+8 elements: the 16 lanes
+//     of a 128-bit read hit 16 distinct bank quads) and runs both tiles'
+//     S^T = K Q^T on v_mfma_f32_16x16x32;
+//   * turns the score accumulators into the P operand in registers (lane
+//     (g, c) holds query c's scores of keys 4g+r and 16+4g+r, which are the
+//     k-slots 8g..8g+7 of the P.V A operand);
+//   * builds each P.V B operand with two ds_read_b64_tr_b16: a 16-lane group
+//     whose lane 4e+q reads 4 dims (4q..4q+3) of key row e gets, in lane j,
+//     element e = V[key e][dim j] -- the transposed 4x16 patch -- so V stays
+//     row-major in LDS (row stride D+16: the 16 rows of one read fall in 8
+//     distinct 32-byte bank groups) and no wave repacks it.
+// Scores, probabilities and the output accumulators all stay in VGPRs (at most
+// 256 per wave), and the second wave on each SIMD fills the matrix pipe while
+// the first runs its softmax. Workgroup ids put the kv head fastest (a kv
+// head's query blocks share one XCD's L2) and the heaviest query blocks first.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void varlen_prefill_lds(PrefillArgs a) {
-  constexpr int KJ = D / 32;
-  constexpr int CPR = D / 8;            // 16-byte chunks per K/V row
-  constexpr int ROW = D + 8;            // padded LDS row, elements
-  constexpr int NCH = 32 * CPR / 256;   // chunks per thread per tensor per block
+__global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
+  constexpr int KJ = D / 32;              // 32-dim slices of the QK reduction
+  constexpr int NU = D / 16;              // 16-dim column tiles of the output
+  constexpr int CPR = D / 8;              // 16-byte chunks per K/V row
+  constexpr int ROWK = D + 8, ROWV = D + 16, ROWO = D + 8;  // LDS row strides, elements
+  constexpr int KCH = 32 * CPR;           // chunks per tensor per block
+  constexpr int NCH = 2 * KCH / 512;      // chunks per thread per block
+  constexpr int KBUF = 32 * ROWK, VBUF = 32 * ROWV;
+  static_assert(NCH >= 1 && 2 * KCH == 512 * NCH, "one K/V block is an exact number of chunks per thread");
+  static_assert(8 * 16 * ROWO <= 2 * (KBUF + VBUF), "output staging fits in the K/V buffers");
   // A row's running max only moves when it grows by more than this (log2
   // units): p = 2^(s - m) then stays below 2^8, and the accumulator is
   // rescaled rarely. l uses the same m, so the result is unchanged.
   constexpr float kRescale = 8.0f;
-  __shared__ __align__(16) uint16_t kl[2][32 * ROW];
-  __shared__ __align__(16) uint16_t vl[2][32 * ROW];
+  __shared__ __align__(16) uint16_t smem[2 * (KBUF + VBUF)];
+  uint16_t* const kl = smem;              // [2][32][ROWK]
+  uint16_t* const vl = smem + 2 * KBUF;   // [2][32][ROWV]
+
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.G, QB = 256 / G;
@@ -243,15 +260,14 @@ __global__ __launch_bounds__(256) void varlen_prefill_lds(PrefillArgs a) {
 
   const T* kb_ptr = static_cast<const T*>(a.k) + k_start64 * a.k_st + kvh * a.k_sh;
   const T* vb_ptr = static_cast<const T*>(a.v) + k_start64 * a.v_st + kvh * a.v_sh;
-  const bool v_lane = 8 * c < D;
   const float cs = a.scale_log2;  // > 0 on this path
 
-  // Row tiles of this wave: rt = 4 wave + t -> query subtile rt / G, head rt % G.
-  int q0[4], head[4];
-  u32x4 qop[4][KJ];
+  // Row tiles of this wave: rt = 2 wave + t -> query subtile rt / G, head rt % G.
+  int q0[2], head[2];
+  u32x4 qop[2][KJ];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int rt = 4 * wave + t;
+  for (int t = 0; t < 2; ++t) {
+    const int rt = 2 * wave + t;
     q0[t] = row0 + 16 * (rt / G);
     head[t] = kvh * G + rt % G;
     const int row = q0[t] + c;
@@ -261,92 +277,84 @@ __global__ __launch_bounds__(256) void varlen_prefill_lds(PrefillArgs a) {
       qop[t][j] = row < q_len ? *reinterpret_cast<const u32x4*>(qp + 8 * (g + 4 * j)) : u32x4{0, 0, 0, 0};
   }
 
-  float m[4], l[4];
-  f32x4 acc[4][8];
+  float m[2], l[2];
+  f32x4 acc[2][NU];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < 2; ++t) {
     m[t] = kNegInfP;
     l[t] = 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < NU; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   const int q_last = row0 + QB < q_len ? row0 + QB : q_len;  // one past the block's last query
   const int kend = a.causal ? (k_len < q_last ? k_len : q_last) : k_len;
   const int nblk = (kend + 31) / 32;
 
-  // Two register stages of global loads: block i+2 is in flight while block
-  // i is computed and block i+1 sits in LDS.
-  u32x4 kr[2][NCH], vr[2][NCH];
+  // Chunk i of this thread: K chunks first, then V; key-major, 16 bytes each.
+  // Loads are unconditional (keys past k_len read the sequence's last key, so
+  // no exec-masked load has to wait for a stage still in flight); those rows
+  // are zeroed when the stage is written to LDS.
+  u32x4 stg[2][NCH];
   auto gload = [&](int blk, int st) {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-      const int qc = tid + 256 * i;
-      const int key = qc / CPR, ch = qc % CPR;
-      const int kk = blk * 32 + key;
-      const bool ok = kk < k_len;
-      kr[st][i] = ok ? *reinterpret_cast<const u32x4*>(kb_ptr + static_cast<int64_t>(kk) * a.k_st + 8 * ch)
-                     : u32x4{0, 0, 0, 0};
-      vr[st][i] = ok ? *reinterpret_cast<const u32x4*>(vb_ptr + static_cast<int64_t>(kk) * a.v_st + 8 * ch)
-                     : u32x4{0, 0, 0, 0};
+      const int q = tid + 512 * i;
+      const bool isk = q < KCH;
+      const int qq = isk ? q : q - KCH;
+      const int key = qq / CPR, ch = qq % CPR;
+      const int kk = min(blk * 32 + key, k_len - 1);
+      const T* src = isk ? kb_ptr + static_cast<int64_t>(kk) * a.k_st : vb_ptr + static_cast<int64_t>(kk) * a.v_st;
+      stg[st][i] = *reinterpret_cast<const u32x4*>(src + 8 * ch);
     }
   };
-  auto swrite = [&](int buf, int st) {
+  auto swrite = [&](int buf, int st, int blk) {
+    const u32x4 zero = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-      const int qc = tid + 256 * i;
-      const int key = qc / CPR, ch = qc % CPR;
-      *reinterpret_cast<u32x4*>(&kl[buf][key * ROW + 8 * ch]) = kr[st][i];
-      *reinterpret_cast<u32x4*>(&vl[buf][key * ROW + 8 * ch]) = vr[st][i];
+      const int q = tid + 512 * i;
+      const bool isk = q < KCH;
+      const int qq = isk ? q : q - KCH;
+      const int key = qq / CPR, ch = qq % CPR;
+      const bool ok = blk * 32 + key < k_len;
+      uint16_t* dst = isk ? kl + buf * KBUF + key * ROWK + 8 * ch : vl + buf * VBUF + key * ROWV + 8 * ch;
+      *reinterpret_cast<u32x4*>(dst) = ok ? stg[st][i] : zero;
     }
   };
 
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  auto clampb = [&](int blk) { return blk < nblk ? blk : nblk - 1; };
   // Block blk computes from LDS buffer blk & 1 while block blk + 2's global
   // loads are in flight into register stage blk & 1 and block blk + 1 (stage
   // (blk + 1) & 1) is written to the other LDS buffer. The loop is unrolled by
-  // two so the stages are compile-time registers, and the loads are
-  // unconditional (the block index is clamped; a repeated block hits the
-  // cache) so each wait covers exactly the stage it needs.
-  auto clampb = [&](int blk) { return blk < nblk ? blk : nblk - 1; };
+  // two so the stages are compile-time registers.
   auto block_step = [&](int blk, auto stage) {
     constexpr int st = decltype(stage)::value;
-    const int buf = st;
     gload(clampb(blk + 2), st);
     __builtin_amdgcn_sched_barrier(0);
     const int kb0 = blk * 32;
+    const uint16_t* kbuf = kl + st * KBUF;
+    const uint16_t* vbuf = vl + st * VBUF;
 
-    // Skip the block only when none of the wave's tiles sees it (a single
-    // wave-uniform branch): per-tile branches around the MFMAs would force the
-    // accumulators through VGPR copies and serialise the matrix pipe. A tile
-    // that is dead for this block is masked to p = 0 instead.
-    bool any_live = false;
+    // S^T for both tiles: lane (g, c) gets query c's scores of keys 16ks+4g+r.
+    f32x4 sc[2][2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) any_live |= q0[t] < q_len && !(a.causal && kb0 > q0[t] + 15);
-    if (any_live) {
-    // K operands of the block: lane (g, c) holds key 16ks + c, dims 8(g+4j)..+8.
-    u32x4 kop[2][KJ];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4 kop[KJ];
 #pragma unroll
       for (int j = 0; j < KJ; ++j)
-        kop[ks][j] = *reinterpret_cast<const u32x4*>(&kl[buf][(16 * ks + c) * ROW + 8 * (g + 4 * j)]);
-
-    // Scores of all live tiles first, so the softmax VALU work of one tile
-    // overlaps the score MFMAs of the next.
-    f32x4 sc[4][2];
+        kop[j] = *reinterpret_cast<const u32x4*>(kbuf + (16 * ks + c) * ROWK + 8 * (g + 4 * j));
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+      for (int t = 0; t < 2; ++t) {
         sc[t][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < KJ; ++j) sc[t][ks] = mfma_k32<T>(kop[ks][j], qop[t][j], sc[t][ks]);
+        for (int j = 0; j < KJ; ++j) sc[t][ks] = mfma_k32<T>(kop[j], qop[t][j], sc[t][ks]);
       }
     }
 
-    u32x4 pop[4];
+    u32x4 pop[2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 2; ++t) {
       // Keys past k_len, and (causal) keys after the row's query, only occur in
       // a sequence's last block or on the diagonal: a wave-uniform branch.
       if (kb0 + 32 > k_len || (a.causal && kb0 + 31 > q0[t])) {
@@ -375,7 +383,7 @@ __global__ __launch_bounds__(256) void varlen_prefill_lds(PrefillArgs a) {
         for (int r = 0; r < 4; ++r) {
           const float ar = __shfl(alpha, 4 * g + r, 64);
 #pragma unroll
-          for (int u = 0; u < 8; ++u) acc[t][u][r] *= ar;
+          for (int u = 0; u < NU; ++u) acc[t][u][r] *= ar;
         }
         m[t] = m_new;
       }
@@ -392,41 +400,27 @@ __global__ __launch_bounds__(256) void varlen_prefill_lds(PrefillArgs a) {
                      pack2<T>(p[1][2], p[1][3])};
     }
 
-    // P.V: B operand for dims 8c+u from the V rows of keys 4g+e / 16+4g+e-4.
-    u32x4 vrow[8];
+    // P.V: the B operand of column tile u holds V[keys 4g+e and 16+4g+e][dims
+    // 16u + c], read transposed from the row-major LDS block.
+    const uint16_t* vt = vbuf + (4 * g + (c >> 2)) * ROWV + 4 * (c & 3);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int key = e < 4 ? 4 * g + e : 16 + 4 * g + e - 4;
-      vrow[e] = v_lane ? *reinterpret_cast<const u32x4*>(&vl[buf][key * ROW + 8 * c]) : u32x4{0, 0, 0, 0};
+    for (int u = 0; u < NU; ++u) {
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vt + 16 * u));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vt + 16 * ROWV + 16 * u));
+      const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+      const u32x4 bop = {lo2[0], lo2[1], hi2[0], hi2[1]};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[t][u] = mfma_k32<T>(pop[t], bop, acc[t][u]);  // O[query q0+4g+r][dim 16u+c]
     }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int wd = u >> 1;
-      u32x4 bop;
-      if (u & 1) {
-        bop[0] = pack_hi(vrow[0][wd], vrow[1][wd]);
-        bop[1] = pack_hi(vrow[2][wd], vrow[3][wd]);
-        bop[2] = pack_hi(vrow[4][wd], vrow[5][wd]);
-        bop[3] = pack_hi(vrow[6][wd], vrow[7][wd]);
-      } else {
-        bop[0] = pack_lo(vrow[0][wd], vrow[1][wd]);
-        bop[1] = pack_lo(vrow[2][wd], vrow[3][wd]);
-        bop[2] = pack_lo(vrow[4][wd], vrow[5][wd]);
-        bop[3] = pack_lo(vrow[6][wd], vrow[7][wd]);
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t][u] = mfma_k32<T>(pop[t], bop, acc[t][u]);  // O[query q0+4g+r][dim 8c+u]
-    }
-    }  // any_live
 
     __builtin_amdgcn_sched_barrier(0);
-    swrite(buf ^ 1, st ^ 1);
+    swrite(st ^ 1, st ^ 1, clampb(blk + 1));
     lds_barrier();
   };
   if (nblk > 0) {
     gload(0, 0);
     gload(clampb(1), 1);
-    swrite(0, 0);
+    swrite(0, 0, 0);
     lds_barrier();
     for (int blk = 0; blk < nblk; blk += 2) {
       block_step(blk, std::integral_constant<int, 0>{});
@@ -434,8 +428,12 @@ __global__ __launch_bounds__(256) void varlen_prefill_lds(PrefillArgs a) {
     }
   }
 
+  // Output: each wave stages its 16 x D tile in its own slice of the (now
+  // idle) K/V buffers and stores it as 16-byte row chunks. The loop ended on
+  // a workgroup barrier after every wave's last read of the K/V buffers.
+  uint16_t* ost = smem + wave * 16 * ROWO;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < 2; ++t) {
     if (q0[t] >= q_len) continue;
     float lt = l[t];
     lt += __shfl_xor(lt, 16, 64);
@@ -443,15 +441,26 @@ __global__ __launch_bounds__(256) void varlen_prefill_lds(PrefillArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float lr = __shfl(lt, 4 * g + r, 64);
-      const int row = q0[t] + 4 * g + r;
-      if (row < q_len && v_lane) {
-        T* op = static_cast<T*>(a.out) + (q_start64 + row) * a.o_st + head[t] * a.o_sh + 8 * c;
-        u32x4 w;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = pack2<T>(acc[t][2 * i][r] / lr, acc[t][2 * i + 1][r] / lr);
+      for (int u = 0; u < NU; ++u) ost[(4 * g + r) * ROWO + 16 * u + c] = from_float<T>(acc[t][u][r] / lr).x;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+    for (int i = 0; i < 16 * CPR / 64; ++i) {
+      const int chunk = lane + 64 * i;
+      const int r = chunk / CPR, ch = chunk % CPR;
+      const int row = q0[t] + r;
+      const u32x4 w = *reinterpret_cast<const u32x4*>(ost + r * ROWO + 8 * ch);
+      if (row < q_len) {
+        T* op = static_cast<T*>(a.out) + (q_start64 + row) * a.o_st + head[t] * a.o_sh + 8 * ch;
         *reinterpret_cast<u32x4*>(op) = w;
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
   }
 }
 
@@ -529,13 +538,13 @@ static int launch_prefill(PrefillArgs& a, bool mfma, int64_t total_q, int64_t ma
     return check_launch("tsa_varlen_prefill");
   }
   if constexpr (sizeof(T) == 2) {
-    if (a.G <= 16 && a.scale_log2 > 0.f) {
+    if (a.G <= 16 && 16 % a.G == 0 && a.scale_log2 > 0.f) {
       const int QB = 256 / a.G;
       a.nqb = static_cast<int32_t>((max_seqlen_q + QB - 1) / QB);
       if (a.nqb == 0) return TSA_OK;
       const dim3 grid(static_cast<uint32_t>(a.nqb) * a.nseq * a.Hkv);
-      if (a.D == 128) varlen_prefill_lds<T, 128><<<grid, dim3(256), 0, stream>>>(a);
-      else varlen_prefill_lds<T, 64><<<grid, dim3(256), 0, stream>>>(a);
+      if (a.D == 128) varlen_prefill_gqa<T, 128><<<grid, dim3(512), 0, stream>>>(a);
+      else varlen_prefill_gqa<T, 64><<<grid, dim3(512), 0, stream>>>(a);
     } else {
       a.nqb = static_cast<int32_t>((max_seqlen_q + 31) / 32);
       if (a.nqb == 0) return TSA_OK;
