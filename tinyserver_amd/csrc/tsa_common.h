@@ -161,6 +161,20 @@ template <> __device__ __forceinline__ f32x4 mfma_k16<f16_t>(u32x2 a, u32x2 b, f
   return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
 }
 
+// D(32x32 f32) += A(32x16) * B(16x32). Lane i supplies A[i%32][8(i/32)..+8]
+// and B[8(i/32)..+8][i%32]; lane i receives D[8(e/4) + 4(i/32) + e%4][i%32]
+// in element e. On gfx950 this form has about 1.6x the throughput of the
+// 16x16x32 one.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+template <typename T> __device__ __forceinline__ f32x16 mfma_k16x32(u32x4 a, u32x4 b, f32x16 c);
+template <> __device__ __forceinline__ f32x16 mfma_k16x32<bf16_t>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+                                                 0);
+}
+template <> __device__ __forceinline__ f32x16 mfma_k16x32<f16_t>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
 // Select 16-bit halves: result = (lo16 of a | lo16 of b << 16) or the high
 // halves, via v_perm_b32.
 __device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {

@@ -201,48 +201,52 @@ __global__ __launch_bounds__(256) void varlen_prefill_mfma(PrefillArgs a) {
   }
 }
 
-// LDS-staged GQA flash attention, two waves per SIMD. A workgroup of 8 waves
-// owns one kv head of one sequence and 256/G queries (G = q heads per kv head,
-// a divisor of 16): each wave holds 2 row tiles of 16 rows, a row being a
-// (query, q-head) pair of the group, so all 16 row tiles read the same K/V.
-// 32-key K/V blocks are staged once per workgroup in double-buffered LDS, the
-// global loads of block i+2 in flight while block i is computed. Per block a
-// wave
-//   * reads its K operands (row-major K, row stride D+8 elements: the 16 lanes
-//     of a 128-bit read hit 16 distinct bank quads) and runs both tiles'
-//     S^T = K Q^T on v_mfma_f32_16x16x32;
-//   * turns the score accumulators into the P operand in registers (lane
-//     (g, c) holds query c's scores of keys 4g+r and 16+4g+r, which are the
-//     k-slots 8g..8g+7 of the P.V A operand);
-//   * builds each P.V B operand with two ds_read_b64_tr_b16: a 16-lane group
-//     whose lane 4e+q reads 4 dims (4q..4q+3) of key row e gets, in lane j,
-//     element e = V[key e][dim j] -- the transposed 4x16 patch -- so V stays
-//     row-major in LDS (row stride D+16: the 16 rows of one read fall in 8
-//     distinct 32-byte bank groups) and no wave repacks it.
+// LDS-staged GQA flash attention on 32x32 tiles. A workgroup of 8 waves owns
+// one kv head of one sequence and 256/G queries (G = q heads per kv head, a
+// divisor of 8): wave w takes the 32 queries 32 (w / G).. of q-head w % G, so
+// all 8 tiles read the same K/V. 32-key K/V blocks are staged once per
+// workgroup in double-buffered LDS, the global loads of block i+2 in flight
+// while block i is computed. Both products run on v_mfma_f32_32x32x16 (the
+// 16x16x32 form has about 60% of its throughput on gfx950). With lane
+// (h, c) = (lane / 32, lane % 32) and accumulator element e holding row
+// 8(e/4) + 4h + e%4, column c:
+//   S^T(32 keys x 32 queries) = K Q^T over head_dim/16 steps: lane (h, c)
+//     reads key c, dims 16jj + 8h..+8 (row-major K, row stride D+8 elements:
+//     the 16 lanes of a 128-bit read hit 16 distinct bank quads) and holds
+//     query c's Q slice in registers; it gets query c's scores of keys
+//     8(e/4) + 4h + e%4;
+//   O(32 queries x 32 dims) += P V over two 16-key steps s: the P operand's
+//     k-slots 8h..8h+7 are keys 16s+4h+0..3 and 16s+8+4h+0..3, i.e. the score
+//     accumulators 8s..8s+7 of the same lane, so P goes to the operand in
+//     registers; the V operand comes from two ds_read_b64_tr_b16, in which a
+//     16-lane group whose lane 4e+q reads dims 4q..4q+3 of key row e gets, in
+//     lane j, element e = V[key e][dim j]. V stays row-major in LDS with row
+//     stride D+32 elements, so the two groups of a half-wave hit disjoint
+//     banks.
 // Scores, probabilities and the output accumulators all stay in VGPRs (at most
-// 256 per wave), and the second wave on each SIMD fills the matrix pipe while
-// the first runs its softmax. Workgroup ids put the kv head fastest (a kv
-// head's query blocks share one XCD's L2) and the heaviest query blocks first.
+// 256 per wave, two waves per SIMD). Workgroup ids put the kv head fastest (a
+// kv head's query blocks share one XCD's L2) and the heaviest query blocks
+// first.
 template <typename T, int D>
 __global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
-  constexpr int KJ = D / 32;              // 32-dim slices of the QK reduction
-  constexpr int NU = D / 16;              // 16-dim column tiles of the output
+  constexpr int KJ = D / 16;              // 16-dim steps of the QK reduction
+  constexpr int NU = D / 32;              // 32-dim column tiles of the output
   constexpr int CPR = D / 8;              // 16-byte chunks per K/V row
-  constexpr int ROWK = D + 8, ROWV = D + 16, ROWO = D + 8;  // LDS row strides, elements
+  constexpr int ROWK = D + 8, ROWV = D + 32, ROWO = D + 8;  // LDS row strides, elements
   constexpr int KCH = 32 * CPR;           // chunks per tensor per block
   constexpr int NCH = 2 * KCH / 512;      // chunks per thread per block
   constexpr int KBUF = 32 * ROWK, VBUF = 32 * ROWV;
   static_assert(NCH >= 1 && 2 * KCH == 512 * NCH, "one K/V block is an exact number of chunks per thread");
-  static_assert(8 * 16 * ROWO <= 2 * (KBUF + VBUF), "output staging fits in the K/V buffers");
+  constexpr int SMEM = 2 * (KBUF + VBUF) > 8 * 32 * ROWO ? 2 * (KBUF + VBUF) : 8 * 32 * ROWO;
   // A row's running max only moves when it grows by more than this (log2
   // units): p = 2^(s - m) then stays below 2^8, and the accumulator is
   // rescaled rarely. l uses the same m, so the result is unchanged.
   constexpr float kRescale = 8.0f;
-  __shared__ __align__(16) uint16_t smem[2 * (KBUF + VBUF)];
-  uint16_t* const kl = smem;              // [2][32][ROWK]
-  uint16_t* const vl = smem + 2 * KBUF;   // [2][32][ROWV]
+  __shared__ __align__(16) uint16_t smem[SMEM];  // K/V blocks, then the output tiles
+  uint16_t* const kl = smem;               // [2][32][ROWK]
+  uint16_t* const vl = smem + 2 * KBUF;    // [2][32][ROWV]
 
-  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.G, QB = 256 / G;
   const int id = blockIdx.x;
@@ -262,30 +266,24 @@ __global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
   const T* vb_ptr = static_cast<const T*>(a.v) + k_start64 * a.v_st + kvh * a.v_sh;
   const float cs = a.scale_log2;  // > 0 on this path
 
-  // Row tiles of this wave: rt = 2 wave + t -> query subtile rt / G, head rt % G.
-  int q0[2], head[2];
-  u32x4 qop[2][KJ];
+  // This wave's tile: queries q0..q0+31 of q-head `head`.
+  const int q0 = row0 + 32 * (wave / G);
+  const int head = kvh * G + wave % G;
+  u32x4 qop[KJ];
+  {
+    const int row = q0 + c;
+    const T* qp = static_cast<const T*>(a.q) + (q_start64 + row) * a.q_st + head * a.q_sh;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int rt = 2 * wave + t;
-    q0[t] = row0 + 16 * (rt / G);
-    head[t] = kvh * G + rt % G;
-    const int row = q0[t] + c;
-    const T* qp = static_cast<const T*>(a.q) + (q_start64 + row) * a.q_st + head[t] * a.q_sh;
-#pragma unroll
-    for (int j = 0; j < KJ; ++j)
-      qop[t][j] = row < q_len ? *reinterpret_cast<const u32x4*>(qp + 8 * (g + 4 * j)) : u32x4{0, 0, 0, 0};
+    for (int jj = 0; jj < KJ; ++jj)
+      qop[jj] = row < q_len ? *reinterpret_cast<const u32x4*>(qp + 16 * jj + 8 * h) : u32x4{0, 0, 0, 0};
   }
 
-  float m[2], l[2];
-  f32x4 acc[2][NU];
+  float m = kNegInfP, l = 0.f;  // query c's running max (log2 domain) and this lane's share of its sum
+  f32x16 acc[NU];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    m[t] = kNegInfP;
-    l[t] = 0.f;
+  for (int u = 0; u < NU; ++u)
 #pragma unroll
-    for (int u = 0; u < NU; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+    for (int e = 0; e < 16; ++e) acc[u][e] = 0.f;
 
   const int q_last = row0 + QB < q_len ? row0 + QB : q_len;  // one past the block's last query
   const int kend = a.causal ? (k_len < q_last ? k_len : q_last) : k_len;
@@ -336,82 +334,70 @@ __global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
     const uint16_t* kbuf = kl + st * KBUF;
     const uint16_t* vbuf = vl + st * VBUF;
 
-    // S^T for both tiles: lane (g, c) gets query c's scores of keys 16ks+4g+r.
-    f32x4 sc[2][2];
+    // S^T: lane (h, c) gets query c's scores of keys 8(e/4) + 4h + e%4.
+    f32x16 sc;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      u32x4 kop[KJ];
+    for (int e = 0; e < 16; ++e) sc[e] = 0.f;
 #pragma unroll
-      for (int j = 0; j < KJ; ++j)
-        kop[j] = *reinterpret_cast<const u32x4*>(kbuf + (16 * ks + c) * ROWK + 8 * (g + 4 * j));
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        sc[t][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < KJ; ++j) sc[t][ks] = mfma_k32<T>(kop[j], qop[t][j], sc[t][ks]);
-      }
+    for (int jj = 0; jj < KJ; ++jj) {
+      const u32x4 kop = *reinterpret_cast<const u32x4*>(kbuf + c * ROWK + 16 * jj + 8 * h);
+      sc = mfma_k16x32<T>(kop, qop[jj], sc);
     }
 
+    // Keys past k_len, and (causal) keys after the query, only occur in a
+    // sequence's last block or on the diagonal: a wave-uniform branch.
+    if (kb0 + 32 > k_len || (a.causal && kb0 + 31 > q0)) {
+      const int qq = q0 + c;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int kk = kb0 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (!(kk < k_len && (!a.causal || kk <= qq))) sc[e] = kNegInfP;
+      }
+    }
+    float tmax = kNegInfP;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mt = tmax * cs;
+    if (__any(mt > m + kRescale)) {
+      const float m_new = fmaxf(m, mt);
+      const float alpha = m_new == kNegInfP ? 1.f : fast_exp2(m - m_new);
+      l *= alpha;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float ar = __shfl(alpha, 8 * (e >> 2) + 4 * h + (e & 3), 64);
+#pragma unroll
+        for (int u = 0; u < NU; ++u) acc[u][e] *= ar;
+      }
+      m = m_new;
+    }
+    const float mm = m == kNegInfP ? 0.f : m;
+    float p[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      p[e] = fast_exp2(fmaf(sc[e], cs, -mm));
+      l += p[e];
+    }
     u32x4 pop[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      // Keys past k_len, and (causal) keys after the row's query, only occur in
-      // a sequence's last block or on the diagonal: a wave-uniform branch.
-      if (kb0 + 32 > k_len || (a.causal && kb0 + 31 > q0[t])) {
-        const int qq = q0[t] + c;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int kk = kb0 + 16 * ks + 4 * g + r;
-            if (!(kk < k_len && (!a.causal || kk <= qq))) sc[t][ks][r] = kNegInfP;
-          }
-      }
-      float tmax = kNegInfP;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[t][ks][r]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float mt = tmax * cs;
-      if (__any(mt > m[t] + kRescale)) {
-        const float m_new = fmaxf(m[t], mt);
-        const float alpha = m_new == kNegInfP ? 1.f : fast_exp2(m[t] - m_new);
-        l[t] *= alpha;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float ar = __shfl(alpha, 4 * g + r, 64);
-#pragma unroll
-          for (int u = 0; u < NU; ++u) acc[t][u][r] *= ar;
-        }
-        m[t] = m_new;
-      }
-      const float mm = m[t] == kNegInfP ? 0.f : m[t];
-      float p[2][4];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[ks][r] = fast_exp2(fmaf(sc[t][ks][r], cs, -mm));
-          l[t] += p[ks][r];
-        }
-      pop[t] = u32x4{pack2<T>(p[0][0], p[0][1]), pack2<T>(p[0][2], p[0][3]), pack2<T>(p[1][0], p[1][1]),
-                     pack2<T>(p[1][2], p[1][3])};
-    }
+    for (int s = 0; s < 2; ++s)
+      pop[s] = u32x4{pack2<T>(p[8 * s], p[8 * s + 1]), pack2<T>(p[8 * s + 2], p[8 * s + 3]),
+                     pack2<T>(p[8 * s + 4], p[8 * s + 5]), pack2<T>(p[8 * s + 6], p[8 * s + 7])};
 
-    // P.V: the B operand of column tile u holds V[keys 4g+e and 16+4g+e][dims
-    // 16u + c], read transposed from the row-major LDS block.
-    const uint16_t* vt = vbuf + (4 * g + (c >> 2)) * ROWV + 4 * (c & 3);
+    // P.V: B operand of step s, column tile u: V[keys 16s+4h+e, 16s+8+4h+e]
+    // [dims 32u + c], read transposed from the row-major LDS block.
+    const int jl = c & 15;
+    const uint16_t* vt = vbuf + (4 * h + (jl >> 2)) * ROWV + 16 * (c >> 4) + 4 * (jl & 3);
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vt + 16 * u));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vt + 16 * ROWV + 16 * u));
-      const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
-      const u32x4 bop = {lo2[0], lo2[1], hi2[0], hi2[1]};
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) acc[t][u] = mfma_k32<T>(pop[t], bop, acc[t][u]);  // O[query q0+4g+r][dim 16u+c]
-    }
+      for (int u = 0; u < NU; ++u) {
+        const uint16_t* base = vt + 16 * s * ROWV + 32 * u;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)base);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + 8 * ROWV));
+        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+        acc[u] = mfma_k16x32<T>(pop[s], u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}, acc[u]);
+      }
 
     __builtin_amdgcn_sched_barrier(0);
     swrite(st ^ 1, st ^ 1, clampb(blk + 1));
@@ -428,39 +414,32 @@ __global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
     }
   }
 
-  // Output: each wave stages its 16 x D tile in its own slice of the (now
+  // Output: each wave stages its 32 x D tile in its own slice of the (now
   // idle) K/V buffers and stores it as 16-byte row chunks. The loop ended on
   // a workgroup barrier after every wave's last read of the K/V buffers.
-  uint16_t* ost = smem + wave * 16 * ROWO;
+  if (q0 >= q_len) return;
+  uint16_t* ost = smem + wave * 32 * ROWO;
+  float lt = l + __shfl_xor(l, 32, 64);  // query c's denominator
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    if (q0[t] >= q_len) continue;
-    float lt = l[t];
-    lt += __shfl_xor(lt, 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
+  for (int e = 0; e < 16; ++e) {
+    const int r = 8 * (e >> 2) + 4 * h + (e & 3);
+    const float lr = __shfl(lt, r, 64);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float lr = __shfl(lt, 4 * g + r, 64);
+    for (int u = 0; u < NU; ++u) ost[r * ROWO + 32 * u + c] = from_float<T>(acc[u][e] / lr).x;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 #pragma unroll
-      for (int u = 0; u < NU; ++u) ost[(4 * g + r) * ROWO + 16 * u + c] = from_float<T>(acc[t][u][r] / lr).x;
+  for (int i = 0; i < 32 * CPR / 64; ++i) {
+    const int chunk = lane + 64 * i;
+    const int r = chunk / CPR, ch = chunk % CPR;
+    const int row = q0 + r;
+    const u32x4 w = *reinterpret_cast<const u32x4*>(ost + r * ROWO + 8 * ch);
+    if (row < q_len) {
+      T* op = static_cast<T*>(a.out) + (q_start64 + row) * a.o_st + head * a.o_sh + 8 * ch;
+      *reinterpret_cast<u32x4*>(op) = w;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-#pragma unroll
-    for (int i = 0; i < 16 * CPR / 64; ++i) {
-      const int chunk = lane + 64 * i;
-      const int r = chunk / CPR, ch = chunk % CPR;
-      const int row = q0[t] + r;
-      const u32x4 w = *reinterpret_cast<const u32x4*>(ost + r * ROWO + 8 * ch);
-      if (row < q_len) {
-        T* op = static_cast<T*>(a.out) + (q_start64 + row) * a.o_st + head[t] * a.o_sh + 8 * ch;
-        *reinterpret_cast<u32x4*>(op) = w;
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
   }
 }
 
@@ -538,7 +517,7 @@ static int launch_prefill(PrefillArgs& a, bool mfma, int64_t total_q, int64_t ma
     return check_launch("tsa_varlen_prefill");
   }
   if constexpr (sizeof(T) == 2) {
-    if (a.G <= 16 && 16 % a.G == 0 && a.scale_log2 > 0.f) {
+    if (a.G <= 8 && 8 % a.G == 0 && a.scale_log2 > 0.f) {
       const int QB = 256 / a.G;
       a.nqb = static_cast<int32_t>((max_seqlen_q + QB - 1) / QB);
       if (a.nqb == 0) return TSA_OK;
