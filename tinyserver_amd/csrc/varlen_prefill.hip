@@ -5,23 +5,17 @@
 // top-left causal mask q_idx >= k_idx within the sequence (:116-119),
 // P cast to the V dtype before P.V (:126), l summing the fp32 P (:128-129).
 //
-// Here a workgroup of 4 waves takes one 32-row query block of one sequence for
-// 4 consecutive q-heads (one head per wave; with GQA the waves of a group read
-// the same K/V, so the second to fourth reads hit the L1/L2). Both products
-// run on v_mfma_f32_16x16x32_{bf16,f16}:
-//   S^T(16 keys x 16 queries) = K Q^T   -- lane (g, c) loads key c, dims
-//                                           8(g+4j)..+8: one 128-bit load
-//   O(16 queries x 16 dims)  += P V     -- k-slot 8g+e of lane (g, c) is key
-//                                           4g+e (e < 4) or 16+4g+e-4, which
-//                                           is where the S^T accumulators
-//                                           already hold query c's scores.
-// So P goes from the score accumulators to the P.V operand in registers, and
-// V rows are read row-major (16 lanes per 256-byte row) and regrouped with
-// v_perm_b32. Causal blocks past the query block are never visited, and the
+// Three kernels, chosen per call:
+//   varlen_prefill_gqa   bf16/f16, head_dim 64/128, GQA group a divisor of 8:
+//                        one workgroup per (kv head, sequence, query block),
+//                        K/V staged in LDS once for the whole group, 32x32x16
+//                        MFMA tiles (the main path);
+//   varlen_prefill_mfma  other group sizes: 4 q-heads per workgroup, operands
+//                        straight from global memory, 16x16x32 MFMA tiles;
+//   varlen_prefill_generic  fp32, other head_dims or non-unit innermost
+//                        strides: one wave per (query, q-head), fp32 VALU.
+// Causal key blocks past a workgroup's last query are never visited, and the
 // heaviest query blocks are dispatched first.
-//
-// A generic kernel (one wave per (query, q-head), fp32 VALU) covers fp32 and
-// head_dims other than 64/128 and non-unit innermost strides.
 #include <cmath>
 #include <type_traits>
 
@@ -338,11 +332,15 @@ __global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
     f32x16 sc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) sc[e] = 0.f;
+    // All K operand reads are issued before the first MFMA, so the LDS latency
+    // is paid once per block rather than once per step.
+    u32x4 kop[KJ];
 #pragma unroll
-    for (int jj = 0; jj < KJ; ++jj) {
-      const u32x4 kop = *reinterpret_cast<const u32x4*>(kbuf + c * ROWK + 16 * jj + 8 * h);
-      sc = mfma_k16x32<T>(kop, qop[jj], sc);
-    }
+    for (int jj = 0; jj < KJ; ++jj) kop[jj] = *reinterpret_cast<const u32x4*>(kbuf + c * ROWK + 16 * jj + 8 * h);
+#pragma unroll
+    for (int jj = 0; jj < KJ; ++jj) sc = mfma_k16x32<T>(kop[jj], qop[jj], sc);
+    __builtin_amdgcn_sched_group_barrier(0x100, KJ, 0);  // the K operand reads
+    __builtin_amdgcn_sched_group_barrier(0x008, KJ, 0);  // then the score MFMAs
 
     // Keys past k_len, and (causal) keys after the query, only occur in a
     // sequence's last block or on the diagonal: a wave-uniform branch.
