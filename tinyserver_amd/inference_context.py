@@ -1,0 +1,48 @@
+"""Per-step inference context read by the patched attention forward.
+
+Mirrors server/model/inference_context.py:18-48: ``InferenceContext{mode,
+sequences}`` with ``sequences[i] = {"num_tokens": int, "block_table":
+list[int]}`` in the order of the flattened batch, a module-global current
+context, and ``inference_context(ctx)`` to swap it for the duration of a
+forward. As in the reference the global is unsynchronised: one engine thread
+drives the forward and the swap.
+
+A context also carries the device-side metadata (padded block tables,
+cu_seqlens, positions) built by the first patched layer of a forward and
+reused by the others (``device_metadata``), so the host work and the
+host-to-device copy happen once per step rather than once per layer and per
+sequence.
+"""
+
+from __future__ import annotations
+
+from contextlib import contextmanager
+from dataclasses import dataclass, field
+from typing import Any, Iterator
+
+
+@dataclass
+class InferenceContext:
+    mode: str = "prefill"
+    sequences: list[dict[str, Any]] = field(default_factory=list)
+    # (position_ids, key, metadata) of the last device-metadata build
+    _device_meta: Any = field(default=None, repr=False, compare=False)
+
+
+_current = InferenceContext()
+
+
+def get_inference_context() -> InferenceContext:
+    """The context of the forward in progress."""
+    return _current
+
+
+@contextmanager
+def inference_context(ctx: InferenceContext) -> Iterator[InferenceContext]:
+    """Make ``ctx`` current inside the block; restore the previous one after."""
+    global _current
+    previous, _current = _current, ctx
+    try:
+        yield ctx
+    finally:
+        _current = previous
