@@ -121,7 +121,8 @@ def test_norm_rope_validation():
 
 def test_workspace_plan():
     lib = _lib.load()
-    # Two partial slots of (acc[G][D], m[G], l[G]) per workgroup.
+    # One partial slot of (acc[G][D], m[G], l[G]) per (unit, wave worker) pair
+    # that can occur -- units + 4 * workgroups -- plus the tile prefix.
     n = lib.tsa_paged_decode_workspace_bytes(2, 8, 2, 128, 64, 16, 10)
-    assert n >= 10 * 2 * 4 * (128 + 2) * 4
+    assert n >= (2 * 2 + 4 * 10) * 4 * (128 + 2) * 4 + 3 * 4
     assert lib.tsa_paged_decode_workspace_bytes(0, 8, 2, 128, 64, 16, 10) == 0

@@ -7,14 +7,17 @@
 //
 // * Work is the list of 16-token tiles of every (sequence, kv head) "unit",
 //   unit-major. A fixed grid of workgroups (by default two per CU, all
-//   resident at once) splits that list into equal contiguous shares, so every
-//   workgroup streams the same number of K/V bytes whatever the mix of
-//   context lengths, and the whole call is a single wave of workgroups.
-//   Every K/V byte is read once and shared by the G = Hq/Hkv query heads of
-//   its kv head. Each workgroup derives the tile prefix over seq_lens itself
-//   (a block scan in LDS), so nothing is precomputed on the host.
-// * Within a unit's segment the 4 waves of a workgroup take its tiles
-//   round-robin.
+//   resident at once) gives each of its waves -- a "wave worker" -- one equal,
+//   contiguous run of that list, so every wave streams the same number of K/V
+//   bytes whatever the mix of context lengths, and the whole call is a single
+//   wave of workgroups. Every K/V byte is read once and shared by the G =
+//   Hq/Hkv query heads of its kv head. Each workgroup derives the tile prefix
+//   over seq_lens itself (a block scan in LDS), so nothing is precomputed on
+//   the host.
+// * A wave crosses unit boundaries without stopping: its ring keeps loading
+//   the next unit's tiles (and that unit's Q) while the current unit
+//   finishes, and at a unit's end it writes its partial (m, l, acc) and starts
+//   afresh. No workgroup barrier follows the prefix scan.
 // * Scores on the matrix cores: S^T(16 tok x 16 head) = K(16 tok x D) Q^T with
 //   v_mfma_f32_16x16x32_{bf16,f16}. The K operand wants token = lane%16 and 8
 //   consecutive dims per lane, which is a plain 128-bit global load (lane
@@ -34,13 +37,11 @@
 //   dtype to feed the MFMA (the reference's P.V is fp32); l sums the fp32 p.
 // * Each wave keeps a ring of RING tiles in registers: the loads of the next
 //   RING-1 tiles are in flight while one is on the matrix cores. Loads are
-//   unconditional (the tile index is clamped to the wave's last tile, whose
-//   repeat hits the cache) so the compiler waits for exactly one tile.
-// * A unit wholly inside one workgroup's share is finished there. Only the
-//   first and last unit of a share can be cut; their (m, l, acc) partials go
-//   to two workspace slots per workgroup and a small second kernel merges
-//   them with a log-sum-exp reduce. The kernel boundary orders the two, so no
-//   cache flushes or atomics are needed; no host sync, no memset.
+//   unconditional (past its last tile a wave reloads that tile, which hits
+//   the cache) so the compiler waits for exactly one tile.
+// * A second kernel merges, per unit, the partials of the wave workers whose
+//   runs cover it with a log-sum-exp reduce. The kernel boundary orders the
+//   two, so no cache flushes or atomics are needed; no host sync, no memset.
 //
 // Tokens past seq_len are scored -inf and their V rows zeroed (the
 // reference's masked loads, :88-105). seq_len is clamped to the block table's
@@ -71,12 +72,11 @@ struct DecodeArgs {
   int64_t bt_s0, bt_s1, sl_s;
   int64_t NB;
   int32_t B, Hq, Hkv, G, BS, max_blocks, D;
-  int32_t W;        // workgroups sharing the tile list
+  int32_t W;        // workgroups of the stream kernel
+  int32_t NW;       // wave workers sharing the tile list (kWaves * W)
   float scale_log2;
-  float* part_o;    // [W][2][G][D]   unnormalised acc of a cut unit
-  float* part_ml;   // [W][2][G][2]   its running max (log2 domain) and sum
-  int64_t* cut;     // [W][4]         unit cut at workgroup w's first tile:
-                    //                {start tile P or -1, tiles n, unit, share}
+  float* part;      // [B * Hkv + NW][G * (D + 2)]: per (unit, worker) acc[G][D], m[G], l[G]
+  int32_t* pref_out;  // [B + 1] tile prefix over the sequences, for the merge
 };
 
 constexpr int kWaves = 4;
@@ -134,319 +134,300 @@ __device__ void tile_prefix(const DecodeArgs& a, int* pref, int* tmp) {
   __syncthreads();
 }
 
+// Position of one wave in the global tile list (unit-major): unit (s, kvh),
+// tile t of the unit's n tiles. Wave-uniform; empty sequences are skipped.
+struct TileCursor {
+  int s, kvh, n, t;
+  // Values read from the LDS prefix go through readfirstlane, so the compiler
+  // keeps the cursor (and the block-table addresses built from it) in SGPRs.
+  __device__ __forceinline__ void next_unit(const int* pref, int B, int Hkv) {
+    if (++kvh == Hkv) {
+      kvh = 0;
+      int nn = 0;
+      while (nn == 0 && ++s < B) nn = __builtin_amdgcn_readfirstlane(pref[s + 1] - pref[s]);
+      s = __builtin_amdgcn_readfirstlane(s);
+    }
+    n = s < B ? __builtin_amdgcn_readfirstlane(pref[s + 1] - pref[s]) : 0;
+    t = 0;
+  }
+  __device__ __forceinline__ void advance(const int* pref, int B, int Hkv) {
+    if (++t == n) next_unit(pref, B, Hkv);
+  }
+};
+
+// Wave worker v = 4 * workgroup + wave streams the contiguous tiles
+// [v * share, (v + 1) * share) of the global list, crossing unit boundaries
+// without stopping: its ring of RING tiles (K operand, V rows and the unit's
+// Q operand, all loaded together) keeps prefetching into the next unit while
+// the current one finishes. At the end of each of its units the wave writes
+// its partial (m, l, acc) to workspace slot unit + v (injective, since a
+// worker's units form a range that starts where the previous worker's ended)
+// and starts afresh; nothing waits for the other waves. The merge kernel
+// combines every unit's partials.
+// The block table, seq_lens and the partial buffer come in again as
+// __restrict__ parameters: with the partial stores inside the loop, that is
+// what lets the compiler read block-table entries and lengths with scalar
+// loads.
 template <typename T, int D, bool PAGE16, bool CONTIG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TSA_DECODE_WAVES_PER_EU)))
-void paged_decode_stream(DecodeArgs a) {
+void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ sl,
+                         float* __restrict__ part) {
   constexpr int KJ = D / 32;  // k-steps of the score MFMA
-  extern __shared__ float lds[];
+  a.bt = bt;
+  a.seq_lens = sl;
+  a.part = part;
+  extern __shared__ int lds_i[];
   const int G = a.G, Hkv = a.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
   // Wave-uniform (scalar) so tile indices, block-table reads and page bases
   // stay in SGPRs and the table lookups are scalar loads.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int w = blockIdx.x;
-
-  float* s_o = lds;                          // [kWaves][G][D]
-  float* s_m = s_o + kWaves * G * D;         // [kWaves][G]
-  float* s_l = s_m + kWaves * G;             // [kWaves][G]
-  int* pref = reinterpret_cast<int*>(s_l + kWaves * G);  // [B + 1]
-  int* tmp = pref + a.B + 1;                 // [256]
+  int* pref = lds_i;             // [B + 1]
+  int* tmp = pref + a.B + 1;     // [256]
   tile_prefix(a, pref, tmp);
+  if (blockIdx.x == 0)
+    for (int i = tid; i <= a.B; i += 256) a.pref_out[i] = pref[i];
 
   const int64_t total = static_cast<int64_t>(Hkv) * pref[a.B];
-  const int64_t share = (total + a.W - 1) / a.W;
-  const int64_t lo = w * share;
+  const int64_t share = (total + a.NW - 1) / a.NW;
+  const int v = blockIdx.x * kWaves + wave;
+  const int64_t lo = static_cast<int64_t>(v) * share;
   const int64_t hi = min(total, lo + share);
-  if (w == 0) {  // empty sequences: 0/0 like the reference
-    for (int sq = 0; sq < a.B; ++sq) {
-      if (pref[sq + 1] != pref[sq]) continue;
-      for (int idx = tid; idx < a.Hq * D; idx += 256) {
-        T* op = static_cast<T*>(a.out) + sq * a.o_ss + (idx / D) * a.o_sh + (idx % D) * a.o_sd;
-        *op = from_float<T>(NAN);
-      }
-    }
-  }
-  if (lo >= hi) {
-    if (tid == 0) a.cut[w * 4] = -1;
-    return;
-  }
+  if (lo >= hi) return;  // no barrier follows: waves leave independently
+  const int n_tiles = static_cast<int>(hi - lo);
 
-  // First unit: the last sequence with Hkv * pref[s] <= lo (that skips empty
-  // sequences), then the kv head inside it.
-  int s;
+  // Locate tile lo: the last sequence with Hkv * pref[s] <= lo (that skips
+  // empty sequences), then the kv head and the tile inside it.
+  TileCursor cur;
   {
     int l0 = 0, h0 = a.B;  // answer in [l0, h0)
     while (h0 - l0 > 1) {
       const int mid = (l0 + h0) >> 1;
       if (static_cast<int64_t>(Hkv) * pref[mid] <= lo) l0 = mid; else h0 = mid;
     }
-    s = l0;
+    cur.s = __builtin_amdgcn_readfirstlane(l0);
+    cur.n = __builtin_amdgcn_readfirstlane(pref[cur.s + 1] - pref[cur.s]);
+    const int64_t off = lo - static_cast<int64_t>(Hkv) * __builtin_amdgcn_readfirstlane(pref[cur.s]);
+    cur.kvh = __builtin_amdgcn_readfirstlane(static_cast<int>(off / cur.n));
+    cur.t = __builtin_amdgcn_readfirstlane(static_cast<int>(off - static_cast<int64_t>(cur.kvh) * cur.n));
   }
-  int kvh = static_cast<int>((lo - static_cast<int64_t>(Hkv) * pref[s]) / (pref[s + 1] - pref[s]));
   const bool v_lane = 8 * c < D;
-  if (tid == 0) {  // tell the merge kernel whether a unit is cut at this share's start
-    const int n0 = pref[s + 1] - pref[s];
-    const int64_t P0 = static_cast<int64_t>(Hkv) * pref[s] + static_cast<int64_t>(kvh) * n0;
-    int64_t* rec = a.cut + w * 4;
-    rec[0] = P0 < lo ? P0 : -1;
-    rec[1] = n0;
-    rec[2] = static_cast<int64_t>(s) * Hkv + kvh;
-    rec[3] = share;
-  }
+  const int cq = c % G;  // lanes past the group load a real head; their rows are never stored
+  // Slot strides: the contiguous pool layout makes them the compile-time D.
+  const int64_t ks = CONTIG ? D : a.kc_s;
+  const int64_t vs = CONTIG ? D : a.vc_s;
 
-  for (bool first_unit = true;; first_unit = false) {
-    const int n_s = pref[s + 1] - pref[s];
-    const int64_t P = static_cast<int64_t>(Hkv) * pref[s] + static_cast<int64_t>(kvh) * n_s;
-    if (P >= hi) break;
-    const int t_begin = static_cast<int>(max(lo, P) - P);
-    const int t_end = static_cast<int>(min(hi, P + n_s) - P);
-    const bool whole = t_begin == 0 && t_end == n_s;
-    const int64_t L = clamp_len(a, s);
+  auto page_of = [&](const int32_t* bt_row, int64_t tok, int64_t& phys, int64_t& slot) -> bool {
+    const int64_t lb = tok / a.BS;
+    phys = bt_row[lb * a.bt_s1];
+    slot = tok - lb * a.BS;
+    return phys >= 0 && phys < a.NB;
+  };
 
-    // Q^T operand: lane (g, c) holds head c, dims 8(g + 4j)..+8 for k-step j.
-    u32x4 qop[KJ];
-    {
-      const T* qrow = static_cast<const T*>(a.q) + s * a.q_ss + (kvh * G + c) * a.q_sh;
+  // One tile's operands: Q^T (lane (g, c): head c, dims 8(g + 4j)..+8), the K
+  // operand (token c of the tile, same dims) and V rows (tokens 4g..4g+3).
+  // With 16-token pages the loads are unconditional (an invalid page id reads
+  // page 0 and the tile is masked in compute), so nothing waits on the data
+  // until it is consumed.
+  auto load_tile = [&](const TileCursor& tc, u32x4 (&qo)[KJ], u32x4 (&ko)[KJ], u32x4 (&vo)[4]) {
+    const int32_t* bt_row = a.bt + tc.s * a.bt_s0;
+    const T* qrow = static_cast<const T*>(a.q) + tc.s * a.q_ss + (tc.kvh * G + cq) * a.q_sh + 8 * g;
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) qo[j] = *reinterpret_cast<const u32x4*>(qrow + 32 * j);
+    const T* kbase = static_cast<const T*>(a.kc) + tc.kvh * a.kc_h;
+    const T* vbase = static_cast<const T*>(a.vc) + tc.kvh * a.vc_h;
+    const int64_t tok0 = static_cast<int64_t>(tc.t) * 16;
+    if constexpr (PAGE16) {
+      int64_t phys, slot0;
+      if (!page_of(bt_row, tok0, phys, slot0)) phys = 0;
+      const T* kp = kbase + phys * a.kc_b + (slot0 + c) * ks + 8 * g;
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) ko[j] = *reinterpret_cast<const u32x4*>(kp + 32 * j);
+      const T* vp = vbase + phys * a.vc_b + (slot0 + 4 * g) * vs + (v_lane ? 8 * c : 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vo[r] = *reinterpret_cast<const u32x4*>(vp + r * vs);
+    } else {
+      const int64_t L = clamp_len(a, tc.s);
+      int64_t phys, slot;
+      const int64_t tk = tok0 + c;
+      const bool okk = tk < L && page_of(bt_row, tk, phys, slot);
+      const T* kp = kbase + (okk ? phys * a.kc_b + slot * ks : 0);
 #pragma unroll
       for (int j = 0; j < KJ; ++j)
-        qop[j] = c < G ? *reinterpret_cast<const u32x4*>(qrow + 8 * (g + 4 * j)) : u32x4{0, 0, 0, 0};
+        ko[j] = okk ? *reinterpret_cast<const u32x4*>(kp + 8 * (g + 4 * j)) : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t tv = tok0 + 4 * g + r;
+        const bool okv = v_lane && tv < L && page_of(bt_row, tv, phys, slot);
+        vo[r] = okv ? *reinterpret_cast<const u32x4*>(vbase + phys * a.vc_b + slot * vs + 8 * c)
+                    : u32x4{0, 0, 0, 0};
+      }
     }
+  };
 
-    const int32_t* bt_row = a.bt + s * a.bt_s0;
-    const T* kbase = static_cast<const T*>(a.kc) + kvh * a.kc_h;
-    const T* vbase = static_cast<const T*>(a.vc) + kvh * a.vc_h;
-    // Slot strides: the contiguous pool layout makes them the compile-time D.
-    const int64_t ks = CONTIG ? D : a.kc_s;
-    const int64_t vs = CONTIG ? D : a.vc_s;
-
-    auto page_of = [&](int64_t tok, int64_t& phys, int64_t& slot) -> bool {
-      const int64_t lb = tok / a.BS;
-      phys = bt_row[lb * a.bt_s1];
-      slot = tok - lb * a.BS;
-      return phys >= 0 && phys < a.NB;
-    };
-
-    // K operand (token c of the tile) and V rows (tokens 4g..4g+3) of one
-    // tile. With 16-token pages the whole tile is one page: the loads are
-    // unconditional (an invalid page id reads page 0 and the tile is masked in
-    // compute_tile), so nothing waits on the data until it is consumed.
-    auto load_tile = [&](int t, u32x4 (&ko)[KJ], u32x4 (&vo)[4]) {
-      const int64_t tok0 = static_cast<int64_t>(t) * 16;
-      if constexpr (PAGE16) {
-        int64_t phys, slot0;
-        if (!page_of(tok0, phys, slot0)) phys = 0;
-        const T* kp = kbase + phys * a.kc_b + (slot0 + c) * ks + 8 * g;
+  float m = kNegInf;  // running max of head c (log2 domain), same in all 4 row-groups
+  float l = 0.f;      // this lane's share of head c's softmax denominator
+  f32x4 acc[8];
 #pragma unroll
-        for (int j = 0; j < KJ; ++j) ko[j] = *reinterpret_cast<const u32x4*>(kp + 32 * j);
-        const T* vp = vbase + phys * a.vc_b + (slot0 + 4 * g) * vs + (v_lane ? 8 * c : 0);
+  for (int u = 0; u < 8; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute_tile = [&](const TileCursor& tc, const u32x4 (&qo)[KJ], const u32x4 (&ko)[KJ], u32x4 (&vo)[4]) {
+    const int64_t tok0 = static_cast<int64_t>(tc.t) * 16;
+    // Tokens past seq_len, and (page-16 path) tiles whose block id is out of
+    // range, are masked: score -inf and V rows zeroed so 0 * (inf/nan) cannot
+    // leak into the accumulator. Only the last tile of a sequence (or a bad
+    // page) takes this wave-uniform branch.
+    int64_t lim = tc.t + 1 < tc.n ? tok0 + 16 : clamp_len(a, tc.s);
+    if constexpr (PAGE16) {
+      int64_t phys, slot0;
+      if (!page_of(a.bt + tc.s * a.bt_s0, tok0, phys, slot0)) lim = tok0;
+    }
+    if (tok0 + 16 > lim) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vo[r] = *reinterpret_cast<const u32x4*>(vp + r * vs);
+      for (int r = 0; r < 4; ++r)
+        if (tok0 + 4 * g + r >= lim) vo[r] = u32x4{0, 0, 0, 0};
+    }
+    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) sc = mfma_k32<T>(ko[j], qo[j], sc);
+    // sc[r] = q_c . k_{tok0 + 4g + r}
+    const int64_t tb = tok0 + 4 * g;
+    float sv[4];
+    float tmax = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sv[r] = tb + r < lim ? sc[r] * a.scale_log2 : kNegInf;
+      tmax = fmaxf(tmax, sv[r]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m, tmax);
+    if (__any(m_new > m)) {
+      const float alpha = m_new == kNegInf ? 1.f : fast_exp2(m - m_new);  // 0 on the first tile
+      l *= alpha;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * g + r, 64);  // alpha of head 4g + r
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u][r] *= ar;
+      }
+      m = m_new;
+    }
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = m == kNegInf ? 0.f : fast_exp2(sv[r] - m);
+      l += p[r];
+    }
+    const u32x2 pop = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int wd = u >> 1;
+      u32x2 bop;
+      if (u & 1) {
+        bop[0] = pack_hi(vo[0][wd], vo[1][wd]);
+        bop[1] = pack_hi(vo[2][wd], vo[3][wd]);
       } else {
-        int64_t phys, slot;
-        const int64_t tk = tok0 + c;
-        const bool okk = tk < L && page_of(tk, phys, slot);
-        const T* kp = kbase + (okk ? phys * a.kc_b + slot * ks : 0);
-#pragma unroll
-        for (int j = 0; j < KJ; ++j)
-          ko[j] = okk ? *reinterpret_cast<const u32x4*>(kp + 8 * (g + 4 * j)) : u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t tv = tok0 + 4 * g + r;
-          const bool okv = v_lane && tv < L && page_of(tv, phys, slot);
-          vo[r] = okv ? *reinterpret_cast<const u32x4*>(vbase + phys * a.vc_b + slot * vs + 8 * c)
-                      : u32x4{0, 0, 0, 0};
-        }
+        bop[0] = pack_lo(vo[0][wd], vo[1][wd]);
+        bop[1] = pack_lo(vo[2][wd], vo[3][wd]);
       }
-    };
-
-    float m = kNegInf;  // running max of head c (log2 domain), same in all 4 row-groups
-    float l = 0.f;      // this lane's share of head c's softmax denominator
-    f32x4 acc[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    auto compute_tile = [&](int t, const u32x4 (&ko)[KJ], u32x4 (&vo)[4]) {
-      const int64_t tok0 = static_cast<int64_t>(t) * 16;
-      // Tokens past seq_len, and (page-16 path) tiles whose block id is out of
-      // range, are masked: score -inf and V rows zeroed so 0 * (inf/nan) cannot
-      // leak into the accumulator. Only the last tile of a sequence (or a bad
-      // page) takes this wave-uniform branch.
-      int64_t lim = L;
-      if constexpr (PAGE16) {
-        int64_t phys, slot0;
-        if (!page_of(tok0, phys, slot0)) lim = tok0;
-      }
-      if (tok0 + 16 > lim) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (tok0 + 4 * g + r >= lim) vo[r] = u32x4{0, 0, 0, 0};
-      }
-      f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < KJ; ++j) sc = mfma_k32<T>(ko[j], qop[j], sc);
-      // sc[r] = q_c . k_{tok0 + 4g + r}
-      const int64_t tb = tok0 + 4 * g;
-      float sv[4];
-      float tmax = kNegInf;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sv[r] = tb + r < lim ? sc[r] * a.scale_log2 : kNegInf;
-        tmax = fmaxf(tmax, sv[r]);
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m, tmax);
-      if (__any(m_new > m)) {
-        const float alpha = m_new == kNegInf ? 1.f : fast_exp2(m - m_new);  // 0 on the first tile
-        l *= alpha;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float ar = __shfl(alpha, 4 * g + r, 64);  // alpha of head 4g + r
-#pragma unroll
-          for (int u = 0; u < 8; ++u) acc[u][r] *= ar;
-        }
-        m = m_new;
-      }
-      float p[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[r] = m == kNegInf ? 0.f : fast_exp2(sv[r] - m);
-        l += p[r];
-      }
-      const u32x2 pop = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int wd = u >> 1;
-        u32x2 bop;
-        if (u & 1) {
-          bop[0] = pack_hi(vo[0][wd], vo[1][wd]);
-          bop[1] = pack_hi(vo[2][wd], vo[3][wd]);
-        } else {
-          bop[0] = pack_lo(vo[0][wd], vo[1][wd]);
-          bop[1] = pack_lo(vo[2][wd], vo[3][wd]);
-        }
-        acc[u] = mfma_k16<T>(pop, bop, acc[u]);  // acc[u][r] = O[head 4g + r][dim 8c + u]
-      }
-    };
-
-    // Ring of RING tile buffers over this wave's tiles t_begin + wave + 4i,
-    // i < nw. The scheduling barriers keep every buffer's loads in ring order
-    // on all paths, so a compute waits for its own tile only.
-    const int first = t_begin + wave;
-    const int nw = first < t_end ? (t_end - first + kWaves - 1) / kWaves : 0;
-    if (nw > 0) {
-      auto tile = [&](int i) { return first + kWaves * min(i, nw - 1); };
-      u32x4 kbuf[RING][KJ], vbuf[RING][4];
-#pragma unroll
-      for (int d = 0; d < RING; ++d) {
-        load_tile(tile(d), kbuf[d], vbuf[d]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      for (int i = 0; i < nw; i += RING) {
-#pragma unroll
-        for (int d = 0; d < RING; ++d) {
-          if (i + d < nw) compute_tile(tile(i + d), kbuf[d], vbuf[d]);
-          __builtin_amdgcn_sched_barrier(0);
-          load_tile(tile(i + d + RING), kbuf[d], vbuf[d]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
+      acc[u] = mfma_k16<T>(pop, bop, acc[u]);  // acc[u][r] = O[head 4g + r][dim 8c + u]
     }
+  };
 
-    // Head c's denominator: sum the four row-groups.
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-
-    // Merge the waves through LDS.
+  // This wave's partial of unit (s, kvh) to slot unit + v: acc[G][D], then
+  // m[G], l[G]; then a fresh state for the next unit.
+  const int64_t slot_floats = static_cast<int64_t>(G) * (D + 2);
+  auto flush = [&](const TileCursor& tc) {
+    float lt = l;
+    lt += __shfl_xor(lt, 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+    float* slot = a.part + (static_cast<int64_t>(tc.s) * Hkv + tc.kvh + v) * slot_floats;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int hd = 4 * g + r;
       if (hd < G && v_lane) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) s_o[(wave * G + hd) * D + 8 * c + u] = acc[u][r];
+        float* dst = slot + hd * D + 8 * c;
+        *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
       }
     }
     if (g == 0 && c < G) {
-      s_m[wave * G + c] = m;
-      s_l[wave * G + c] = l;
+      slot[G * D + c] = m;
+      slot[G * D + G + c] = lt;
     }
-    __syncthreads();
-    const int slot = first_unit ? 0 : 1;
-    for (int idx = tid; idx < G * D; idx += 256) {
-      const int hd = idx / D, d = idx - hd * D;
-      float M = kNegInf;
+    m = kNegInf;
+    l = 0.f;
 #pragma unroll
-      for (int wv = 0; wv < kWaves; ++wv) M = fmaxf(M, s_m[wv * G + hd]);
-      float o = 0.f, den = 0.f;
-#pragma unroll
-      for (int wv = 0; wv < kWaves; ++wv) {
-        const float mw = s_m[wv * G + hd];
-        const float e = mw == kNegInf ? 0.f : fast_exp2(mw - M);
-        o += e * s_o[(wv * G + hd) * D + d];
-        den += e * s_l[wv * G + hd];
-      }
-      if (whole) {
-        T* op = static_cast<T*>(a.out) + s * a.o_ss + (kvh * G + hd) * a.o_sh + d * a.o_sd;
-        *op = from_float<T>(o / den);
-      } else {
-        const int64_t sl = (static_cast<int64_t>(w) * 2 + slot) * G + hd;
-        a.part_o[sl * D + d] = o;
-        if (d == 0) {
-          a.part_ml[sl * 2] = M;
-          a.part_ml[sl * 2 + 1] = den;
-        }
-      }
-    }
-    __syncthreads();  // the LDS is reused by the next unit
+    for (int u = 0; u < 8; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
 
-    // Next unit: next kv head, then the next non-empty sequence.
-    if (++kvh == Hkv) {
-      kvh = 0;
-      do {
-        ++s;
-      } while (s < a.B && pref[s + 1] == pref[s]);
-      if (s >= a.B) break;
+  // Ring of RING tile buffers; the load cursor runs RING tiles ahead of the
+  // compute cursor and stops on the wave's last tile (repeats hit the cache),
+  // so every load is unconditional and each compute waits for its own tile.
+  TileCursor ld = cur;
+  int ld_left = n_tiles - 1;  // advances the load cursor may still make
+  auto advance_load = [&]() {
+    if (ld_left > 0) {
+      ld.advance(pref, a.B, Hkv);
+      --ld_left;
+    }
+  };
+  u32x4 qbuf[RING][KJ], kbuf[RING][KJ], vbuf[RING][4];
+#pragma unroll
+  for (int d = 0; d < RING; ++d) {
+    load_tile(ld, qbuf[d], kbuf[d], vbuf[d]);
+    advance_load();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int i = 0; i < n_tiles; i += RING) {
+#pragma unroll
+    for (int d = 0; d < RING; ++d) {
+      if (i + d < n_tiles) {
+        compute_tile(cur, qbuf[d], kbuf[d], vbuf[d]);
+        if (cur.t + 1 == cur.n || i + d + 1 == n_tiles) flush(cur);
+        cur.advance(pref, a.B, Hkv);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      load_tile(ld, qbuf[d], kbuf[d], vbuf[d]);
+      advance_load();
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
 
-// Finish the units that were cut between workgroups: out = sum_w 2^(m_w - M)
-// acc_w / sum_w 2^(m_w - M) l_w over the contributing workgroups' slots.
-// Merge workgroup w reads the cut record of stream workgroup w; the unit is
-// merged by the first boundary inside it (w == w0 + 1, w0 the workgroup whose
-// share it starts in), every other workgroup returns at once. The unit is
-// w0's last unit (slot 1) unless it starts exactly at w0's share (slot 0);
-// in every later workgroup it is the first unit (slot 0).
+// out[s, kvh * G + hd] = sum_v 2^(m_v - M) acc_v / sum_v 2^(m_v - M) l_v over
+// the wave workers v whose tiles cover unit (s, kvh); an empty sequence gives
+// 0/0 = NaN, as the reference's does. One workgroup per unit.
 template <typename T>
 __global__ __launch_bounds__(256) void paged_decode_stream_merge(DecodeArgs a) {
-  const int w = blockIdx.x, tid = threadIdx.x;
-  const int64_t* rec = a.cut + w * 4;
-  const int64_t P = rec[0];
-  if (P < 0) return;
-  const int64_t n = rec[1], share = rec[3];
-  const int w0 = static_cast<int>(P / share);
-  if (w != w0 + 1) return;
-  const int w1 = static_cast<int>((P + n - 1) / share);
-  const int u = static_cast<int>(rec[2]);
-  const int s = u / a.Hkv, kvh = u - s * a.Hkv;
-  const int G = a.G, D = a.D;
+  const int u = blockIdx.x, tid = threadIdx.x;
+  const int Hkv = a.Hkv, G = a.G, D = a.D;
+  const int s = u / Hkv, kvh = u - s * Hkv;
+  const int p0 = a.pref_out[s], n = a.pref_out[s + 1] - p0;
+  const int64_t total = static_cast<int64_t>(Hkv) * a.pref_out[a.B];
   T* orow = static_cast<T*>(a.out) + s * a.o_ss + (kvh * G) * a.o_sh;
-  const int slot0 = P == static_cast<int64_t>(w0) * share ? 0 : 1;
+  if (n == 0) {
+    for (int idx = tid; idx < G * D; idx += 256)
+      orow[(idx / D) * a.o_sh + (idx % D) * a.o_sd] = from_float<T>(NAN);
+    return;
+  }
+  const int64_t share = (total + a.NW - 1) / a.NW;
+  const int64_t P = static_cast<int64_t>(Hkv) * p0 + static_cast<int64_t>(kvh) * n;
+  const int v0 = static_cast<int>(P / share), v1 = static_cast<int>((P + n - 1) / share);
+  const int64_t slot_floats = static_cast<int64_t>(G) * (D + 2);
+  const float* base = a.part + static_cast<int64_t>(u) * slot_floats;  // slot u + v = base + v * slot_floats
   for (int idx = tid; idx < G * D; idx += 256) {
     const int hd = idx / D, d = idx - hd * D;
     float M = kNegInf;
-    for (int v = w0; v <= w1; ++v) {
-      const int slot = v == w0 ? slot0 : 0;
-      M = fmaxf(M, a.part_ml[((static_cast<int64_t>(v) * 2 + slot) * G + hd) * 2]);
-    }
+    for (int v = v0; v <= v1; ++v) M = fmaxf(M, base[v * slot_floats + G * D + hd]);
     float o = 0.f, den = 0.f;
-    for (int v = w0; v <= w1; ++v) {
-      const int slot = v == w0 ? slot0 : 0;
-      const int64_t sl = (static_cast<int64_t>(v) * 2 + slot) * G + hd;
-      const float mw = a.part_ml[sl * 2];
+    for (int v = v0; v <= v1; ++v) {
+      const float* sl = base + v * slot_floats;
+      const float mw = sl[G * D + hd];
       const float e = mw == kNegInf ? 0.f : fast_exp2(mw - M);
-      o += e * a.part_o[sl * D + d];
-      den += e * a.part_ml[sl * 2 + 1];
+      o += e * sl[hd * D + d];
+      den += e * sl[G * D + G + hd];
     }
     orow[hd * a.o_sh + d * a.o_sd] = from_float<T>(o / den);
   }
@@ -532,17 +513,19 @@ static int default_workgroups() {
 
 struct DecodePlan {
   int W;
-  size_t part_o_bytes, part_ml_bytes, cut_bytes, total;
+  size_t part_bytes, pref_bytes, total;
 };
 
-static DecodePlan make_plan(int64_t Hq, int64_t Hkv, int64_t D, int32_t num_workgroups) {
+// Workspace: one partial slot per (unit, wave worker) pair that can occur --
+// units * 1 + workers, since slot = unit + worker -- and the tile prefix.
+static DecodePlan make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int32_t num_workgroups) {
   DecodePlan p{};
   p.W = num_workgroups > 0 ? num_workgroups : default_workgroups();
   const int64_t G = Hq / Hkv;
-  p.part_o_bytes = align256(static_cast<size_t>(p.W) * 2 * G * D * sizeof(float));
-  p.part_ml_bytes = align256(static_cast<size_t>(p.W) * 2 * G * 2 * sizeof(float));
-  p.cut_bytes = align256(static_cast<size_t>(p.W) * 4 * sizeof(int64_t));
-  p.total = p.part_o_bytes + p.part_ml_bytes + p.cut_bytes;
+  const int64_t slots = B * Hkv + static_cast<int64_t>(kWaves) * p.W;
+  p.part_bytes = align256(static_cast<size_t>(slots) * G * (D + 2) * sizeof(float));
+  p.pref_bytes = align256(static_cast<size_t>(B + 1) * sizeof(int32_t));
+  p.total = p.part_bytes + p.pref_bytes;
   return p;
 }
 
@@ -554,13 +537,12 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream) {
     return check_launch("tsa_paged_decode");
   }
   if constexpr (sizeof(T) == 2) {
-    const size_t prefix_lds = static_cast<size_t>(a.B + 1 + 256) * sizeof(int);
-    const size_t lds = static_cast<size_t>(kWaves) * a.G * (a.D + 2) * sizeof(float) + prefix_lds;
+    const size_t lds = static_cast<size_t>(a.B + 1 + 256) * sizeof(int);
     const bool page16 = a.BS % 16 == 0;
     const bool contig = a.kc_s == a.D && a.vc_s == a.D;
     const dim3 grid(a.W);
 #define TSA_DECODE_LAUNCH(DD, P16, CT) \
-  paged_decode_stream<T, DD, P16, CT><<<grid, dim3(256), lds, stream>>>(a)
+  paged_decode_stream<T, DD, P16, CT><<<grid, dim3(256), lds, stream>>>(a, a.bt, a.seq_lens, a.part)
     if (a.D == 128) {
       if (page16 && contig) TSA_DECODE_LAUNCH(128, true, true);
       else if (page16) TSA_DECODE_LAUNCH(128, true, false);
@@ -572,7 +554,7 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream) {
     }
 #undef TSA_DECODE_LAUNCH
     if (int rc = check_launch("tsa_paged_decode")) return rc;
-    paged_decode_stream_merge<T><<<dim3(a.W), dim3(256), 0, stream>>>(a);
+    paged_decode_stream_merge<T><<<dim3(a.B * a.Hkv), dim3(256), 0, stream>>>(a);
   }
   return check_launch("tsa_paged_decode");
 }
@@ -587,7 +569,7 @@ extern "C" size_t tsa_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num
   (void)max_blocks_per_seq;
   (void)block_size;
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || num_heads % num_kv_heads) return 0;
-  return make_plan(num_heads, num_kv_heads, head_dim, num_workgroups).total;
+  return make_plan(num_seqs, num_heads, num_kv_heads, head_dim, num_workgroups).total;
 }
 
 extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache,
@@ -638,15 +620,15 @@ extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, cons
   const bool mfma = (dt == TSA_BF16 || dt == TSA_F16) && (D == 64 || D == 128) && a.G <= 16 &&
                     rows_vec16(query) && rows_vec16(k_cache) && rows_vec16(v_cache) && out->stride[2] == 1;
   if (mfma) {
-    const DecodePlan plan = make_plan(Hq, Hkv, D, num_workgroups);
+    const DecodePlan plan = make_plan(B, Hq, Hkv, D, num_workgroups);
     a.W = plan.W;
+    a.NW = kWaves * plan.W;
     TSA_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total,
                 "workspace of %zu bytes is too small: %zu needed", workspace_bytes, plan.total);
     TSA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
     char* ws = static_cast<char*>(workspace);
-    a.part_o = reinterpret_cast<float*>(ws);
-    a.part_ml = reinterpret_cast<float*>(ws + plan.part_o_bytes);
-    a.cut = reinterpret_cast<int64_t*>(ws + plan.part_o_bytes + plan.part_ml_bytes);
+    a.part = reinterpret_cast<float*>(ws);
+    a.pref_out = reinterpret_cast<int32_t*>(ws + plan.part_bytes);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dt) {
