@@ -79,7 +79,16 @@ struct DecodeArgs {
   int32_t* pref_out;  // [B + 1] tile prefix over the sequences, for the merge
 };
 
-constexpr int kWaves = 4;
+// Waves per stream-kernel workgroup, and workgroups per CU of the default
+// grid (kWaves * kWgPerCu waves per CU in all).
+#ifndef TSA_DECODE_WAVES
+#define TSA_DECODE_WAVES 4
+#endif
+#ifndef TSA_DECODE_WG_PER_CU
+#define TSA_DECODE_WG_PER_CU 1
+#endif
+constexpr int kWaves = TSA_DECODE_WAVES;
+constexpr int kThreads = 64 * kWaves;
 constexpr float kNegInf = -INFINITY;
 
 // Minimum waves per SIMD the stream kernel is compiled for (register budget:
@@ -104,10 +113,10 @@ __device__ __forceinline__ int tiles_of(const DecodeArgs& a, int s) {
 }
 
 // Exclusive prefix of tiles per sequence into pref[0..B] (pref[B] = total),
-// computed by the whole 256-thread workgroup; tmp holds 256 ints of scratch.
+// computed by the whole workgroup; tmp holds kThreads ints of scratch.
 __device__ void tile_prefix(const DecodeArgs& a, int* pref, int* tmp) {
   const int tid = threadIdx.x;
-  const int per = (a.B + 255) / 256;
+  const int per = (a.B + kThreads - 1) / kThreads;
   int local = 0;
   for (int i = 0; i < per; ++i) {
     const int s = tid * per + i;
@@ -119,7 +128,7 @@ __device__ void tile_prefix(const DecodeArgs& a, int* pref, int* tmp) {
   }
   tmp[tid] = local;
   __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {  // inclusive Hillis-Steele scan
+  for (int off = 1; off < kThreads; off <<= 1) {  // inclusive Hillis-Steele scan
     const int v = tid >= off ? tmp[tid - off] : 0;
     __syncthreads();
     tmp[tid] += v;
@@ -130,7 +139,7 @@ __device__ void tile_prefix(const DecodeArgs& a, int* pref, int* tmp) {
     const int s = tid * per + i;
     if (s < a.B) pref[s] += base;
   }
-  if (tid == 255) pref[a.B] = tmp[255];
+  if (tid == kThreads - 1) pref[a.B] = tmp[kThreads - 1];
   __syncthreads();
 }
 
@@ -169,7 +178,7 @@ struct TileCursor {
 // what lets the compiler read block-table entries and lengths with scalar
 // loads.
 template <typename T, int D, bool PAGE16, bool CONTIG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TSA_DECODE_WAVES_PER_EU)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TSA_DECODE_WAVES_PER_EU)))
 void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ sl,
                          float* __restrict__ part) {
   constexpr int KJ = D / 32;  // k-steps of the score MFMA
@@ -183,10 +192,10 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   // stay in SGPRs and the table lookups are scalar loads.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int* pref = lds_i;             // [B + 1]
-  int* tmp = pref + a.B + 1;     // [256]
+  int* tmp = pref + a.B + 1;     // [kThreads]
   tile_prefix(a, pref, tmp);
   if (blockIdx.x == 0)
-    for (int i = tid; i <= a.B; i += 256) a.pref_out[i] = pref[i];
+    for (int i = tid; i <= a.B; i += kThreads) a.pref_out[i] = pref[i];
 
   const int64_t total = static_cast<int64_t>(Hkv) * pref[a.B];
   const int64_t share = (total + a.NW - 1) / a.NW;
@@ -398,17 +407,23 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
 
 // out[s, kvh * G + hd] = sum_v 2^(m_v - M) acc_v / sum_v 2^(m_v - M) l_v over
 // the wave workers v whose tiles cover unit (s, kvh); an empty sequence gives
-// 0/0 = NaN, as the reference's does. One workgroup per unit.
-template <typename T>
+// 0/0 = NaN, as the reference's does. One workgroup per unit, one thread per
+// (head, dim) output (head_dim * G <= 2048 outputs over 256 threads). The
+// contributors are combined with an online log-sum-exp in batches of 8 whose
+// loads are all issued before any is used, so a unit costs a few memory
+// round trips however many waves covered it.
+template <typename T, int kOut>  // kOut: outputs per thread, G * head_dim / 256 rounded up
 __global__ __launch_bounds__(256) void paged_decode_stream_merge(DecodeArgs a) {
+  constexpr int kBatch = 8;  // contributors per batch
   const int u = blockIdx.x, tid = threadIdx.x;
   const int Hkv = a.Hkv, G = a.G, D = a.D;
   const int s = u / Hkv, kvh = u - s * Hkv;
   const int p0 = a.pref_out[s], n = a.pref_out[s + 1] - p0;
   const int64_t total = static_cast<int64_t>(Hkv) * a.pref_out[a.B];
   T* orow = static_cast<T*>(a.out) + s * a.o_ss + (kvh * G) * a.o_sh;
+  const int nout = G * D;
   if (n == 0) {
-    for (int idx = tid; idx < G * D; idx += 256)
+    for (int idx = tid; idx < nout; idx += 256)
       orow[(idx / D) * a.o_sh + (idx % D) * a.o_sd] = from_float<T>(NAN);
     return;
   }
@@ -417,19 +432,45 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(DecodeArgs a) {
   const int v0 = static_cast<int>(P / share), v1 = static_cast<int>((P + n - 1) / share);
   const int64_t slot_floats = static_cast<int64_t>(G) * (D + 2);
   const float* base = a.part + static_cast<int64_t>(u) * slot_floats;  // slot u + v = base + v * slot_floats
-  for (int idx = tid; idx < G * D; idx += 256) {
-    const int hd = idx / D, d = idx - hd * D;
-    float M = kNegInf;
-    for (int v = v0; v <= v1; ++v) M = fmaxf(M, base[v * slot_floats + G * D + hd]);
-    float o = 0.f, den = 0.f;
-    for (int v = v0; v <= v1; ++v) {
-      const float* sl = base + v * slot_floats;
-      const float mw = sl[G * D + hd];
-      const float e = mw == kNegInf ? 0.f : fast_exp2(mw - M);
-      o += e * sl[hd * D + d];
-      den += e * sl[G * D + G + hd];
+  int hd[kOut];
+  float M[kOut], den[kOut], o[kOut];
+#pragma unroll
+  for (int i = 0; i < kOut; ++i) {
+    const int idx = min(tid + 256 * i, nout - 1);  // spare threads repeat the last output
+    hd[i] = idx / D;
+    M[i] = kNegInf;
+    den[i] = 0.f;
+    o[i] = 0.f;
+  }
+  for (int v = v0; v <= v1; v += kBatch) {
+    float mb[kBatch][kOut], lb[kBatch][kOut], ab[kBatch][kOut];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const float* sl = base + static_cast<int64_t>(min(v + k, v1)) * slot_floats;
+#pragma unroll
+      for (int i = 0; i < kOut; ++i) {
+        const int idx = min(tid + 256 * i, nout - 1);
+        mb[k][i] = v + k <= v1 ? sl[G * D + hd[i]] : kNegInf;
+        lb[k][i] = sl[G * D + G + hd[i]];
+        ab[k][i] = sl[idx];
+      }
     }
-    orow[hd * a.o_sh + d * a.o_sd] = from_float<T>(o / den);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+#pragma unroll
+      for (int i = 0; i < kOut; ++i) {
+        const float mn = fmaxf(M[i], mb[k][i]);
+        if (mn == kNegInf) continue;
+        const float c_old = fast_exp2(M[i] - mn), c_new = fast_exp2(mb[k][i] - mn);
+        o[i] = o[i] * c_old + ab[k][i] * c_new;
+        den[i] = den[i] * c_old + lb[k][i] * c_new;
+        M[i] = mn;
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < kOut; ++i) {
+    const int idx = tid + 256 * i;
+    if (idx < nout) orow[hd[i] * a.o_sh + (idx % D) * a.o_sd] = from_float<T>(o[i] / den[i]);
   }
 }
 
@@ -508,7 +549,7 @@ static int default_workgroups() {
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
-  return 2 * cus;
+  return TSA_DECODE_WG_PER_CU * cus;
 }
 
 struct DecodePlan {
@@ -537,12 +578,12 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream) {
     return check_launch("tsa_paged_decode");
   }
   if constexpr (sizeof(T) == 2) {
-    const size_t lds = static_cast<size_t>(a.B + 1 + 256) * sizeof(int);
+    const size_t lds = static_cast<size_t>(a.B + 1 + kThreads) * sizeof(int);
     const bool page16 = a.BS % 16 == 0;
     const bool contig = a.kc_s == a.D && a.vc_s == a.D;
     const dim3 grid(a.W);
 #define TSA_DECODE_LAUNCH(DD, P16, CT) \
-  paged_decode_stream<T, DD, P16, CT><<<grid, dim3(256), lds, stream>>>(a, a.bt, a.seq_lens, a.part)
+  paged_decode_stream<T, DD, P16, CT><<<grid, dim3(kThreads), lds, stream>>>(a, a.bt, a.seq_lens, a.part)
     if (a.D == 128) {
       if (page16 && contig) TSA_DECODE_LAUNCH(128, true, true);
       else if (page16) TSA_DECODE_LAUNCH(128, true, false);
@@ -554,7 +595,12 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream) {
     }
 #undef TSA_DECODE_LAUNCH
     if (int rc = check_launch("tsa_paged_decode")) return rc;
-    paged_decode_stream_merge<T><<<dim3(a.B * a.Hkv), dim3(256), 0, stream>>>(a);
+    const dim3 mgrid(a.B * a.Hkv);
+    const int outs = (a.G * a.D + 255) / 256;
+    if (outs <= 1) paged_decode_stream_merge<T, 1><<<mgrid, dim3(256), 0, stream>>>(a);
+    else if (outs <= 2) paged_decode_stream_merge<T, 2><<<mgrid, dim3(256), 0, stream>>>(a);
+    else if (outs <= 4) paged_decode_stream_merge<T, 4><<<mgrid, dim3(256), 0, stream>>>(a);
+    else paged_decode_stream_merge<T, 8><<<mgrid, dim3(256), 0, stream>>>(a);
   }
   return check_launch("tsa_paged_decode");
 }
