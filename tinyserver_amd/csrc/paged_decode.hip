@@ -113,34 +113,35 @@ __device__ __forceinline__ int tiles_of(const DecodeArgs& a, int s) {
 }
 
 // Exclusive prefix of tiles per sequence into pref[0..B] (pref[B] = total),
-// computed by the whole workgroup; tmp holds kThreads ints of scratch.
-__device__ void tile_prefix(const DecodeArgs& a, int* pref, int* tmp) {
-  const int tid = threadIdx.x;
-  const int per = (a.B + kThreads - 1) / kThreads;
+// computed by one wave alone into its own LDS copy: lane i sums sequences
+// [i * per, (i + 1) * per), a shuffle scan combines the lanes, and no
+// workgroup barrier is needed. Only this wave reads pref afterwards.
+__device__ void tile_prefix_wave(const DecodeArgs& a, int* pref) {
+  const int lane = threadIdx.x & 63;
+  const int per = (a.B + 63) / 64;
   int local = 0;
   for (int i = 0; i < per; ++i) {
-    const int s = tid * per + i;
+    const int s = lane * per + i;
+    if (s < a.B) local += tiles_of(a, s);
+  }
+  int incl = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int up = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += up;
+  }
+  int run = incl - local;  // exclusive prefix of this lane's first sequence
+  for (int i = 0; i < per; ++i) {
+    const int s = lane * per + i;
     if (s < a.B) {
-      const int n = tiles_of(a, s);
-      pref[s] = local;
-      local += n;
+      pref[s] = run;
+      run += tiles_of(a, s);
     }
   }
-  tmp[tid] = local;
-  __syncthreads();
-  for (int off = 1; off < kThreads; off <<= 1) {  // inclusive Hillis-Steele scan
-    const int v = tid >= off ? tmp[tid - off] : 0;
-    __syncthreads();
-    tmp[tid] += v;
-    __syncthreads();
-  }
-  const int base = tid > 0 ? tmp[tid - 1] : 0;
-  for (int i = 0; i < per; ++i) {
-    const int s = tid * per + i;
-    if (s < a.B) pref[s] += base;
-  }
-  if (tid == kThreads - 1) pref[a.B] = tmp[kThreads - 1];
-  __syncthreads();
+  if (lane == 63) pref[a.B] = incl;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
 // Position of one wave in the global tile list (unit-major): unit (s, kvh),
@@ -191,11 +192,10 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   // Wave-uniform (scalar) so tile indices, block-table reads and page bases
   // stay in SGPRs and the table lookups are scalar loads.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  int* pref = lds_i;             // [B + 1]
-  int* tmp = pref + a.B + 1;     // [kThreads]
-  tile_prefix(a, pref, tmp);
-  if (blockIdx.x == 0)
-    for (int i = tid; i <= a.B; i += kThreads) a.pref_out[i] = pref[i];
+  int* pref = lds_i + wave * (a.B + 1);  // this wave's copy, [B + 1]
+  tile_prefix_wave(a, pref);
+  if (blockIdx.x == 0 && wave == 0)
+    for (int i = lane; i <= a.B; i += 64) a.pref_out[i] = pref[i];
 
   const int64_t total = static_cast<int64_t>(Hkv) * pref[a.B];
   const int64_t share = (total + a.NW - 1) / a.NW;
@@ -578,7 +578,7 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream) {
     return check_launch("tsa_paged_decode");
   }
   if constexpr (sizeof(T) == 2) {
-    const size_t lds = static_cast<size_t>(a.B + 1 + kThreads) * sizeof(int);
+    const size_t lds = static_cast<size_t>(kWaves) * (a.B + 1) * sizeof(int);
     const bool page16 = a.BS % 16 == 0;
     const bool contig = a.kc_s == a.D && a.vc_s == a.D;
     const dim3 grid(a.W);
@@ -663,7 +663,9 @@ extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, cons
   a.max_blocks = static_cast<int32_t>(block_tables->size[1]); a.D = static_cast<int32_t>(D);
   a.scale_log2 = static_cast<float>(softmax_scale * 1.4426950408889634);
 
+  // The MFMA path keeps a per-wave tile prefix of B + 1 ints in LDS.
   const bool mfma = (dt == TSA_BF16 || dt == TSA_F16) && (D == 64 || D == 128) && a.G <= 16 &&
+                    static_cast<int64_t>(kWaves) * (B + 1) * 4 <= 64 * 1024 &&
                     rows_vec16(query) && rows_vec16(k_cache) && rows_vec16(v_cache) && out->stride[2] == 1;
   if (mfma) {
     const DecodePlan plan = make_plan(B, Hq, Hkv, D, num_workgroups);
