@@ -195,10 +195,10 @@ __global__ __launch_bounds__(256) void varlen_prefill_mfma(PrefillArgs a) {
   }
 }
 
-// LDS-staged GQA flash attention on 32x32 tiles. A workgroup of 8 waves owns
-// one kv head of one sequence and 256/G queries (G = q heads per kv head, a
-// divisor of 8): wave w takes the 32 queries 32 (w / G).. of q-head w % G, so
-// all 8 tiles read the same K/V. 32-key K/V blocks are staged once per
+// LDS-staged GQA flash attention on 32x32 tiles. A workgroup of NW waves (4
+// or 8) owns one kv head of one sequence and 32 NW/G queries (G = q heads per
+// kv head, a divisor of NW): wave w takes the 32 queries 32 (w / G).. of
+// q-head w % G, so all NW tiles read the same K/V. 32-key K/V blocks are staged once per
 // workgroup in double-buffered LDS, the global loads of block i+2 in flight
 // while block i is computed. Both products run on v_mfma_f32_32x32x16 (the
 // 16x16x32 form has about 60% of its throughput on gfx950). With lane
@@ -218,20 +218,23 @@ __global__ __launch_bounds__(256) void varlen_prefill_mfma(PrefillArgs a) {
 //     stride D+32 elements, so the two groups of a half-wave hit disjoint
 //     banks.
 // Scores, probabilities and the output accumulators all stay in VGPRs (at most
-// 256 per wave, two waves per SIMD). Workgroup ids put the kv head fastest (a
-// kv head's query blocks share one XCD's L2) and the heaviest query blocks
-// first.
-template <typename T, int D>
-__global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
+// 256 per wave, two waves per SIMD). With NW = 4 two workgroups share a CU and
+// drift apart, so one workgroup's softmax overlaps the other's MFMAs. A wave
+// skips the blocks whose keys all lie after its last query. Workgroup ids put
+// the kv head fastest (a kv head's query blocks share one XCD's L2) and the
+// heaviest query blocks first.
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void varlen_prefill_gqa(PrefillArgs a) {
+  constexpr int NT = 64 * NW;             // threads per workgroup
   constexpr int KJ = D / 16;              // 16-dim steps of the QK reduction
   constexpr int NU = D / 32;              // 32-dim column tiles of the output
   constexpr int CPR = D / 8;              // 16-byte chunks per K/V row
   constexpr int ROWK = D + 8, ROWV = D + 32, ROWO = D + 8;  // LDS row strides, elements
   constexpr int KCH = 32 * CPR;           // chunks per tensor per block
-  constexpr int NCH = 2 * KCH / 512;      // chunks per thread per block
+  constexpr int NCH = 2 * KCH / NT;       // chunks per thread per block
   constexpr int KBUF = 32 * ROWK, VBUF = 32 * ROWV;
-  static_assert(NCH >= 1 && 2 * KCH == 512 * NCH, "one K/V block is an exact number of chunks per thread");
-  constexpr int SMEM = 2 * (KBUF + VBUF) > 8 * 32 * ROWO ? 2 * (KBUF + VBUF) : 8 * 32 * ROWO;
+  static_assert(NCH >= 1 && 2 * KCH == NT * NCH, "one K/V block is an exact number of chunks per thread");
+  constexpr int SMEM = 2 * (KBUF + VBUF) > NW * 32 * ROWO ? 2 * (KBUF + VBUF) : NW * 32 * ROWO;
   // A row's running max only moves when it grows by more than this (log2
   // units): p = 2^(s - m) then stays below 2^8, and the accumulator is
   // rescaled rarely. l uses the same m, so the result is unchanged.
@@ -242,7 +245,7 @@ __global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int G = a.G, QB = 256 / G;
+  const int G = a.G, QB = 32 * NW / G;
   const int id = blockIdx.x;
   const int kvh = id % a.Hkv;
   const int rest = id / a.Hkv;
@@ -282,35 +285,54 @@ __global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
   const int q_last = row0 + QB < q_len ? row0 + QB : q_len;  // one past the block's last query
   const int kend = a.causal ? (k_len < q_last ? k_len : q_last) : k_len;
   const int nblk = (kend + 31) / 32;
+  // Keys this wave needs (its tile is 32 queries from q0).
+  const int wend = q0 >= q_len ? 0 : (a.causal ? (kend < q0 + 32 ? kend : q0 + 32) : kend);
 
-  // Chunk i of this thread: K chunks first, then V; key-major, 16 bytes each.
-  // Loads are unconditional (keys past k_len read the sequence's last key, so
-  // no exec-masked load has to wait for a stage still in flight); those rows
-  // are zeroed when the stage is written to LDS.
+  // Chunk i of this thread: K chunks first, then V; key-major, 16 bytes
+  // each. A thread's chunks share the column chunk ch0 and lie whole rows
+  // apart, so each address is a per-thread offset plus a uniform term. A
+  // block wholly inside the sequence loads from a uniform block pointer plus
+  // those offsets. In the sequence's last, partial block keys past k_len read
+  // the last key instead (no exec-masked load has to wait for a stage still
+  // in flight), and those rows are zeroed when the stage is written to LDS.
+  constexpr bool kSplitUniform = KCH % NT == 0;  // chunk i is all K or all V
+  const int r0 = tid / CPR, ch0 = tid % CPR;
+  auto chunk_isk = [&](int i) { return kSplitUniform ? NT * i < KCH : tid + NT * i < KCH; };
+  auto chunk_drow = [&](int i) { return (NT * i - (chunk_isk(i) ? 0 : KCH)) / CPR; };  // row - r0
+  const int64_t kst_b = a.k_st * static_cast<int64_t>(sizeof(T)), vst_b = a.v_st * static_cast<int64_t>(sizeof(T));
+  const uint32_t koff0 = static_cast<uint32_t>(r0 * kst_b) + 16u * ch0;  // < 2^32: strides checked on the host
+  const uint32_t voff0 = static_cast<uint32_t>(r0 * vst_b) + 16u * ch0;
   u32x4 stg[2][NCH];
   auto gload = [&](int blk, int st) {
+    const int kb = blk * 32;
+    if (kb + 32 <= k_len) {
+      const char* kbase = reinterpret_cast<const char*>(kb_ptr) + kb * kst_b;
+      const char* vbase = reinterpret_cast<const char*>(vb_ptr) + kb * vst_b;
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int q = tid + 512 * i;
-      const bool isk = q < KCH;
-      const int qq = isk ? q : q - KCH;
-      const int key = qq / CPR, ch = qq % CPR;
-      const int kk = min(blk * 32 + key, k_len - 1);
-      const T* src = isk ? kb_ptr + static_cast<int64_t>(kk) * a.k_st : vb_ptr + static_cast<int64_t>(kk) * a.v_st;
-      stg[st][i] = *reinterpret_cast<const u32x4*>(src + 8 * ch);
+      for (int i = 0; i < NCH; ++i) {
+        const int dr = chunk_drow(i);
+        const char* src = chunk_isk(i) ? kbase + dr * kst_b + koff0 : vbase + dr * vst_b + voff0;
+        stg[st][i] = *reinterpret_cast<const u32x4*>(src);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const bool isk = chunk_isk(i);
+        const int kk = min(kb + r0 + chunk_drow(i), k_len - 1);
+        const T* src = isk ? kb_ptr + static_cast<int64_t>(kk) * a.k_st : vb_ptr + static_cast<int64_t>(kk) * a.v_st;
+        stg[st][i] = *reinterpret_cast<const u32x4*>(src + 8 * ch0);
+      }
     }
   };
   auto swrite = [&](int buf, int st, int blk) {
-    const u32x4 zero = {0, 0, 0, 0};
+    const bool full = blk * 32 + 32 <= k_len;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-      const int q = tid + 512 * i;
-      const bool isk = q < KCH;
-      const int qq = isk ? q : q - KCH;
-      const int key = qq / CPR, ch = qq % CPR;
-      const bool ok = blk * 32 + key < k_len;
-      uint16_t* dst = isk ? kl + buf * KBUF + key * ROWK + 8 * ch : vl + buf * VBUF + key * ROWV + 8 * ch;
-      *reinterpret_cast<u32x4*>(dst) = ok ? stg[st][i] : zero;
+      const int dr = chunk_drow(i);
+      uint16_t* dst = chunk_isk(i) ? kl + buf * KBUF + (r0 + dr) * ROWK + 8 * ch0 : vl + buf * VBUF + (r0 + dr) * ROWV + 8 * ch0;
+      u32x4 w = stg[st][i];
+      if (!full && blk * 32 + r0 + dr >= k_len) w = u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(dst) = w;
     }
   };
 
@@ -327,76 +349,86 @@ __global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
     const int kb0 = blk * 32;
     const uint16_t* kbuf = kl + st * KBUF;
     const uint16_t* vbuf = vl + st * VBUF;
+    // A block whose keys all lie after this wave's last query (or a wave
+    // with no queries) contributes nothing: p would be exactly 0.
+    if (kb0 < wend) {
+      // S^T: lane (h, c) gets query c's scores of keys 8(e/4) + 4h + e%4.
+      // All K operand reads are issued before the first MFMA, so the LDS latency
+      // is paid once per block rather than once per step. The reduction over
+      // head_dim runs as two interleaved accumulator chains (even and odd
+      // steps), so consecutive MFMAs never wait on each other's result.
+      u32x4 kop[KJ];
+#pragma unroll
+      for (int jj = 0; jj < KJ; ++jj) kop[jj] = *reinterpret_cast<const u32x4*>(kbuf + c * ROWK + 16 * jj + 8 * h);
+      f32x16 sc0, sc1;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc0[e] = sc1[e] = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < KJ; jj += 2) {
+        sc0 = mfma_k16x32<T>(kop[jj], qop[jj], sc0);
+        sc1 = mfma_k16x32<T>(kop[jj + 1], qop[jj + 1], sc1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, KJ, 0);  // the K operand reads
+      __builtin_amdgcn_sched_group_barrier(0x008, KJ, 0);  // then the score MFMAs
+      f32x16 sc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = sc0[e] + sc1[e];
 
-    // S^T: lane (h, c) gets query c's scores of keys 8(e/4) + 4h + e%4.
-    f32x16 sc;
+      // Keys past k_len, and (causal) keys after the query, only occur in a
+      // sequence's last block or on the diagonal: a wave-uniform branch.
+      if (kb0 + 32 > k_len || (a.causal && kb0 + 31 > q0)) {
+        const int qq = q0 + c;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) sc[e] = 0.f;
-    // All K operand reads are issued before the first MFMA, so the LDS latency
-    // is paid once per block rather than once per step.
-    u32x4 kop[KJ];
+        for (int e = 0; e < 16; ++e) {
+          const int kk = kb0 + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (!(kk < k_len && (!a.causal || kk <= qq))) sc[e] = kNegInfP;
+        }
+      }
+      float tmax = kNegInfP;
 #pragma unroll
-    for (int jj = 0; jj < KJ; ++jj) kop[jj] = *reinterpret_cast<const u32x4*>(kbuf + c * ROWK + 16 * jj + 8 * h);
+      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float mt = tmax * cs;
+      if (__any(mt > m + kRescale)) {
+        const float m_new = fmaxf(m, mt);
+        const float alpha = m_new == kNegInfP ? 1.f : fast_exp2(m - m_new);
+        l *= alpha;
 #pragma unroll
-    for (int jj = 0; jj < KJ; ++jj) sc = mfma_k16x32<T>(kop[jj], qop[jj], sc);
-    __builtin_amdgcn_sched_group_barrier(0x100, KJ, 0);  // the K operand reads
-    __builtin_amdgcn_sched_group_barrier(0x008, KJ, 0);  // then the score MFMAs
-
-    // Keys past k_len, and (causal) keys after the query, only occur in a
-    // sequence's last block or on the diagonal: a wave-uniform branch.
-    if (kb0 + 32 > k_len || (a.causal && kb0 + 31 > q0)) {
-      const int qq = q0 + c;
+        for (int e = 0; e < 16; ++e) {
+          const float ar = __shfl(alpha, 8 * (e >> 2) + 4 * h + (e & 3), 64);
+#pragma unroll
+          for (int u = 0; u < NU; ++u) acc[u][e] *= ar;
+        }
+        m = m_new;
+      }
+      const float mm = m == kNegInfP ? 0.f : m;
+      float p[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int kk = kb0 + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (!(kk < k_len && (!a.causal || kk <= qq))) sc[e] = kNegInfP;
+        p[e] = fast_exp2(fmaf(sc[e], cs, -mm));
+        l += p[e];
       }
-    }
-    float tmax = kNegInfP;
+      u32x4 pop[2];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float mt = tmax * cs;
-    if (__any(mt > m + kRescale)) {
-      const float m_new = fmaxf(m, mt);
-      const float alpha = m_new == kNegInfP ? 1.f : fast_exp2(m - m_new);
-      l *= alpha;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float ar = __shfl(alpha, 8 * (e >> 2) + 4 * h + (e & 3), 64);
-#pragma unroll
-        for (int u = 0; u < NU; ++u) acc[u][e] *= ar;
-      }
-      m = m_new;
-    }
-    const float mm = m == kNegInfP ? 0.f : m;
-    float p[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      p[e] = fast_exp2(fmaf(sc[e], cs, -mm));
-      l += p[e];
-    }
-    u32x4 pop[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-      pop[s] = u32x4{pack2<T>(p[8 * s], p[8 * s + 1]), pack2<T>(p[8 * s + 2], p[8 * s + 3]),
-                     pack2<T>(p[8 * s + 4], p[8 * s + 5]), pack2<T>(p[8 * s + 6], p[8 * s + 7])};
+      for (int s = 0; s < 2; ++s)
+        pop[s] = u32x4{pack2<T>(p[8 * s], p[8 * s + 1]), pack2<T>(p[8 * s + 2], p[8 * s + 3]),
+                       pack2<T>(p[8 * s + 4], p[8 * s + 5]), pack2<T>(p[8 * s + 6], p[8 * s + 7])};
 
-    // P.V: B operand of step s, column tile u: V[keys 16s+4h+e, 16s+8+4h+e]
-    // [dims 32u + c], read transposed from the row-major LDS block.
-    const int jl = c & 15;
-    const uint16_t* vt = vbuf + (4 * h + (jl >> 2)) * ROWV + 16 * (c >> 4) + 4 * (jl & 3);
+      // P.V: B operand of step s, column tile u: V[keys 16s+4h+e, 16s+8+4h+e]
+      // [dims 32u + c], read transposed from the row-major LDS block.
+      const int jl = c & 15;
+      const uint16_t* vt = vbuf + (4 * h + (jl >> 2)) * ROWV + 16 * (c >> 4) + 4 * (jl & 3);
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int u = 0; u < NU; ++u) {
-        const uint16_t* base = vt + 16 * s * ROWV + 32 * u;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)base);
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + 8 * ROWV));
-        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
-        acc[u] = mfma_k16x32<T>(pop[s], u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}, acc[u]);
-      }
-
+        for (int u = 0; u < NU; ++u) {
+          const uint16_t* base = vt + 16 * s * ROWV + 32 * u;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)base);
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + 8 * ROWV));
+          const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+          acc[u] = mfma_k16x32<T>(pop[s], u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}, acc[u]);
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
     swrite(st ^ 1, st ^ 1, clampb(blk + 1));
     lds_barrier();
@@ -417,13 +449,13 @@ __global__ __launch_bounds__(512) void varlen_prefill_gqa(PrefillArgs a) {
   // a workgroup barrier after every wave's last read of the K/V buffers.
   if (q0 >= q_len) return;
   uint16_t* ost = smem + wave * 32 * ROWO;
-  float lt = l + __shfl_xor(l, 32, 64);  // query c's denominator
+  const float rl = 1.f / (l + __shfl_xor(l, 32, 64));  // 1 / query c's denominator
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int r = 8 * (e >> 2) + 4 * h + (e & 3);
-    const float lr = __shfl(lt, r, 64);
+    const float rr = __shfl(rl, r, 64);
 #pragma unroll
-    for (int u = 0; u < NU; ++u) ost[r * ROWO + 32 * u + c] = from_float<T>(acc[u][e] / lr).x;
+    for (int u = 0; u < NU; ++u) ost[r * ROWO + 32 * u + c] = from_float<T>(acc[u][e] * rr).x;
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
   __builtin_amdgcn_wave_barrier();
@@ -515,13 +547,23 @@ static int launch_prefill(PrefillArgs& a, bool mfma, int64_t total_q, int64_t ma
     return check_launch("tsa_varlen_prefill");
   }
   if constexpr (sizeof(T) == 2) {
-    if (a.G <= 8 && 8 % a.G == 0 && a.scale_log2 > 0.f) {
-      const int QB = 256 / a.G;
+    // The LDS-staged kernel keeps 32 rows of K/V byte offsets in 32 bits.
+    const int64_t kMaxStride = int64_t{1} << 24;
+    if (a.G <= 8 && 8 % a.G == 0 && a.scale_log2 > 0.f && a.k_st < kMaxStride && a.v_st < kMaxStride) {
+      // Four waves per workgroup when the group fits (two workgroups per CU),
+      // else eight.
+      const int nw = 4 % a.G == 0 ? 4 : 8;
+      const int QB = 32 * nw / a.G;
       a.nqb = static_cast<int32_t>((max_seqlen_q + QB - 1) / QB);
       if (a.nqb == 0) return TSA_OK;
       const dim3 grid(static_cast<uint32_t>(a.nqb) * a.nseq * a.Hkv);
-      if (a.D == 128) varlen_prefill_gqa<T, 128><<<grid, dim3(512), 0, stream>>>(a);
-      else varlen_prefill_gqa<T, 64><<<grid, dim3(512), 0, stream>>>(a);
+      if (nw == 4) {
+        if (a.D == 128) varlen_prefill_gqa<T, 128, 4><<<grid, dim3(256), 0, stream>>>(a);
+        else varlen_prefill_gqa<T, 64, 4><<<grid, dim3(256), 0, stream>>>(a);
+      } else {
+        if (a.D == 128) varlen_prefill_gqa<T, 128, 8><<<grid, dim3(512), 0, stream>>>(a);
+        else varlen_prefill_gqa<T, 64, 8><<<grid, dim3(512), 0, stream>>>(a);
+      }
     } else {
       a.nqb = static_cast<int32_t>((max_seqlen_q + 31) / 32);
       if (a.nqb == 0) return TSA_OK;
