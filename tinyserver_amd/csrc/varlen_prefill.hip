@@ -6,8 +6,8 @@
 // P cast to the V dtype before P.V (:126), l summing the fp32 P (:128-129).
 //
 // Three kernels, chosen per call:
-//   varlen_prefill_gqa   bf16/f16, head_dim 64/128, GQA group a divisor of 8:
-//                        one workgroup per (kv head, sequence, query block),
+//   varlen_prefill_gqa   bf16/f16, head_dim 64/128, GQA group 2, 4 or 8:
+//                        one workgroup per (kv head, sequence, 32 queries),
 //                        K/V staged in LDS once for the whole group, 32x32x16
 //                        MFMA tiles (the main path);
 //   varlen_prefill_mfma  other group sizes: 4 q-heads per workgroup, operands
@@ -20,6 +20,9 @@
 #include <type_traits>
 
 #include "tsa_common.h"
+
+// The K/V loads set M0 in inline assembly and list it as clobbered.
+#pragma clang diagnostic ignored "-Winline-asm"
 
 namespace tsa {
 
@@ -195,12 +198,13 @@ __global__ __launch_bounds__(256) void varlen_prefill_mfma(PrefillArgs a) {
   }
 }
 
-// LDS-staged GQA flash attention on 32x32 tiles. A workgroup of NW waves (4
-// or 8) owns one kv head of one sequence and 32 NW/G queries (G = q heads per
-// kv head, a divisor of NW): wave w takes the 32 queries 32 (w / G).. of
-// q-head w % G, so all NW tiles read the same K/V. 32-key K/V blocks are staged once per
-// workgroup in double-buffered LDS, the global loads of block i+2 in flight
-// while block i is computed. Both products run on v_mfma_f32_32x32x16 (the
+// LDS-staged GQA flash attention on 32x32 tiles. A workgroup of NW = G waves
+// (G = q heads per kv head: 2, 4 or 8) owns one kv head of one sequence and
+// 32 queries: wave w takes those queries of q-head w, so all NW tiles read
+// the same K/V and need the same key blocks. 32-key K/V blocks are staged
+// once per workgroup in double-buffered LDS, with K one block ahead of V and
+// the global loads of the next blocks in flight while a block is computed.
+// Both products run on v_mfma_f32_32x32x16 (the
 // 16x16x32 form has about 60% of its throughput on gfx950). With lane
 // (h, c) = (lane / 32, lane % 32) and accumulator element e holding row
 // 8(e/4) + 4h + e%4, column c:
@@ -218,34 +222,37 @@ __global__ __launch_bounds__(256) void varlen_prefill_mfma(PrefillArgs a) {
 //     stride D+32 elements, so the two groups of a half-wave hit disjoint
 //     banks.
 // Scores, probabilities and the output accumulators all stay in VGPRs (at most
-// 256 per wave, two waves per SIMD). With NW = 4 two workgroups share a CU and
-// drift apart, so one workgroup's softmax overlaps the other's MFMAs. A wave
-// skips the blocks whose keys all lie after its last query. Workgroup ids put
-// the kv head fastest (a kv head's query blocks share one XCD's L2) and the
-// heaviest query blocks first.
+// 256 per wave, two waves per SIMD); several workgroups share a CU and drift
+// apart, so one workgroup's softmax overlaps another's MFMAs. Workgroup ids
+// put the kv head fastest (a kv head's query blocks share one XCD's L2) and
+// the heaviest query blocks first.
 template <typename T, int D, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void varlen_prefill_gqa(PrefillArgs a) {
-  constexpr int NT = 64 * NW;             // threads per workgroup
   constexpr int KJ = D / 16;              // 16-dim steps of the QK reduction
   constexpr int NU = D / 32;              // 32-dim column tiles of the output
   constexpr int CPR = D / 8;              // 16-byte chunks per K/V row
-  constexpr int ROWK = D + 8, ROWV = D + 32, ROWO = D + 8;  // LDS row strides, elements
-  constexpr int KCH = 32 * CPR;           // chunks per tensor per block
-  constexpr int NCH = 2 * KCH / NT;       // chunks per thread per block
-  constexpr int KBUF = 32 * ROWK, VBUF = 32 * ROWV;
-  static_assert(NCH >= 1 && 2 * KCH == NT * NCH, "one K/V block is an exact number of chunks per thread");
-  constexpr int SMEM = 2 * (KBUF + VBUF) > NW * 32 * ROWO ? 2 * (KBUF + VBUF) : NW * 32 * ROWO;
+  constexpr int RB = 2 * D;               // bytes per K/V row in LDS (unpadded)
+  constexpr int ROWO = D + 8;             // output staging row stride, elements
+  constexpr int BLKB = 32 * RB;           // bytes per 32-row K or V block
+  // K/V block slots in LDS and the prefetch distance in blocks: the loads
+  // of a block are issued A iterations before it is needed.
+  constexpr int NB = NW == 2 ? 2 : 4, A = NB - 1;
+  constexpr int RPI = 1024 / RB;          // rows per 1 KB load instruction
+  constexpr int IPW = 2 * (32 / RPI) / NW;  // load instructions per wave per block step
+  constexpr int SMEM = NB * 2 * BLKB > NW * 32 * ROWO * 2 ? NB * 2 * BLKB : NW * 32 * ROWO * 2;  // bytes
+  static_assert(IPW >= 1 && IPW * NW == 2 * (32 / RPI), "a block step is a whole number of loads per wave");
+  static_assert((A > 1 ? A - 1 : 0) * IPW <= 63, "outstanding loads fit the vmcnt field");
   // A row's running max only moves when it grows by more than this (log2
   // units): p = 2^(s - m) then stays below 2^8, and the accumulator is
   // rescaled rarely. l uses the same m, so the result is unchanged.
   constexpr float kRescale = 8.0f;
-  __shared__ __align__(16) uint16_t smem[SMEM];  // K/V blocks, then the output tiles
-  uint16_t* const kl = smem;               // [2][32][ROWK]
-  uint16_t* const vl = smem + 2 * KBUF;    // [2][32][ROWV]
+  // K slots [NB][32 rows][RB], then V slots; afterwards the output tiles.
+  __shared__ __align__(16) char smem[SMEM];
+  constexpr int VOFF = NB * BLKB;           // byte offset of the V slots
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int G = a.G, QB = 32 * NW / G;
+  constexpr int QB = 32;  // queries per workgroup
   const int id = blockIdx.x;
   const int kvh = id % a.Hkv;
   const int rest = id / a.Hkv;
@@ -264,8 +271,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   const float cs = a.scale_log2;  // > 0 on this path
 
   // This wave's tile: queries q0..q0+31 of q-head `head`.
-  const int q0 = row0 + 32 * (wave / G);
-  const int head = kvh * G + wave % G;
+  const int q0 = row0;
+  const int head = kvh * NW + wave;
   u32x4 qop[KJ];
   {
     const int row = q0 + c;
@@ -285,170 +292,237 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   const int q_last = row0 + QB < q_len ? row0 + QB : q_len;  // one past the block's last query
   const int kend = a.causal ? (k_len < q_last ? k_len : q_last) : k_len;
   const int nblk = (kend + 31) / 32;
-  // Keys this wave needs (its tile is 32 queries from q0).
-  const int wend = q0 >= q_len ? 0 : (a.causal ? (kend < q0 + 32 ? kend : q0 + 32) : kend);
 
-  // Chunk i of this thread: K chunks first, then V; key-major, 16 bytes
-  // each. A thread's chunks share the column chunk ch0 and lie whole rows
-  // apart, so each address is a per-thread offset plus a uniform term. A
-  // block wholly inside the sequence loads from a uniform block pointer plus
-  // those offsets. In the sequence's last, partial block keys past k_len read
-  // the last key instead (no exec-masked load has to wait for a stage still
-  // in flight), and those rows are zeroed when the stage is written to LDS.
-  constexpr bool kSplitUniform = KCH % NT == 0;  // chunk i is all K or all V
-  const int r0 = tid / CPR, ch0 = tid % CPR;
-  auto chunk_isk = [&](int i) { return kSplitUniform ? NT * i < KCH : tid + NT * i < KCH; };
-  auto chunk_drow = [&](int i) { return (NT * i - (chunk_isk(i) ? 0 : KCH)) / CPR; };  // row - r0
-  const int64_t kst_b = a.k_st * static_cast<int64_t>(sizeof(T)), vst_b = a.v_st * static_cast<int64_t>(sizeof(T));
-  const uint32_t koff0 = static_cast<uint32_t>(r0 * kst_b) + 16u * ch0;  // < 2^32: strides checked on the host
-  const uint32_t voff0 = static_cast<uint32_t>(r0 * vst_b) + 16u * ch0;
-  u32x4 stg[2][NCH];
-  auto gload = [&](int blk, int st) {
-    const int kb = blk * 32;
-    if (kb + 32 <= k_len) {
-      const char* kbase = reinterpret_cast<const char*>(kb_ptr) + kb * kst_b;
-      const char* vbase = reinterpret_cast<const char*>(vb_ptr) + kb * vst_b;
+  // K/V rows are stored unpadded, RB bytes each, with the 16-byte chunk ch
+  // of row r at position ch ^ swz(r). swz is a bijection on r % 16, so the
+  // 16 lanes of a K operand read (16 rows, one chunk) hit 16 distinct bank
+  // quads, and it maps r % 4 to the upper bits, so a transposed V read (4
+  // consecutive rows x 2 chunks per 16 lanes) is conflict-free as well.
+  auto swz = [](int r) {
+    return D == 128 ? ((r & 3) << 2) | ((r >> 2) & 3) : (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  };
+
+  // K and V go from global memory straight into LDS (global_load_lds_dwordx4:
+  // each lane carries 16 bytes, the wave's 1 KB lands contiguously at a
+  // wave-uniform LDS address), so no registers stage them and the loads run
+  // A blocks ahead. Lane l of a load whose first row is R0 fetches the chunk
+  // that belongs at row R0 + l / CPR, position l % CPR. Block step s moves K
+  // block s + 1 and V block s, IPW loads per wave: waves 0 .. NW/2 - 1 the K
+  // rows, the others the V rows. Rows past the sequence's end re-read its
+  // last key, which the mask or a zero probability then ignores. Slots are
+  // taken by the nominal block number, so a step past the last block (its
+  // rows clamped) still writes a free slot and every wave issues the same
+  // number of loads per step.
+  typedef __attribute__((address_space(3))) void lds_void;
+  auto clampb = [&](int blk) { return blk < nblk ? blk : nblk - 1; };
+  const bool k_wave = wave < NW / 2;
+  const int row0w = (wave % (NW / 2)) * IPW * RPI;  // first row this wave loads
+  const int64_t st_b = (k_wave ? a.k_st : a.v_st) * static_cast<int64_t>(sizeof(T));
+  const char* const gbase = reinterpret_cast<const char*>(k_wave ? kb_ptr : vb_ptr);
+  const int lrow = lane / CPR;
+  auto lane_chunk = [&](int i) { return (lane % CPR) ^ swz(row0w + i * RPI + lrow); };
+  uint32_t doff[IPW];  // lane byte offsets from the first row of load i (< 2^32: strides checked on the host)
 #pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        const int dr = chunk_drow(i);
-        const char* src = chunk_isk(i) ? kbase + dr * kst_b + koff0 : vbase + dr * vst_b + voff0;
-        stg[st][i] = *reinterpret_cast<const u32x4*>(src);
-      }
+  for (int i = 0; i < IPW; ++i) doff[i] = static_cast<uint32_t>(lrow * st_b) + 16u * lane_chunk(i);
+  // The loads are written as assembly: the form with a uniform 64-bit base
+  // and a 32-bit lane offset reads half the address registers of the
+  // 64-bit-address form, and M0 (the LDS address) is set right before each,
+  // with the one wait state an LDS DMA needs after an M0 write. Nothing else
+  // in this file uses M0.
+  const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)smem));  // address-space cast
+  auto dma = [&](const char* sbase, uint32_t voff, int lds_byte) __attribute__((always_inline)) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+                 "s"(smem_lds + lds_byte)
+                 : "memory", "m0");
+  };
+  auto dma64 = [&](const char* src, int lds_byte) __attribute__((always_inline)) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(smem_lds + lds_byte)
+                 : "memory", "m0");
+  };
+  // This wave's loads of block blk (K if k_wave) into slot `slot`.
+  auto load_block = [&](int blk, int slot) __attribute__((always_inline)) {
+    const int key0 = clampb(blk) * 32 + row0w;
+    const int lds0 = (k_wave ? 0 : VOFF) + slot * BLKB + row0w * RB;
+    if (key0 + IPW * RPI <= k_len) {
+      const char* src = gbase + key0 * st_b;
+#pragma unroll
+      for (int i = 0; i < IPW; ++i) dma(src + i * RPI * st_b, doff[i], lds0 + i * 1024);
     } else {
 #pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        const bool isk = chunk_isk(i);
-        const int kk = min(kb + r0 + chunk_drow(i), k_len - 1);
-        const T* src = isk ? kb_ptr + static_cast<int64_t>(kk) * a.k_st : vb_ptr + static_cast<int64_t>(kk) * a.v_st;
-        stg[st][i] = *reinterpret_cast<const u32x4*>(src + 8 * ch0);
+      for (int i = 0; i < IPW; ++i) {
+        const int key = min(key0 + i * RPI + lrow, k_len - 1);
+        dma64(gbase + key * st_b + 16 * lane_chunk(i), lds0 + i * 1024);
       }
     }
   };
-  auto swrite = [&](int buf, int st, int blk) {
-    const bool full = blk * 32 + 32 <= k_len;
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int dr = chunk_drow(i);
-      uint16_t* dst = chunk_isk(i) ? kl + buf * KBUF + (r0 + dr) * ROWK + 8 * ch0 : vl + buf * VBUF + (r0 + dr) * ROWV + 8 * ch0;
-      u32x4 w = stg[st][i];
-      if (!full && blk * 32 + r0 + dr >= k_len) w = u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(dst) = w;
-    }
+  auto load_step = [&](int s) __attribute__((always_inline)) {
+    if (k_wave) load_block(s + 1, (s + 1) % NB);
+    else load_block(s, s % NB);
   };
+  // Wait until at most n of this wave's loads are in flight (they complete
+  // in issue order).
+  auto wait_loads = [&](auto n) {
+    constexpr int N = decltype(n)::value;
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  };
+  constexpr int kInFlight = (A - 1) * IPW;  // loads of the later steps, still in flight at a block's end
 
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-  auto clampb = [&](int blk) { return blk < nblk ? blk : nblk - 1; };
-  // Block blk computes from LDS buffer blk & 1 while block blk + 2's global
-  // loads are in flight into register stage blk & 1 and block blk + 1 (stage
-  // (blk + 1) & 1) is written to the other LDS buffer. The loop is unrolled by
-  // two so the stages are compile-time registers.
-  auto block_step = [&](int blk, auto stage) {
-    constexpr int st = decltype(stage)::value;
-    gload(clampb(blk + 2), st);
-    __builtin_amdgcn_sched_barrier(0);
-    const int kb0 = blk * 32;
-    const uint16_t* kbuf = kl + st * KBUF;
-    const uint16_t* vbuf = vl + st * VBUF;
-    // A block whose keys all lie after this wave's last query (or a wave
-    // with no queries) contributes nothing: p would be exactly 0.
-    if (kb0 < wend) {
-      // S^T: lane (h, c) gets query c's scores of keys 8(e/4) + 4h + e%4.
-      // All K operand reads are issued before the first MFMA, so the LDS latency
-      // is paid once per block rather than once per step. The reduction over
-      // head_dim runs as two interleaved accumulator chains (even and odd
-      // steps), so consecutive MFMAs never wait on each other's result.
-      u32x4 kop[KJ];
-#pragma unroll
-      for (int jj = 0; jj < KJ; ++jj) kop[jj] = *reinterpret_cast<const u32x4*>(kbuf + c * ROWK + 16 * jj + 8 * h);
-      f32x16 sc0, sc1;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sc0[e] = sc1[e] = 0.f;
-#pragma unroll
-      for (int jj = 0; jj < KJ; jj += 2) {
-        sc0 = mfma_k16x32<T>(kop[jj], qop[jj], sc0);
-        sc1 = mfma_k16x32<T>(kop[jj + 1], qop[jj + 1], sc1);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x100, KJ, 0);  // the K operand reads
-      __builtin_amdgcn_sched_group_barrier(0x008, KJ, 0);  // then the score MFMAs
-      f32x16 sc;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sc[e] = sc0[e] + sc1[e];
 
-      // Keys past k_len, and (causal) keys after the query, only occur in a
-      // sequence's last block or on the diagonal: a wave-uniform branch.
-      if (kb0 + 32 > k_len || (a.causal && kb0 + 31 > q0)) {
-        const int qq = q0 + c;
+  // K operands of the block in slot ks: lane (h, c) reads key c, dims
+  // 16jj + 8h..+8, i.e. chunk 2jj + h at position (2jj + h) ^ swz(c): byte
+  // c RB + ((32 jj) ^ 16 (h ^ swz(c))), the XOR staying inside the row.
+  const int ka = c * RB + 16 * (h ^ swz(c));
+  u32x4 kop[KJ];
+  auto kread = [&](int ks) {
+    const int kb = ks * BLKB + ka;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int kk = kb0 + 8 * (e >> 2) + 4 * h + (e & 3);
-          if (!(kk < k_len && (!a.causal || kk <= qq))) sc[e] = kNegInfP;
-        }
-      }
-      float tmax = kNegInfP;
+    for (int jj = 0; jj < KJ; ++jj) kop[jj] = *reinterpret_cast<const u32x4*>(smem + (kb ^ (32 * jj)));
+  };
+  // S^T(block) = K Q^T: lane (h, c) gets query c's scores of keys
+  // 8(e/4) + 4h + e%4 of the block.
+  auto qk = [&](f32x16& sc) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float mt = tmax * cs;
-      if (__any(mt > m + kRescale)) {
-        const float m_new = fmaxf(m, mt);
-        const float alpha = m_new == kNegInfP ? 1.f : fast_exp2(m - m_new);
-        l *= alpha;
+    for (int e = 0; e < 16; ++e) sc[e] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float ar = __shfl(alpha, 8 * (e >> 2) + 4 * h + (e & 3), 64);
-#pragma unroll
-          for (int u = 0; u < NU; ++u) acc[u][e] *= ar;
-        }
-        m = m_new;
-      }
-      const float mm = m == kNegInfP ? 0.f : m;
-      float p[16];
+    for (int jj = 0; jj < KJ; ++jj) sc = mfma_k16x32<T>(kop[jj], qop[jj], sc);
+  };
+  // Masking, the running max and the (rare) rescale for block blk's scores.
+  auto softmax_max = [&](f32x16& sc, int blk) {
+    const int kb0 = blk * 32;
+    // Keys past k_len, and (causal) keys after the query, only occur in a
+    // sequence's last block or on the diagonal: a wave-uniform branch.
+    if (kb0 + 32 > k_len || (a.causal && kb0 + 31 > q0)) {
+      const int qq = q0 + c;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        p[e] = fast_exp2(fmaf(sc[e], cs, -mm));
-        l += p[e];
+        const int kk = kb0 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (!(kk < k_len && (!a.causal || kk <= qq))) sc[e] = kNegInfP;
       }
-      u32x4 pop[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        pop[s] = u32x4{pack2<T>(p[8 * s], p[8 * s + 1]), pack2<T>(p[8 * s + 2], p[8 * s + 3]),
-                       pack2<T>(p[8 * s + 4], p[8 * s + 5]), pack2<T>(p[8 * s + 6], p[8 * s + 7])};
-
-      // P.V: B operand of step s, column tile u: V[keys 16s+4h+e, 16s+8+4h+e]
-      // [dims 32u + c], read transposed from the row-major LDS block.
-      const int jl = c & 15;
-      const uint16_t* vt = vbuf + (4 * h + (jl >> 2)) * ROWV + 16 * (c >> 4) + 4 * (jl & 3);
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int u = 0; u < NU; ++u) {
-          const uint16_t* base = vt + 16 * s * ROWV + 32 * u;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)base);
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + 8 * ROWV));
-          const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
-          acc[u] = mfma_k16x32<T>(pop[s], u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}, acc[u]);
-        }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    swrite(st ^ 1, st ^ 1, clampb(blk + 1));
+    float tmax = kNegInfP;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mt = tmax * cs;
+    if (__any(mt > m + kRescale)) {
+      const float m_new = fmaxf(m, mt);
+      const float alpha = m_new == kNegInfP ? 1.f : fast_exp2(m - m_new);
+      l *= alpha;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float ar = __shfl(alpha, 8 * (e >> 2) + 4 * h + (e & 3), 64);
+#pragma unroll
+        for (int u = 0; u < NU; ++u) acc[u][e] *= ar;
+      }
+      m = m_new;
+    }
+  };
+  // p = 2^(s cs - m) in fp32 (summed into l), packed to the P operands of
+  // the two 16-key steps: k-slots 8h..8h+7 of step s are keys 16s+4h+0..3
+  // and 16s+8+4h+0..3, i.e. score accumulators 8s..8s+7 of the same lane.
+  u32x4 pop[2];
+  auto softmax_exp = [&](const f32x16& sc) {
+    const float mm = m == kNegInfP ? 0.f : m;
+    float p[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      p[e] = fast_exp2(fmaf(sc[e], cs, -mm));
+      l += p[e];
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+      pop[s2] = u32x4{pack2<T>(p[8 * s2], p[8 * s2 + 1]), pack2<T>(p[8 * s2 + 2], p[8 * s2 + 3]),
+                      pack2<T>(p[8 * s2 + 4], p[8 * s2 + 5]), pack2<T>(p[8 * s2 + 6], p[8 * s2 + 7])};
+  };
+  // O += P V from the V block in slot vs: the B operand of step s, column
+  // tile u is V[keys 16s+4h+e, 16s+8+4h+e][dims 32u + c], read transposed.
+  // Lane (h, c) with jl = c % 16 reads 8 bytes of row 4h + jl/4 (+8, +16s),
+  // dims 32u + 16(c/16) + 4(jl%4): vofs[u] for the first row; the row 8
+  // further has swz XORed by 2, i.e. the byte offset XORed by 32.
+  int vofs[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int jl = c & 15, r = 4 * h + (jl >> 2), ch = 4 * u + 2 * (c >> 4) + ((jl & 3) >> 1);
+    vofs[u] = r * RB + 16 * (ch ^ swz(r)) + 8 * (jl & 1);
+  }
+  auto pv = [&](int vs) {
+    const int vb = VOFF + vs * BLKB;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const int lo_b = vb + 16 * s2 * RB + vofs[u];
+        const int hi_b = vb + 16 * s2 * RB + 8 * RB + (vofs[u] ^ 32);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(smem + lo_b));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(smem + hi_b));
+        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+        acc[u] = mfma_k16x32<T>(pop[s2], u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}, acc[u]);
+      }
+  };
+
+  // Software pipeline, one 32-key block per iteration j. On entry S(j) is in
+  // registers, K block j + 1 and V block j are in their LDS slots. The wave
+  // issues block step j + A's loads (into the slots of K(j) and V(j - 1),
+  // both last read before the previous barrier), reads K(j + 1), does the
+  // max/rescale of S(j), then issues the S(j + 1) MFMAs interleaved with the
+  // exponentials of S(j), so the matrix pipe and the VALU work at once, and
+  // finally P(j) V(j). It then waits for step j + 1's rows and meets the
+  // other waves at the barrier.
+  auto full = [&](int j, f32x16& cur, f32x16& nxt) {
+    load_step(j + A);
+    kread((j + 1) % NB);
+    softmax_max(cur, j);
+    qk(nxt);
+    softmax_exp(cur);
+    // One score MFMA, then a slice of the exponentials, and so on.
+#pragma unroll
+    for (int jj = 0; jj < KJ; ++jj) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 64 / KJ, 0);
+    }
+    pv(j % NB);
+    wait_loads(std::integral_constant<int, kInFlight>{});
     lds_barrier();
   };
+  auto last = [&](int j, f32x16& cur) {
+    softmax_max(cur, j);
+    softmax_exp(cur);
+    pv(j % NB);
+  };
   if (nblk > 0) {
-    gload(0, 0);
-    gload(clampb(1), 1);
-    swrite(0, 0, 0);
+    // K block 0, then steps 0 .. A - 1; wait for K(0) and step 0.
+    if (k_wave) load_block(0, 0);
+#pragma unroll
+    for (int s0 = 0; s0 < A; ++s0) load_step(s0);
+    wait_loads(std::integral_constant<int, kInFlight>{});
     lds_barrier();
-    for (int blk = 0; blk < nblk; blk += 2) {
-      block_step(blk, std::integral_constant<int, 0>{});
-      if (blk + 1 < nblk) block_step(blk + 1, std::integral_constant<int, 1>{});
+    f32x16 sca, scb;  // S of the even / odd blocks
+    kread(0);
+    qk(sca);
+    // Iteration 0's loads overwrite K(0)'s slot: every wave must have read it.
+    lds_barrier();
+    int j = 0;
+    for (; j + 2 < nblk; j += 2) {
+      full(j, sca, scb);
+      full(j + 1, scb, sca);
     }
+    if (j + 1 < nblk) {
+      full(j, sca, scb);
+      last(j + 1, scb);
+    } else {
+      last(j, sca);
+    }
+    // Clamped loads past the last block may still be landing in LDS.
+    wait_loads(std::integral_constant<int, 0>{});
+    lds_barrier();
   }
 
   // Output: each wave stages its 32 x D tile in its own slice of the (now
   // idle) K/V buffers and stores it as 16-byte row chunks. The loop ended on
   // a workgroup barrier after every wave's last read of the K/V buffers.
   if (q0 >= q_len) return;
-  uint16_t* ost = smem + wave * 32 * ROWO;
+  uint16_t* ost = reinterpret_cast<uint16_t*>(smem) + wave * 32 * ROWO;
   const float rl = 1.f / (l + __shfl_xor(l, 32, 64));  // 1 / query c's denominator
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
@@ -549,20 +623,18 @@ static int launch_prefill(PrefillArgs& a, bool mfma, int64_t total_q, int64_t ma
   if constexpr (sizeof(T) == 2) {
     // The LDS-staged kernel keeps 32 rows of K/V byte offsets in 32 bits.
     const int64_t kMaxStride = int64_t{1} << 24;
-    if (a.G <= 8 && 8 % a.G == 0 && a.scale_log2 > 0.f && a.k_st < kMaxStride && a.v_st < kMaxStride) {
-      // Four waves per workgroup when the group fits (two workgroups per CU),
-      // else eight.
-      const int nw = 4 % a.G == 0 ? 4 : 8;
-      const int QB = 32 * nw / a.G;
-      a.nqb = static_cast<int32_t>((max_seqlen_q + QB - 1) / QB);
+    if ((a.G == 2 || a.G == 4 || a.G == 8) && a.scale_log2 > 0.f && a.k_st < kMaxStride && a.v_st < kMaxStride) {
+      a.nqb = static_cast<int32_t>((max_seqlen_q + 31) / 32);
       if (a.nqb == 0) return TSA_OK;
-      const dim3 grid(static_cast<uint32_t>(a.nqb) * a.nseq * a.Hkv);
-      if (nw == 4) {
-        if (a.D == 128) varlen_prefill_gqa<T, 128, 4><<<grid, dim3(256), 0, stream>>>(a);
-        else varlen_prefill_gqa<T, 64, 4><<<grid, dim3(256), 0, stream>>>(a);
+      const dim3 grid(static_cast<uint32_t>(a.nqb) * a.nseq * a.Hkv), block(64 * a.G);
+      if (a.D == 128) {
+        if (a.G == 2) varlen_prefill_gqa<T, 128, 2><<<grid, block, 0, stream>>>(a);
+        else if (a.G == 4) varlen_prefill_gqa<T, 128, 4><<<grid, block, 0, stream>>>(a);
+        else varlen_prefill_gqa<T, 128, 8><<<grid, block, 0, stream>>>(a);
       } else {
-        if (a.D == 128) varlen_prefill_gqa<T, 128, 8><<<grid, dim3(512), 0, stream>>>(a);
-        else varlen_prefill_gqa<T, 64, 8><<<grid, dim3(512), 0, stream>>>(a);
+        if (a.G == 2) varlen_prefill_gqa<T, 64, 2><<<grid, block, 0, stream>>>(a);
+        else if (a.G == 4) varlen_prefill_gqa<T, 64, 4><<<grid, block, 0, stream>>>(a);
+        else varlen_prefill_gqa<T, 64, 8><<<grid, block, 0, stream>>>(a);
       }
     } else {
       a.nqb = static_cast<int32_t>((max_seqlen_q + 31) / 32);
