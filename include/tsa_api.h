@@ -124,7 +124,7 @@ int tsa_qk_norm_rope_store(const tsa_view* q, const tsa_view* k, const tsa_view*
 /* Bytes of workspace tsa_paged_decode needs: one partial-result slot per
  * (sequence x kv head, wave) pair that can occur -- num_seqs * num_kv_heads
  * + 4 * num_workgroups slots of (G * head_dim + 2 * G) floats -- and the tile
- * prefix (num_workgroups 0 = the library's choice, two per CU). */
+ * prefix (num_workgroups 0 = the library's choice, one per CU). */
 size_t tsa_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads,
                                         int64_t head_dim, int64_t max_blocks_per_seq,
                                         int64_t block_size, int32_t num_workgroups);
@@ -134,7 +134,7 @@ size_t tsa_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int
  * seq_lens[s] tokens gathered through block_tables[s], kv head h / (Hq/Hkv).
  * query/out: (B, Hq, D); caches (NB, Hkv, BS, D); block_tables (B, max_blocks)
  * int32; seq_lens (B,) int32. The 16-token tiles of all sequences are split
- * evenly over the 4 waves of num_workgroups workgroups (0 = two per CU); a
+ * evenly over the 4 waves of num_workgroups workgroups (0 = one per CU); a
  * second launch merges each sequence's per-wave partial results, which the
  * workspace holds (no initialisation needed; calls that share one must be
  * ordered on one stream). */

@@ -6,13 +6,14 @@
 // serial program. Here:
 //
 // * Work is the list of 16-token tiles of every (sequence, kv head) "unit",
-//   unit-major. A fixed grid of workgroups (by default two per CU, all
-//   resident at once) gives each of its waves -- a "wave worker" -- one equal,
-//   contiguous run of that list, so every wave streams the same number of K/V
-//   bytes whatever the mix of context lengths, and the whole call is a single
-//   wave of workgroups. Every K/V byte is read once and shared by the G =
-//   Hq/Hkv query heads of its kv head. Each workgroup derives the tile prefix
-//   over seq_lens itself (a block scan in LDS), so nothing is precomputed on
+//   unit-major. A fixed grid of workgroups (by default one 4-wave
+//   workgroup per CU, all resident at once) gives each of its waves -- a
+//   "wave worker" -- one equal, contiguous run of that list, so every wave
+//   streams the same number of K/V bytes whatever the mix of context
+//   lengths, and the whole call is a single wave of workgroups. Every K/V
+//   byte is read once and shared by the G = Hq/Hkv query heads of its kv
+//   head. Each wave derives the tile prefix over seq_lens itself (a
+//   wave-shuffle scan into its own LDS copy), so nothing is precomputed on
 //   the host.
 // * A wave crosses unit boundaries without stopping: its ring keeps loading
 //   the next unit's tiles (and that unit's Q) while the current unit
@@ -80,7 +81,7 @@ struct DecodeArgs {
 };
 
 // Waves per stream-kernel workgroup, and workgroups per CU of the default
-// grid (kWaves * kWgPerCu waves per CU in all).
+// grid (TSA_DECODE_WAVES * TSA_DECODE_WG_PER_CU waves per CU in all).
 #ifndef TSA_DECODE_WAVES
 #define TSA_DECODE_WAVES 4
 #endif
@@ -542,8 +543,9 @@ __global__ __launch_bounds__(64) void paged_decode_generic(DecodeArgs a) {
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Workgroups of the stream kernel: two per CU (the register budget lets two
-// 4-wave workgroups share a CU), so all of them are resident at once.
+// Workgroups of the stream kernel: TSA_DECODE_WG_PER_CU per CU (one by
+// default: one 4-wave workgroup per CU streams as fast as two, and with one
+// per CU no workgroup runs ahead of another on its CU), all resident at once.
 static int default_workgroups() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
