@@ -19,6 +19,8 @@
 // c ^ (D/16), one cross-lane exchange away. Rows are ordered token-major
 // (all Hq + Hkv heads of a token are adjacent) so a token's cos/sin and its
 // block-table lookup are shared by neighbouring lanes.
+#include <type_traits>
+
 #include "kv_store.h"
 
 namespace tsa {
@@ -85,53 +87,61 @@ __device__ __forceinline__ void store8(T* p, int64_t stride, const float (&v)[8]
 template <typename T>
 __device__ __forceinline__ float round_t(float x) { return to_float(from_float<T>(x)); }
 
-template <typename T, int D, bool VEC>
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs<T> a) {
+// Cross-lane moves inside the 16-lane rows of a wave (DPP, no LDS traffic):
+// lane i gets lane i + N of its row (row_shl), or lane (i - N) mod 16
+// (row_ror).
+template <int N>
+__device__ __forceinline__ float dpp_row_shl(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + N, 0xF, 0xF, true));
+}
+template <int N>
+__device__ __forceinline__ float dpp_row_ror(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x120 + N, 0xF, 0xF, false));
+}
+
+// One (token, head) row's norm + RoPE on the values already in registers.
+template <typename T, int D>
+__device__ __forceinline__ void norm_rope_row(const float (&x)[8], const float (&wf)[8], const float (&cs)[8],
+                                              const float (&sn)[8], float eps, int lane_in_row, float (&o)[8]) {
   constexpr int LANES = D / 8;  // lanes per (token, head) row
-  constexpr int ROWS = 256 / LANES;
-  const int lane_in_row = threadIdx.x % LANES;
-  const int64_t heads = a.Hq + a.Hkv;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * ROWS + threadIdx.x / LANES;
-  const bool live = row < a.T_ * heads;
-  // Dead lanes still join the cross-lane exchanges below (they read row 0).
-  const int64_t r = live ? row : 0;
-  const int64_t t = r / heads;
-  const int64_t hh = r - t * heads;
-  const bool is_k = hh >= a.Hq;
-  const int64_t h = is_k ? hh - a.Hq : hh;
-  const int d0 = lane_in_row * 8;
-
-  const T* src = is_k ? a.k + t * a.k_st + h * a.k_sh + d0 * a.k_sd : a.q + t * a.q_st + h * a.q_sh + d0 * a.q_sd;
-  const T* w = is_k ? a.kw + d0 * a.kw_s : a.qw + d0 * a.qw_s;
-  float x[8], wf[8], cs[8], sn[8];
-  load8<T, VEC>(src, is_k ? a.k_sd : a.q_sd, x);
-  load8<T, VEC>(w, is_k ? a.kw_s : a.qw_s, wf);
-  load8<T, VEC>(a.cos + t * a.cos_st + d0 * a.cos_sd, a.cos_sd, cs);
-  load8<T, VEC>(a.sin + t * a.sin_st + d0 * a.sin_sd, a.sin_sd, sn);
-
   // mean(x^2) in fp32, summed in the order of the CPU reduction the model's
   // RMSNorm runs through (four 8-wide accumulators over 32-element strides,
   // added in order, then the 8 lanes in order), so the rounded sum -- and the
   // bf16 results downstream of it -- match it bit for bit. Element 8c + e of
   // the row lives in lane c: accumulator k = c % 4 collects lanes k, k+4, ...
+  // (The sums are meaningful in lanes 0..3 of the row.)
   float sq[8], acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = sq[e] = __fmul_rn(x[e], x[e]);
-#pragma unroll
-  for (int step = 4; step < LANES; step += 4)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = __fadd_rn(acc[e], __shfl_down(sq[e], step, LANES));
   float ss = 0.f;
+  if constexpr (LANES == 16) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float v = acc[e];
+    for (int e = 0; e < 8; ++e) {
+      acc[e] = __fadd_rn(acc[e], dpp_row_shl<4>(sq[e]));
+      acc[e] = __fadd_rn(acc[e], dpp_row_shl<8>(sq[e]));
+      acc[e] = __fadd_rn(acc[e], dpp_row_shl<12>(sq[e]));
+      float v = acc[e];
+      v = __fadd_rn(v, dpp_row_shl<1>(acc[e]));
+      v = __fadd_rn(v, dpp_row_shl<2>(acc[e]));
+      v = __fadd_rn(v, dpp_row_shl<3>(acc[e]));
+      ss = __fadd_rn(ss, v);
+    }
+  } else {
 #pragma unroll
-    for (int k = 1; k < 4; ++k) v = __fadd_rn(v, __shfl_down(acc[e], k, LANES));
-    ss = __fadd_rn(ss, v);  // meaningful in lane 0 of the row
+    for (int step = 4; step < LANES; step += 4)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = __fadd_rn(acc[e], __shfl_down(sq[e], step, LANES));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[e];
+#pragma unroll
+      for (int k = 1; k < 4; ++k) v = __fadd_rn(v, __shfl_down(acc[e], k, LANES));
+      ss = __fadd_rn(ss, v);  // meaningful in lane 0 of the row
+    }
   }
   ss = __shfl(ss, 0, LANES);
   const float var = __fdiv_rn(ss, static_cast<float>(D));
-  const float rinv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, a.eps)));
+  const float rinv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
 
   float z[8];
 #pragma unroll
@@ -140,50 +150,166 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs<T> a) {
   // Partner half: lane c holds dims 8c..8c+7, dims +- D/2 are in lane c ^ (LANES/2).
   float zp[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) zp[i] = __shfl_xor(z[i], LANES / 2, 64);
+  for (int i = 0; i < 8; ++i) zp[i] = LANES == 16 ? dpp_row_ror<8>(z[i]) : __shfl_xor(z[i], LANES / 2, 64);
   const bool first_half = lane_in_row < LANES / 2;
-  float o[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float rot = first_half ? -zp[i] : zp[i];
     o[i] = round_t<T>(__fadd_rn(round_t<T>(__fmul_rn(z[i], cs[i])), round_t<T>(__fmul_rn(rot, sn[i]))));
   }
+}
+
+// One lane per 8 elements of a (token, head) row; rows are token-major. With
+// IDX32 (the host has checked every offset fits) the index arithmetic is
+// 32-bit, which is most of this kernel's integer work.
+template <typename T, int D, bool VEC, bool IDX32>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs<T> a) {
+  typedef typename std::conditional<IDX32, int32_t, int64_t>::type I;
+  constexpr int LANES = D / 8;  // lanes per (token, head) row
+  constexpr int ROWS = 256 / LANES;
+  const int lane_in_row = threadIdx.x % LANES;
+  const I heads = static_cast<I>(a.Hq + a.Hkv);
+  const I row = static_cast<I>(blockIdx.x) * ROWS + static_cast<I>(threadIdx.x / LANES);
+  const bool live = row < static_cast<I>(a.T_) * heads;
+  // Dead lanes still join the cross-lane exchanges below (they read row 0).
+  const I r = live ? row : 0;
+  const I t = IDX32 ? static_cast<I>(static_cast<uint32_t>(r) / static_cast<uint32_t>(heads)) : r / heads;
+  const I hh = r - t * heads;
+  const bool is_k = hh >= static_cast<I>(a.Hq);
+  const I h = is_k ? hh - static_cast<I>(a.Hq) : hh;
+  const int d0 = lane_in_row * 8;
+
+  const T* src = is_k ? a.k + (t * static_cast<I>(a.k_st) + h * static_cast<I>(a.k_sh) + d0 * static_cast<I>(a.k_sd))
+                      : a.q + (t * static_cast<I>(a.q_st) + h * static_cast<I>(a.q_sh) + d0 * static_cast<I>(a.q_sd));
+  const T* w = is_k ? a.kw + d0 * a.kw_s : a.qw + d0 * a.qw_s;
+  float x[8], wf[8], cs[8], sn[8], vv[8];
+  load8<T, VEC>(src, is_k ? a.k_sd : a.q_sd, x);
+  load8<T, VEC>(w, is_k ? a.kw_s : a.qw_s, wf);
+  load8<T, VEC>(a.cos + (t * static_cast<I>(a.cos_st) + d0 * static_cast<I>(a.cos_sd)), a.cos_sd, cs);
+  load8<T, VEC>(a.sin + (t * static_cast<I>(a.sin_st) + d0 * static_cast<I>(a.sin_sd)), a.sin_sd, sn);
+  // A stored k row: its V row and its cache slot are fetched before the math.
+  const bool store = a.k_cache != nullptr && is_k && live;
+  int64_t blk = 0, slot = 0;
+  bool placed = false;
+  if (store) {
+    load8<T, VEC>(a.v + (t * static_cast<I>(a.v_st) + h * static_cast<I>(a.v_sh) + d0 * static_cast<I>(a.v_sd)), a.v_sd,
+                  vv);
+    placed = a.addr.locate(t, a.BS, a.NB, blk, slot);
+  }
+
+  float o[8];
+  norm_rope_row<T, D>(x, wf, cs, sn, a.eps, lane_in_row, o);
   if (!live) return;
 
   if (!is_k) {
-    store8<T, VEC>(a.q_out + t * a.qo_st + h * a.qo_sh + d0 * a.qo_sd, a.qo_sd, o);
+    store8<T, VEC>(a.q_out + (t * static_cast<I>(a.qo_st) + h * static_cast<I>(a.qo_sh) + d0 * static_cast<I>(a.qo_sd)),
+                   a.qo_sd, o);
     return;
   }
-  if (a.k_out) store8<T, VEC>(a.k_out + t * a.ko_st + h * a.ko_sh + d0 * a.ko_sd, a.ko_sd, o);
-  if (a.k_cache) {
-    int64_t blk, slot;
-    if (!a.addr.locate(t, a.BS, a.NB, blk, slot)) return;
+  if (a.k_out)
+    store8<T, VEC>(a.k_out + (t * static_cast<I>(a.ko_st) + h * static_cast<I>(a.ko_sh) + d0 * static_cast<I>(a.ko_sd)),
+                   a.ko_sd, o);
+  if (placed) {
     store8<T, VEC>(a.k_cache + blk * a.kc_b + h * a.kc_h + slot * a.kc_s + d0 * a.kc_d, a.kc_d, o);
-    float vv[8];
-    load8<T, VEC>(a.v + t * a.v_st + h * a.v_sh + d0 * a.v_sd, a.v_sd, vv);
     store8<T, VEC>(a.v_cache + blk * a.vc_b + h * a.vc_h + slot * a.vc_s + d0 * a.vc_d, a.vc_d, vv);
   }
 }
 
 static bool vec_ok(const tsa_view* v) { return v == nullptr || v->data == nullptr || rows_vec16(v); }
 
+// Head-dim-128 path: one workgroup per token, 16 groups of 16 lanes; group g
+// takes the token's rows (heads, q first then k) g, g + 16, ..., at most R of
+// them. The token is workgroup-uniform, so its cos/sin are loaded once per
+// lane and its cache slot is found with scalar loads, and the rows of a lane
+// differ only by a head stride.
+template <typename T, int R>
+__global__ __launch_bounds__(256) void qk_norm_rope_token(NormRopeArgs<T> a) {
+  constexpr int D = 128;
+  const int t = blockIdx.x;
+  const int g = threadIdx.x >> 4, c = threadIdx.x & 15, d0 = 8 * c;
+  const int Hq = static_cast<int>(a.Hq), H = static_cast<int>(a.Hq + a.Hkv);
+  float qwf[8], kwf[8], cs[8], sn[8];
+  load8<T, true>(a.qw + d0, 1, qwf);
+  load8<T, true>(a.kw + d0, 1, kwf);
+  load8<T, true>(a.cos + t * a.cos_st + d0, 1, cs);
+  load8<T, true>(a.sin + t * a.sin_st + d0, 1, sn);
+  const T* qrow = a.q + t * a.q_st + d0;
+  const T* krow = a.k + t * a.k_st + d0;
+  const T* vrow = a.v + t * a.v_st + d0;
+  const bool store = a.k_cache != nullptr;
+  int64_t blk = 0, slot = 0;
+  const bool placed = store && a.addr.locate(t, a.BS, a.NB, blk, slot);
+
+  float x[R][8], vv[R][8];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int hh = min(g + 16 * j, H - 1);  // rows past the token's last head redo it (never stored)
+    if (hh < Hq) load8<T, true>(qrow + hh * a.q_sh, 1, x[j]);
+    else load8<T, true>(krow + (hh - Hq) * a.k_sh, 1, x[j]);
+    if (placed && hh >= Hq) load8<T, true>(vrow + (hh - Hq) * a.v_sh, 1, vv[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int hh = g + 16 * j;
+    const bool is_k = hh >= Hq;
+    float o[8];
+    norm_rope_row<T, D>(x[j], is_k ? kwf : qwf, cs, sn, a.eps, c, o);
+    if (hh >= H) continue;
+    if (!is_k) {
+      store8<T, true>(a.q_out + t * a.qo_st + hh * a.qo_sh + d0, 1, o);
+      continue;
+    }
+    const int h = hh - Hq;
+    if (a.k_out) store8<T, true>(a.k_out + t * a.ko_st + h * a.ko_sh + d0, 1, o);
+    if (placed) {
+      store8<T, true>(a.k_cache + blk * a.kc_b + h * a.kc_h + slot * a.kc_s + d0, 1, o);
+      store8<T, true>(a.v_cache + blk * a.vc_b + h * a.vc_h + slot * a.vc_s + d0, 1, vv[j]);
+    }
+  }
+}
+
+// Largest element offset a view reaches (0 for an absent view).
+static int64_t max_offset(const tsa_view* v) {
+  if (!v || !v->data) return 0;
+  int64_t m = 0;
+  for (int d = 0; d < v->ndim; ++d) m += (v->size[d] > 0 ? v->size[d] - 1 : 0) * (v->stride[d] < 0 ? -v->stride[d] : v->stride[d]);
+  return m;
+}
+
 template <typename T, int D>
-static int launch_norm_rope(const NormRopeArgs<T>& a, bool vec, hipStream_t stream) {
+static int launch_norm_rope(const NormRopeArgs<T>& a, bool vec, bool idx32, hipStream_t stream) {
   constexpr int ROWS = 256 / (D / 8);
   const int64_t rows = a.T_ * (a.Hq + a.Hkv);
   if (rows == 0) return TSA_OK;
+  // Unit innermost strides everywhere (vec) and at most 80 heads per token:
+  // the token-per-workgroup kernel.
+  const int64_t H = a.Hq + a.Hkv;
+  if constexpr (D == 128) {
+    if (vec && a.T_ <= INT32_MAX && H <= 80) {
+      const dim3 grid(static_cast<uint32_t>(a.T_));
+      switch ((H + 15) / 16) {
+        case 1: qk_norm_rope_token<T, 1><<<grid, dim3(256), 0, stream>>>(a); break;
+        case 2: qk_norm_rope_token<T, 2><<<grid, dim3(256), 0, stream>>>(a); break;
+        case 3: qk_norm_rope_token<T, 3><<<grid, dim3(256), 0, stream>>>(a); break;
+        case 4: qk_norm_rope_token<T, 4><<<grid, dim3(256), 0, stream>>>(a); break;
+        default: qk_norm_rope_token<T, 5><<<grid, dim3(256), 0, stream>>>(a); break;
+      }
+      return check_launch("tsa_qk_norm_rope");
+    }
+  }
   const dim3 grid((rows + ROWS - 1) / ROWS);
-  if (vec) qk_norm_rope_kernel<T, D, true><<<grid, dim3(256), 0, stream>>>(a);
-  else qk_norm_rope_kernel<T, D, false><<<grid, dim3(256), 0, stream>>>(a);
+  if (vec && idx32) qk_norm_rope_kernel<T, D, true, true><<<grid, dim3(256), 0, stream>>>(a);
+  else if (vec) qk_norm_rope_kernel<T, D, true, false><<<grid, dim3(256), 0, stream>>>(a);
+  else qk_norm_rope_kernel<T, D, false, false><<<grid, dim3(256), 0, stream>>>(a);
   return check_launch("tsa_qk_norm_rope");
 }
 
 template <typename T>
-static int run_norm_rope(NormRopeArgs<T>& a, int64_t D, bool vec, hipStream_t stream) {
+static int run_norm_rope(NormRopeArgs<T>& a, int64_t D, bool vec, bool idx32, hipStream_t stream) {
   switch (D) {
-    case 64: return launch_norm_rope<T, 64>(a, vec, stream);
-    case 128: return launch_norm_rope<T, 128>(a, vec, stream);
-    case 256: return launch_norm_rope<T, 256>(a, vec, stream);
+    case 64: return launch_norm_rope<T, 64>(a, vec, idx32, stream);
+    case 128: return launch_norm_rope<T, 128>(a, vec, idx32, stream);
+    case 256: return launch_norm_rope<T, 256>(a, vec, idx32, stream);
   }
   set_error("tsa_qk_norm_rope: head_dim %lld is not implemented (64, 128, 256)", (long long)D);
   return TSA_ERR_UNSUPPORTED;
@@ -227,7 +353,13 @@ static int norm_rope_entry(const tsa_view* q, const tsa_view* k, const tsa_view*
     a.addr = *addr;
     vec = vec && vec_ok(v) && vec_ok(k_cache) && vec_ok(v_cache);
   }
-  return run_norm_rope<T>(a, q->size[2], vec, stream);
+  // 32-bit index arithmetic when every row index and every offset into the
+  // token-major tensors fits (the cache offsets stay 64-bit).
+  const int64_t lim = int64_t{1} << 31;
+  const bool idx32 = a.T_ * (a.Hq + a.Hkv) < lim && max_offset(q) < lim && max_offset(k) < lim &&
+                     max_offset(q_out) < lim && max_offset(k_out) < lim && max_offset(cos) < lim &&
+                     max_offset(sin) < lim && max_offset(v) < lim;
+  return run_norm_rope<T>(a, q->size[2], vec, idx32, stream);
 }
 
 static int check_norm_rope(const tsa_view* q, const tsa_view* k, const tsa_view* q_out, const tsa_view* k_out,
