@@ -308,11 +308,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   // A blocks ahead. Lane l of a load whose first row is R0 fetches the chunk
   // that belongs at row R0 + l / CPR, position l % CPR. Block step s moves K
   // block s + 1 and V block s, IPW loads per wave: waves 0 .. NW/2 - 1 the K
-  // rows, the others the V rows. Rows past the sequence's end re-read its
-  // last key, which the mask or a zero probability then ignores. Slots are
-  // taken by the nominal block number, so a step past the last block (its
-  // rows clamped) still writes a free slot and every wave issues the same
-  // number of loads per step.
+  // rows, the others the V rows; every wave issues the same number of loads
+  // per step. Rows past the sequence's end re-read its last key, which the
+  // mask or a zero probability then ignores; so does the last step's K block
+  // (one past the end, a clamped copy of the last block). Slots are taken by
+  // the nominal block number.
   typedef __attribute__((address_space(3))) void lds_void;
   auto clampb = [&](int blk) { return blk < nblk ? blk : nblk - 1; };
   const bool k_wave = wave < NW / 2;
@@ -469,8 +469,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   // exponentials of S(j), so the matrix pipe and the VALU work at once, and
   // finally P(j) V(j). It then waits for step j + 1's rows and meets the
   // other waves at the barrier.
+  // Steps past the last block are not issued; once they stop, fewer loads
+  // than kInFlight are younger than the one a block needs, so those blocks
+  // wait for all of them (they are needed within a block or two anyway).
   auto full = [&](int j, f32x16& cur, f32x16& nxt) {
-    load_step(j + A);
+    const bool issue = j + A < nblk;
+    if (issue) load_step(j + A);
     kread((j + 1) % NB);
     softmax_max(cur, j);
     qk(nxt);
@@ -482,7 +486,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
       __builtin_amdgcn_sched_group_barrier(0x002, 64 / KJ, 0);
     }
     pv(j % NB);
-    wait_loads(std::integral_constant<int, kInFlight>{});
+    if (issue) wait_loads(std::integral_constant<int, kInFlight>{});
+    else wait_loads(std::integral_constant<int, 0>{});
     lds_barrier();
   };
   auto last = [&](int j, f32x16& cur) {
@@ -491,11 +496,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     pv(j % NB);
   };
   if (nblk > 0) {
-    // K block 0, then steps 0 .. A - 1; wait for K(0) and step 0.
+    // K block 0, then steps 0 .. A - 1 (those that exist); wait for K(0)
+    // and step 0.
     if (k_wave) load_block(0, 0);
 #pragma unroll
-    for (int s0 = 0; s0 < A; ++s0) load_step(s0);
-    wait_loads(std::integral_constant<int, kInFlight>{});
+    for (int s0 = 0; s0 < A; ++s0)
+      if (s0 < nblk) load_step(s0);
+    if (nblk >= A) wait_loads(std::integral_constant<int, kInFlight>{});
+    else wait_loads(std::integral_constant<int, 0>{});
     lds_barrier();
     f32x16 sca, scb;  // S of the even / odd blocks
     kread(0);
@@ -513,8 +521,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     } else {
       last(j, sca);
     }
-    // Clamped loads past the last block may still be landing in LDS.
-    wait_loads(std::integral_constant<int, 0>{});
+    // (Every load has landed: the last blocks waited for all of them.)
     lds_barrier();
   }
 
