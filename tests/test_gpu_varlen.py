@@ -93,6 +93,37 @@ def test_q_len_differs_from_k_len(causal):
     assert_close(out, ref, what=f"lq!=lk causal={causal}")
 
 
+def test_sequence_without_keys():
+    """A sequence with queries but no keys: 0/0 (NaN) rows, as the reference's
+    l = 0 division gives; the other sequence is unaffected."""
+    lq, lk = [16, 40], [0, 50]
+    q, k, v, cq, ck = _inputs(lq, lk, 8, 2, 128, torch.bfloat16, seed=13)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cq.to(DEV), ck.to(DEV), max(lq), max(lk),
+                                 False).cpu()
+    ref = ov.flash_attn_varlen_func(q, k, v, cq, ck, max(lq), max(lk), False)
+    assert torch.isnan(ref[:16]).all() and torch.isnan(out[:16]).all()
+    assert_close(out[16:], ref[16:], what="sequence after an empty one")
+
+
+def test_repeated_calls_are_identical():
+    """More calls than the persistent kernel's work-queue slots, two shapes
+    interleaved: every call claims each work item exactly once, so every
+    output is bit-identical to the first call's."""
+    lens_a, lens_b = [300, 17, 1000, 64], [33, 700]
+    qa, ka, va, ca, _ = _inputs(lens_a, lens_a, 32, 8, 128, torch.bfloat16, seed=21)
+    qb, kb, vb, cb, _ = _inputs(lens_b, lens_b, 32, 8, 128, torch.bfloat16, seed=22)
+    qa, ka, va, ca = qa.to(DEV), ka.to(DEV), va.to(DEV), ca.to(DEV)
+    qb, kb, vb, cb = qb.to(DEV), kb.to(DEV), vb.to(DEV), cb.to(DEV)
+    first_a = flash_attn_varlen_func(qa, ka, va, ca, ca, max(lens_a), max(lens_a), True)
+    first_b = flash_attn_varlen_func(qb, kb, vb, cb, cb, max(lens_b), max(lens_b), True)
+    for _ in range(40):
+        oa = flash_attn_varlen_func(qa, ka, va, ca, ca, max(lens_a), max(lens_a), True)
+        ob = flash_attn_varlen_func(qb, kb, vb, cb, cb, max(lens_b), max(lens_b), True)
+        assert torch.equal(oa, first_a) and torch.equal(ob, first_b)
+    ref = ov.flash_attn_varlen_func(qa.cpu(), ka.cpu(), va.cpu(), ca.cpu(), ca.cpu(), max(lens_a), max(lens_a), True)
+    assert_close(first_a.cpu(), ref, what="repeated calls")
+
+
 def test_single_token_sequences_return_v():
     lens = [1, 1, 1]
     q, k, v, cu, _ = _inputs(lens, lens, 8, 2, 128, torch.bfloat16, seed=5)

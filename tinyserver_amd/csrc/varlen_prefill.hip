@@ -16,6 +16,7 @@
 //                        strides: one wave per (query, q-head), fp32 VALU.
 // Causal key blocks past a workgroup's last query are never visited, and the
 // heaviest query blocks are dispatched first.
+#include <atomic>
 #include <cmath>
 #include <type_traits>
 
@@ -39,7 +40,17 @@ struct PrefillArgs {
   int32_t nseq, Hq, Hkv, G, D, nqb;
   int32_t causal;
   float scale_log2;
+  int32_t queue;  // work-queue slot of this call (persistent kernel)
 };
+
+// Work queue of the persistent kernel: per call a slot holding the next work
+// item and the number of workgroups done. The last workgroup to finish puts
+// both back to zero, and consecutive calls take consecutive slots, so calls
+// in flight on different streams do not share one.
+constexpr int kQueueSlots = 64;
+__device__ unsigned int g_prefill_queue[kQueueSlots][2];
+// Sequences per call the persistent kernel keeps counts of in LDS.
+constexpr int max_persist_seqs(int nw) { return nw == 2 ? 1024 : 2048; }
 
 constexpr float kNegInfP = -INFINITY;
 
@@ -227,7 +238,8 @@ __global__ __launch_bounds__(256) void varlen_prefill_mfma(PrefillArgs a) {
 // put the kv head fastest (a kv head's query blocks share one XCD's L2) and
 // the heaviest query blocks first.
 template <typename T, int D, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void varlen_prefill_gqa(PrefillArgs a) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void varlen_prefill_gqa(
+    PrefillArgs a, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
   constexpr int KJ = D / 16;              // 16-dim steps of the QK reduction
   constexpr int NU = D / 32;              // 32-dim column tiles of the output
   constexpr int CPR = D / 8;              // 16-byte chunks per K/V row
@@ -239,65 +251,107 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   constexpr int NB = NW == 2 ? 2 : 4, A = NB - 1;
   constexpr int RPI = 1024 / RB;          // rows per 1 KB load instruction
   constexpr int IPW = 2 * (32 / RPI) / NW;  // load instructions per wave per block step
-  constexpr int SMEM = NB * 2 * BLKB > NW * 32 * ROWO * 2 ? NB * 2 * BLKB : NW * 32 * ROWO * 2;  // bytes
+  constexpr int VOFF = NB * BLKB;           // byte offset of the V slots
+  constexpr int OOFF = 2 * NB * BLKB;       // byte offset of the output staging (8 rows per wave)
+  constexpr int QOFF = OOFF + NW * 8 * ROWO * 2;  // byte offset of the per-sequence query-block counts
+  constexpr int IOFF = QOFF + max_persist_seqs(NW) * 2;  // byte offset of the published item index
+  constexpr int SMEM = IOFF + 16;
   static_assert(IPW >= 1 && IPW * NW == 2 * (32 / RPI), "a block step is a whole number of loads per wave");
   static_assert((A > 1 ? A - 1 : 0) * IPW <= 63, "outstanding loads fit the vmcnt field");
   // A row's running max only moves when it grows by more than this (log2
   // units): p = 2^(s - m) then stays below 2^8, and the accumulator is
   // rescaled rarely. l uses the same m, so the result is unchanged.
   constexpr float kRescale = 8.0f;
-  // K slots [NB][32 rows][RB], then V slots; afterwards the output tiles.
   __shared__ __align__(16) char smem[SMEM];
-  constexpr int VOFF = NB * BLKB;           // byte offset of the V slots
+  uint16_t* const nqb_s = reinterpret_cast<uint16_t*>(smem + QOFF);  // query blocks of each sequence
+  int* const item_s = reinterpret_cast<int*>(smem + IOFF);           // the next item, published to all waves
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  constexpr int QB = 32;  // queries per workgroup
-  const int id = blockIdx.x;
-  const int kvh = id % a.Hkv;
-  const int rest = id / a.Hkv;
-  const int b = rest % a.nseq;
-  const int qblk = a.nqb - 1 - rest / a.nseq;
-  int64_t q_start64, q_len64, k_start64, k_len64;
-  seq_range(a.cu_q, a.cuq_s, b, a.total_q, q_start64, q_len64);
-  seq_range(a.cu_k, a.cuk_s, b, a.total_k, k_start64, k_len64);
-  // Positions inside one sequence fit 32 bits (cu_seqlens are int32).
-  const int q_len = static_cast<int>(q_len64), k_len = static_cast<int>(k_len64);
-  const int row0 = qblk * QB;
-  if (row0 >= q_len) return;
-
-  const T* kb_ptr = static_cast<const T*>(a.k) + k_start64 * a.k_st + kvh * a.k_sh;
-  const T* vb_ptr = static_cast<const T*>(a.v) + k_start64 * a.v_st + kvh * a.v_sh;
+  const int nseq = a.nseq, Hkv = a.Hkv;
   const float cs = a.scale_log2;  // > 0 on this path
+  unsigned int* const queue = g_prefill_queue[a.queue];
 
-  // This wave's tile: queries q0..q0+31 of q-head `head`.
-  const int q0 = row0;
-  const int head = kvh * NW + wave;
-  u32x4 qop[KJ];
-  {
-    const int row = q0 + c;
-    const T* qp = static_cast<const T*>(a.q) + (q_start64 + row) * a.q_st + head * a.q_sh;
-#pragma unroll
-    for (int jj = 0; jj < KJ; ++jj)
-      qop[jj] = row < q_len ? *reinterpret_cast<const u32x4*>(qp + 16 * jj + 8 * h) : u32x4{0, 0, 0, 0};
+  // ---- Work items: (query block, sequence, kv head) with a non-empty query
+  // block, heaviest (latest) query blocks first: level Q holds query block Q
+  // of every sequence that has one, in sequence order, kv head fastest. Items
+  // are handed out one at a time through an atomic counter, so workgroups
+  // that run fast take more; the per-sequence counts live in LDS.
+  for (int b = tid; b < nseq; b += 64 * NW) {
+    int64_t qs, ql;
+    seq_range(cu_q, a.cuq_s, b, a.total_q, qs, ql);
+    nqb_s[b] = static_cast<uint16_t>((ql + 31) / 32);
   }
-
-  float m = kNegInfP, l = 0.f;  // query c's running max (log2 domain) and this lane's share of its sum
-  f32x16 acc[NU];
+  if (tid == 0) item_s[0] = static_cast<int>(atomicAdd(queue, 1u));
+  __syncthreads();
+  // Items above level Q: Hkv * sum_b max(0, nqb_b - Q - 1) (wave reduction).
+  auto items_above = [&](int Q) {
+    int sum = 0;
+    for (int b = lane; b < nseq; b += 64) sum += max(0, static_cast<int>(nqb_s[b]) - Q - 1);
 #pragma unroll
-  for (int u = 0; u < NU; ++u)
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    return __builtin_amdgcn_readfirstlane(sum) * Hkv;
+  };
+  int qb_max = 0;
+  for (int b = lane; b < nseq; b += 64) qb_max = max(qb_max, static_cast<int>(nqb_s[b]));
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[u][e] = 0.f;
+  for (int off = 32; off >= 1; off >>= 1) qb_max = max(qb_max, __shfl_xor(qb_max, off, 64));
+  qb_max = __builtin_amdgcn_readfirstlane(qb_max);
+  const int n_items = items_above(-1);
 
-  const int q_last = row0 + QB < q_len ? row0 + QB : q_len;  // one past the block's last query
-  const int kend = a.causal ? (k_len < q_last ? k_len : q_last) : k_len;
-  const int nblk = (kend + 31) / 32;
+  struct Item {
+    int b, kvh, q0, q_len, k_len, nblk;
+    int64_t q_start;
+    const T* kb;
+    const T* vb;
+  };
+  // Item i -> its level (the smallest Q with items_above(Q) <= i), then the
+  // sequence of rank (i - items_above(Q)) / Hkv among those with nqb > Q.
+  auto resolve = [&](int i, Item& it) {
+    int lo = 0, hi = qb_max - 1;  // answer in [lo, hi]
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (items_above(mid) <= i) hi = mid; else lo = mid + 1;
+    }
+    const int Q = lo;
+    const int r = i - items_above(Q);
+    int rank = r / Hkv;
+    it.kvh = r - rank * Hkv;
+    int b = 0;
+    for (int base = 0; base < nseq; base += 64) {
+      const int bb = base + lane;
+      const uint64_t m = __ballot(bb < nseq && static_cast<int>(nqb_s[bb]) > Q);
+      const int cnt = __builtin_popcountll(m);
+      if (rank < cnt) {
+        // the rank-th set bit of m
+        uint64_t mm = m;
+        for (int k = 0; k < rank; ++k) mm &= mm - 1;
+        b = base + __builtin_ctzll(mm);
+        break;
+      }
+      rank -= cnt;
+    }
+    it.b = __builtin_amdgcn_readfirstlane(b);
+    int64_t qs, ql, ks, kl;
+    seq_range(cu_q, a.cuq_s, it.b, a.total_q, qs, ql);
+    seq_range(cu_k, a.cuk_s, it.b, a.total_k, ks, kl);
+    it.q_start = qs;
+    it.q_len = static_cast<int>(ql);
+    it.k_len = static_cast<int>(kl);
+    it.q0 = Q * 32;
+    const int q_last = it.q0 + 32 < it.q_len ? it.q0 + 32 : it.q_len;
+    const int kend = a.causal ? (it.k_len < q_last ? it.k_len : q_last) : it.k_len;
+    it.nblk = (kend + 31) / 32;
+    it.kb = static_cast<const T*>(a.k) + ks * a.k_st + it.kvh * a.k_sh;
+    it.vb = static_cast<const T*>(a.v) + ks * a.v_st + it.kvh * a.v_sh;
+  };
 
-  // K/V rows are stored unpadded, RB bytes each, with the 16-byte chunk ch
-  // of row r at position ch ^ swz(r). swz is a bijection on r % 16, so the
-  // 16 lanes of a K operand read (16 rows, one chunk) hit 16 distinct bank
-  // quads, and it maps r % 4 to the upper bits, so a transposed V read (4
-  // consecutive rows x 2 chunks per 16 lanes) is conflict-free as well.
+  // ---- LDS layout of K/V: rows are stored unpadded, RB bytes each, with the
+  // 16-byte chunk ch of row r at position ch ^ swz(r). swz is a bijection on
+  // r % 16, so the 16 lanes of a K operand read (16 rows, one chunk) hit 16
+  // distinct bank quads, and it maps r % 4 to the upper bits, so a
+  // transposed V read (4 consecutive rows x 2 chunks per 16 lanes) is
+  // conflict-free as well.
   auto swz = [](int r) {
     return D == 128 ? ((r & 3) << 2) | ((r >> 2) & 3) : (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
   };
@@ -311,14 +365,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   // rows, the others the V rows; every wave issues the same number of loads
   // per step. Rows past the sequence's end re-read its last key, which the
   // mask or a zero probability then ignores; so does the last step's K block
-  // (one past the end, a clamped copy of the last block). Slots are taken by
-  // the nominal block number.
+  // (one past the end, a clamped copy of the last block). Blocks take slots
+  // in order across items: block j of an item whose first block is the
+  // workgroup's g-th goes to slot (g + j) % NB.
   typedef __attribute__((address_space(3))) void lds_void;
-  auto clampb = [&](int blk) { return blk < nblk ? blk : nblk - 1; };
   const bool k_wave = wave < NW / 2;
   const int row0w = (wave % (NW / 2)) * IPW * RPI;  // first row this wave loads
   const int64_t st_b = (k_wave ? a.k_st : a.v_st) * static_cast<int64_t>(sizeof(T));
-  const char* const gbase = reinterpret_cast<const char*>(k_wave ? kb_ptr : vb_ptr);
   const int lrow = lane / CPR;
   auto lane_chunk = [&](int i) { return (lane % CPR) ^ swz(row0w + i * RPI + lrow); };
   uint32_t doff[IPW];  // lane byte offsets from the first row of load i (< 2^32: strides checked on the host)
@@ -339,28 +392,40 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(smem_lds + lds_byte)
                  : "memory", "m0");
   };
-  // This wave's loads of block blk (K if k_wave) into slot `slot`.
-  auto load_block = [&](int blk, int slot) __attribute__((always_inline)) {
-    const int key0 = clampb(blk) * 32 + row0w;
+  // This wave's loads of block blk of item `it` (K if k_wave) into slot `slot`.
+  auto load_block = [&](const Item& it, int blk, int slot) __attribute__((always_inline)) {
+    const int key0 = min(blk, it.nblk - 1) * 32 + row0w;
     const int lds0 = (k_wave ? 0 : VOFF) + slot * BLKB + row0w * RB;
-    if (key0 + IPW * RPI <= k_len) {
+    const char* gbase = reinterpret_cast<const char*>(k_wave ? it.kb : it.vb);
+    if (key0 + IPW * RPI <= it.k_len) {
       const char* src = gbase + key0 * st_b;
 #pragma unroll
       for (int i = 0; i < IPW; ++i) dma(src + i * RPI * st_b, doff[i], lds0 + i * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < IPW; ++i) {
-        const int key = min(key0 + i * RPI + lrow, k_len - 1);
+        const int key = min(key0 + i * RPI + lrow, it.k_len - 1);
         dma64(gbase + key * st_b + 16 * lane_chunk(i), lds0 + i * 1024);
       }
     }
   };
-  auto load_step = [&](int s) __attribute__((always_inline)) {
-    if (k_wave) load_block(s + 1, (s + 1) % NB);
-    else load_block(s, s % NB);
+  // Block step s of item `it` (first block: the workgroup's g-th).
+  auto load_step = [&](const Item& it, int g, int s) __attribute__((always_inline)) {
+    if (k_wave) load_block(it, s + 1, (g + s + 1) % NB);
+    else load_block(it, s, (g + s) % NB);
+  };
+  // K block 0 and steps 0 .. A - 1 (those that exist) of an item; nothing
+  // for an item without keys.
+  auto load_head = [&](const Item& it, int g) __attribute__((always_inline)) {
+    if (it.nblk == 0) return;
+    if (k_wave) load_block(it, 0, g % NB);
+#pragma unroll
+    for (int s0 = 0; s0 < A; ++s0)
+      if (s0 < it.nblk) load_step(it, g, s0);
   };
   // Wait until at most n of this wave's loads are in flight (they complete
-  // in issue order).
+  // in issue order; other memory operations issued among them only make the
+  // wait stricter).
   auto wait_loads = [&](auto n) {
     constexpr int N = decltype(n)::value;
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
@@ -368,6 +433,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   constexpr int kInFlight = (A - 1) * IPW;  // loads of the later steps, still in flight at a block's end
 
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+  // Q operand of the item (lane (h, c): query q0 + c, dims 16jj + 8h..+8).
+  u32x4 qop[KJ];
+  auto load_q = [&](const Item& it) {
+    const int row = it.q0 + c;
+    const int head = it.kvh * NW + wave;
+    const T* qp = static_cast<const T*>(a.q) + (it.q_start + row) * a.q_st + head * a.q_sh;
+#pragma unroll
+    for (int jj = 0; jj < KJ; ++jj)
+      qop[jj] = row < it.q_len ? *reinterpret_cast<const u32x4*>(qp + 16 * jj + 8 * h) : u32x4{0, 0, 0, 0};
+  };
 
   // K operands of the block in slot ks: lane (h, c) reads key c, dims
   // 16jj + 8h..+8, i.e. chunk 2jj + h at position (2jj + h) ^ swz(c): byte
@@ -387,17 +463,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
     for (int jj = 0; jj < KJ; ++jj) sc = mfma_k16x32<T>(kop[jj], qop[jj], sc);
   };
+  float m = kNegInfP, l = 0.f;  // query c's running max (log2 domain) and this lane's share of its sum
+  f32x16 acc[NU];
   // Masking, the running max and the (rare) rescale for block blk's scores.
-  auto softmax_max = [&](f32x16& sc, int blk) {
+  auto softmax_max = [&](const Item& it, f32x16& sc, int blk) {
     const int kb0 = blk * 32;
     // Keys past k_len, and (causal) keys after the query, only occur in a
     // sequence's last block or on the diagonal: a wave-uniform branch.
-    if (kb0 + 32 > k_len || (a.causal && kb0 + 31 > q0)) {
-      const int qq = q0 + c;
+    if (kb0 + 32 > it.k_len || (a.causal && kb0 + 31 > it.q0)) {
+      const int qq = it.q0 + c;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int kk = kb0 + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (!(kk < k_len && (!a.causal || kk <= qq))) sc[e] = kNegInfP;
+        if (!(kk < it.k_len && (!a.causal || kk <= qq))) sc[e] = kNegInfP;
       }
     }
     float tmax = kNegInfP;
@@ -468,15 +546,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   // max/rescale of S(j), then issues the S(j + 1) MFMAs interleaved with the
   // exponentials of S(j), so the matrix pipe and the VALU work at once, and
   // finally P(j) V(j). It then waits for step j + 1's rows and meets the
-  // other waves at the barrier.
-  // Steps past the last block are not issued; once they stop, fewer loads
-  // than kInFlight are younger than the one a block needs, so those blocks
-  // wait for all of them (they are needed within a block or two anyway).
-  auto full = [&](int j, f32x16& cur, f32x16& nxt) {
-    const bool issue = j + A < nblk;
-    if (issue) load_step(j + A);
-    kread((j + 1) % NB);
-    softmax_max(cur, j);
+  // other waves at the barrier. Steps past the last block are not issued;
+  // once they stop, fewer loads than kInFlight are younger than the one a
+  // block needs, so those blocks wait for all of them.
+  auto full = [&](const Item& it, int g, int j, f32x16& cur, f32x16& nxt) {
+    const bool issue = j + A < it.nblk;
+    if (issue) load_step(it, g, j + A);
+    kread((g + j + 1) % NB);
+    softmax_max(it, cur, j);
     qk(nxt);
     softmax_exp(cur);
     // One score MFMA, then a slice of the exponentials, and so on.
@@ -485,71 +562,118 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 64 / KJ, 0);
     }
-    pv(j % NB);
+    pv((g + j) % NB);
     if (issue) wait_loads(std::integral_constant<int, kInFlight>{});
     else wait_loads(std::integral_constant<int, 0>{});
     lds_barrier();
   };
-  auto last = [&](int j, f32x16& cur) {
-    softmax_max(cur, j);
-    softmax_exp(cur);
-    pv(j % NB);
-  };
-  if (nblk > 0) {
-    // K block 0, then steps 0 .. A - 1 (those that exist); wait for K(0)
-    // and step 0.
-    if (k_wave) load_block(0, 0);
+  // The output tile of a finished item, normalised and stored through this
+  // wave's 8-row staging area in four rounds of 8 rows, as 16-byte chunks.
+  uint16_t* const ost = reinterpret_cast<uint16_t*>(smem + OOFF) + wave * 8 * ROWO;
+  auto store_out = [&](const Item& it) {
+    const float rl = 1.f / (l + __shfl_xor(l, 32, 64));  // 1 / query c's denominator
+    T* const obase = static_cast<T*>(a.out) + it.q_start * a.o_st + (it.kvh * NW + wave) * a.o_sh;
 #pragma unroll
-    for (int s0 = 0; s0 < A; ++s0)
-      if (s0 < nblk) load_step(s0);
-    if (nblk >= A) wait_loads(std::integral_constant<int, kInFlight>{});
+    for (int R = 0; R < 4; ++R) {
+      __builtin_amdgcn_sched_barrier(0);  // one round's addresses at a time
+#pragma unroll
+      for (int e = 4 * R; e < 4 * R + 4; ++e) {
+        const int rr = 4 * h + (e & 3);  // row inside the round
+        const float sc = __shfl(rl, 8 * R + rr, 64);
+#pragma unroll
+        for (int u = 0; u < NU; ++u) ost[rr * ROWO + 32 * u + c] = from_float<T>(acc[u][e] * sc).x;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+      for (int i = 0; i < 8 * CPR / 64; ++i) {
+        const int chunk = lane + 64 * i;
+        const int r = chunk / CPR, ch = chunk % CPR;
+        const int row = it.q0 + 8 * R + r;
+        const u32x4 w = *reinterpret_cast<const u32x4*>(ost + r * ROWO + 8 * ch);
+        if (row < it.q_len) *reinterpret_cast<u32x4*>(obase + row * a.o_st + 8 * ch) = w;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    }
+  };
+
+  // ---- The item loop. While item X computes, the atomic that claims the
+  // next item is in flight; it is read once X's last loads have landed, and
+  // the next item's K/V blocks and Q are fetched while X's last block and its
+  // output are finished, so its first block is usually in LDS when it starts.
+  int idx = item_s[0];
+  Item X;
+  if (idx < n_items) {
+    resolve(idx, X);
+    load_q(X);
+    load_head(X, 0);
+  }
+  int g = 0;  // slot counter: X's block 0 is the workgroup's g-th block
+  while (idx < n_items) {
+    // (item_s is rewritten below only after this loop's barriers, so every
+    // wave has read the current value by then.)
+    unsigned int next_raw = 0;
+    if (tid == 0) next_raw = atomicAdd(queue, 1u);
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[u][e] = 0.f;
+    m = kNegInfP;
+    l = 0.f;
+    // X's K(0) and step 0 (steps 1 .. A-1 may still be in flight).
+    if (X.nblk >= A) wait_loads(std::integral_constant<int, kInFlight>{});
     else wait_loads(std::integral_constant<int, 0>{});
     lds_barrier();
     f32x16 sca, scb;  // S of the even / odd blocks
-    kread(0);
-    qk(sca);
+    if (X.nblk > 0) {
+      kread(g % NB);
+      qk(sca);
+    }
     // Iteration 0's loads overwrite K(0)'s slot: every wave must have read it.
     lds_barrier();
     int j = 0;
-    for (; j + 2 < nblk; j += 2) {
-      full(j, sca, scb);
-      full(j + 1, scb, sca);
+    for (; j + 2 < X.nblk; j += 2) {
+      full(X, g, j, sca, scb);
+      full(X, g, j + 1, scb, sca);
     }
-    if (j + 1 < nblk) {
-      full(j, sca, scb);
-      last(j + 1, scb);
-    } else {
-      last(j, sca);
+    if (j + 1 < X.nblk) {
+      full(X, g, j, sca, scb);
+      sca = scb;  // the last block's scores, in one place
+      ++j;
     }
-    // (Every load has landed: the last blocks waited for all of them.)
+    // X's last block j, after all of X's loads have landed (and the claim
+    // with them): publish the next item, fetch its blocks and Q behind X's
+    // last block, then store X's output.
+    if (tid == 0) item_s[0] = static_cast<int>(next_raw);
     lds_barrier();
+    const int nidx = item_s[0];
+    Item Y;
+    if (nidx < n_items) resolve(nidx, Y);
+    // (An item without keys has no block: its output is 0/0, as the
+    // reference's.)
+    if (X.nblk > 0) {
+      softmax_max(X, sca, j);
+      softmax_exp(sca);
+    }
+    if (nidx < n_items) {
+      load_head(Y, g + X.nblk);
+      load_q(Y);
+    }
+    if (X.nblk > 0) pv((g + j) % NB);
+    store_out(X);
+    g += X.nblk;
+    X = Y;
+    idx = nidx;
   }
-
-  // Output: each wave stages its 32 x D tile in its own slice of the (now
-  // idle) K/V buffers and stores it as 16-byte row chunks. The loop ended on
-  // a workgroup barrier after every wave's last read of the K/V buffers.
-  if (q0 >= q_len) return;
-  uint16_t* ost = reinterpret_cast<uint16_t*>(smem) + wave * 32 * ROWO;
-  const float rl = 1.f / (l + __shfl_xor(l, 32, 64));  // 1 / query c's denominator
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int r = 8 * (e >> 2) + 4 * h + (e & 3);
-    const float rr = __shfl(rl, r, 64);
-#pragma unroll
-    for (int u = 0; u < NU; ++u) ost[r * ROWO + 32 * u + c] = from_float<T>(acc[u][e] * rr).x;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-#pragma unroll
-  for (int i = 0; i < 32 * CPR / 64; ++i) {
-    const int chunk = lane + 64 * i;
-    const int r = chunk / CPR, ch = chunk % CPR;
-    const int row = q0 + r;
-    const u32x4 w = *reinterpret_cast<const u32x4*>(ost + r * ROWO + 8 * ch);
-    if (row < q_len) {
-      T* op = static_cast<T*>(a.out) + (q_start64 + row) * a.o_st + head * a.o_sh + 8 * ch;
-      *reinterpret_cast<u32x4*>(op) = w;
+  // The last workgroup to finish resets this call's queue slot.
+  if (tid == 0) {
+    const unsigned int done = atomicAdd(queue + 1, 1u);
+    if (done == gridDim.x - 1) {
+      queue[0] = 0;
+      queue[1] = 0;
     }
   }
 }
@@ -620,6 +744,25 @@ __global__ __launch_bounds__(64) void varlen_prefill_generic(PrefillArgs a, int6
   }
 }
 
+// The persistent kernel runs as many workgroups as fit on the device at once
+// (the occupancy the compiler's resources allow, times the CU count).
+template <typename T, int D, int NW>
+static int launch_persistent(const PrefillArgs& a, hipStream_t stream) {
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, varlen_prefill_gqa<T, D, NW>, 64 * NW, 0) != hipSuccess || n <= 0)
+      n = 1;
+    per_cu = n;
+  }
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  varlen_prefill_gqa<T, D, NW><<<dim3(per_cu * cus), dim3(64 * NW), 0, stream>>>(a, a.cu_q, a.cu_k);
+  return check_launch("tsa_varlen_prefill");
+}
+
 template <typename T>
 static int launch_prefill(PrefillArgs& a, bool mfma, int64_t total_q, int64_t max_seqlen_q, hipStream_t stream) {
   if (a.nseq == 0 || a.Hq == 0 || total_q == 0) return TSA_OK;
@@ -630,19 +773,18 @@ static int launch_prefill(PrefillArgs& a, bool mfma, int64_t total_q, int64_t ma
   if constexpr (sizeof(T) == 2) {
     // The LDS-staged kernel keeps 32 rows of K/V byte offsets in 32 bits.
     const int64_t kMaxStride = int64_t{1} << 24;
-    if ((a.G == 2 || a.G == 4 || a.G == 8) && a.scale_log2 > 0.f && a.k_st < kMaxStride && a.v_st < kMaxStride) {
-      a.nqb = static_cast<int32_t>((max_seqlen_q + 31) / 32);
-      if (a.nqb == 0) return TSA_OK;
-      const dim3 grid(static_cast<uint32_t>(a.nqb) * a.nseq * a.Hkv), block(64 * a.G);
+    if ((a.G == 2 || a.G == 4 || a.G == 8) && a.scale_log2 > 0.f && a.k_st < kMaxStride && a.v_st < kMaxStride &&
+        a.nseq <= max_persist_seqs(a.G)) {
+      static std::atomic<unsigned int> calls{0};
+      a.queue = static_cast<int32_t>(calls.fetch_add(1, std::memory_order_relaxed) % kQueueSlots);
       if (a.D == 128) {
-        if (a.G == 2) varlen_prefill_gqa<T, 128, 2><<<grid, block, 0, stream>>>(a);
-        else if (a.G == 4) varlen_prefill_gqa<T, 128, 4><<<grid, block, 0, stream>>>(a);
-        else varlen_prefill_gqa<T, 128, 8><<<grid, block, 0, stream>>>(a);
-      } else {
-        if (a.G == 2) varlen_prefill_gqa<T, 64, 2><<<grid, block, 0, stream>>>(a);
-        else if (a.G == 4) varlen_prefill_gqa<T, 64, 4><<<grid, block, 0, stream>>>(a);
-        else varlen_prefill_gqa<T, 64, 8><<<grid, block, 0, stream>>>(a);
+        if (a.G == 2) return launch_persistent<T, 128, 2>(a, stream);
+        if (a.G == 4) return launch_persistent<T, 128, 4>(a, stream);
+        return launch_persistent<T, 128, 8>(a, stream);
       }
+      if (a.G == 2) return launch_persistent<T, 64, 2>(a, stream);
+      if (a.G == 4) return launch_persistent<T, 64, 4>(a, stream);
+      return launch_persistent<T, 64, 8>(a, stream);
     } else {
       a.nqb = static_cast<int32_t>((max_seqlen_q + 31) / 32);
       if (a.nqb == 0) return TSA_OK;
