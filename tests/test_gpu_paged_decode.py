@@ -138,6 +138,23 @@ def test_stream_partition(num_workgroups):
         assert_close(out[keep], ref[keep], what=f"W={num_workgroups} call {call}")
 
 
+def test_repeated_calls_are_identical():
+    """More calls than the stream kernel's work-queue slots, two shapes
+    interleaved: whichever wave streams a chunk, its partial lands in the same
+    slot and the merge order is fixed, so every output is bit-identical."""
+    qa, kca, vca, bta, sla = _random_paged_inputs([3000, 17, 900, 64], 32, 8, 128, 16, torch.bfloat16, seed=31)
+    qb, kcb, vcb, btb, slb = _random_paged_inputs([257, 1200], 16, 4, 128, 16, torch.bfloat16, seed=32)
+    a = [t.to(DEV) for t in (qa, kca, vca, bta)] + [sla.to(DEV)]
+    b = [t.to(DEV) for t in (qb, kcb, vcb, btb)] + [slb.to(DEV)]
+    first_a = paged_attention_forward(a[0], a[1], a[2], a[3], 16, a[4])
+    first_b = paged_attention_forward(b[0], b[1], b[2], b[3], 16, b[4])
+    for _ in range(40):
+        oa = paged_attention_forward(a[0], a[1], a[2], a[3], 16, a[4])
+        ob = paged_attention_forward(b[0], b[1], b[2], b[3], 16, b[4])
+        assert torch.equal(oa, first_a) and torch.equal(ob, first_b)
+    assert_close(first_a.cpu(), op.paged_attention_forward(qa, kca, vca, bta, 16, sla), what="repeated calls")
+
+
 def test_seq_len_one_returns_v_row():
     q, kc, vc, bt, sl = _random_paged_inputs([1, 1], 8, 2, 128, 16, torch.bfloat16, seed=5)
     out = _run(q, kc, vc, bt, 16, sl).cpu()

@@ -106,9 +106,9 @@ def test_sequence_without_keys():
 
 
 def test_repeated_calls_are_identical():
-    """More calls than the persistent kernel's work-queue slots, two shapes
-    interleaved: every call claims each work item exactly once, so every
-    output is bit-identical to the first call's."""
+    """Many calls in a row, two shapes interleaved: the persistent
+    workgroups compute every work item exactly once, in a fixed assignment, so
+    every output is bit-identical to the first call's."""
     lens_a, lens_b = [300, 17, 1000, 64], [33, 700]
     qa, ka, va, ca, _ = _inputs(lens_a, lens_a, 32, 8, 128, torch.bfloat16, seed=21)
     qb, kb, vb, cb, _ = _inputs(lens_b, lens_b, 32, 8, 128, torch.bfloat16, seed=22)

@@ -6,17 +6,17 @@
 // P cast to the V dtype before P.V (:126), l summing the fp32 P (:128-129).
 //
 // Three kernels, chosen per call:
-//   varlen_prefill_gqa   bf16/f16, head_dim 64/128, GQA group 2, 4 or 8:
-//                        one workgroup per (kv head, sequence, 32 queries),
+//   varlen_prefill_gqa   bf16/f16, head_dim 64/128, GQA group 2, 4 or 8, up
+//                        to 1024-2048 sequences: persistent workgroups, each
+//                        computing (kv head, sequence, 32 queries) items with
 //                        K/V staged in LDS once for the whole group, 32x32x16
 //                        MFMA tiles (the main path);
 //   varlen_prefill_mfma  other group sizes: 4 q-heads per workgroup, operands
 //                        straight from global memory, 16x16x32 MFMA tiles;
 //   varlen_prefill_generic  fp32, other head_dims or non-unit innermost
 //                        strides: one wave per (query, q-head), fp32 VALU.
-// Causal key blocks past a workgroup's last query are never visited, and the
-// heaviest query blocks are dispatched first.
-#include <atomic>
+// Causal key blocks past a query block's last query are never visited, and
+// the heaviest query blocks are computed first.
 #include <cmath>
 #include <type_traits>
 
@@ -40,15 +40,8 @@ struct PrefillArgs {
   int32_t nseq, Hq, Hkv, G, D, nqb;
   int32_t causal;
   float scale_log2;
-  int32_t queue;  // work-queue slot of this call (persistent kernel)
 };
 
-// Work queue of the persistent kernel: per call a slot holding the next work
-// item and the number of workgroups done. The last workgroup to finish puts
-// both back to zero, and consecutive calls take consecutive slots, so calls
-// in flight on different streams do not share one.
-constexpr int kQueueSlots = 64;
-__device__ unsigned int g_prefill_queue[kQueueSlots][2];
 // Sequences per call the persistent kernel keeps counts of in LDS.
 constexpr int max_persist_seqs(int nw) { return nw == 2 ? 1024 : 2048; }
 
@@ -209,34 +202,33 @@ __global__ __launch_bounds__(256) void varlen_prefill_mfma(PrefillArgs a) {
   }
 }
 
-// LDS-staged GQA flash attention on 32x32 tiles. A workgroup of NW = G waves
-// (G = q heads per kv head: 2, 4 or 8) owns one kv head of one sequence and
-// 32 queries: wave w takes those queries of q-head w, so all NW tiles read
-// the same K/V and need the same key blocks. 32-key K/V blocks are staged
-// once per workgroup in double-buffered LDS, with K one block ahead of V and
-// the global loads of the next blocks in flight while a block is computed.
-// Both products run on v_mfma_f32_32x32x16 (the
-// 16x16x32 form has about 60% of its throughput on gfx950). With lane
+// LDS-staged GQA flash attention on 32x32 tiles, persistent. A work item is
+// one kv head of one sequence and 32 queries; a workgroup of NW = G waves
+// (G = q heads per kv head: 2, 4 or 8) computes it, wave w taking those
+// queries of q-head w, so all NW tiles read the same K/V and need the same
+// key blocks. The grid is as many workgroups as fit on the device at once,
+// each walking its share of the items (the item loop below). 32-key K/V
+// blocks go from global memory straight into LDS (global_load_lds_dwordx4,
+// no registers), NB slots per tensor, the loads A = NB - 1 blocks ahead and
+// K one block ahead of V. Rows are unpadded; the 16-byte chunk ch of row r
+// sits at position ch ^ swz(r). Both products run on v_mfma_f32_32x32x16
+// (the 16x16x32 form has about 60% of its throughput on gfx950). With lane
 // (h, c) = (lane / 32, lane % 32) and accumulator element e holding row
 // 8(e/4) + 4h + e%4, column c:
 //   S^T(32 keys x 32 queries) = K Q^T over head_dim/16 steps: lane (h, c)
-//     reads key c, dims 16jj + 8h..+8 (row-major K, row stride D+8 elements:
-//     the 16 lanes of a 128-bit read hit 16 distinct bank quads) and holds
-//     query c's Q slice in registers; it gets query c's scores of keys
-//     8(e/4) + 4h + e%4;
+//     reads key c, dims 16jj + 8h..+8 (the swizzle puts the 16 rows of a
+//     128-bit read in 16 distinct bank quads) and holds query c's Q slice in
+//     registers; it gets query c's scores of keys 8(e/4) + 4h + e%4;
 //   O(32 queries x 32 dims) += P V over two 16-key steps s: the P operand's
 //     k-slots 8h..8h+7 are keys 16s+4h+0..3 and 16s+8+4h+0..3, i.e. the score
 //     accumulators 8s..8s+7 of the same lane, so P goes to the operand in
 //     registers; the V operand comes from two ds_read_b64_tr_b16, in which a
 //     16-lane group whose lane 4e+q reads dims 4q..4q+3 of key row e gets, in
-//     lane j, element e = V[key e][dim j]. V stays row-major in LDS with row
-//     stride D+32 elements, so the two groups of a half-wave hit disjoint
-//     banks.
+//     lane j, element e = V[key e][dim j]. V stays row-major in LDS, and the
+//     swizzle keeps these reads free of bank conflicts too.
 // Scores, probabilities and the output accumulators all stay in VGPRs (at most
-// 256 per wave, two waves per SIMD); several workgroups share a CU and drift
-// apart, so one workgroup's softmax overlaps another's MFMAs. Workgroup ids
-// put the kv head fastest (a kv head's query blocks share one XCD's L2) and
-// the heaviest query blocks first.
+// 256 per wave, two waves per SIMD); the workgroups sharing a CU drift apart,
+// so one workgroup's softmax overlaps another's MFMAs.
 template <typename T, int D, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void varlen_prefill_gqa(
     PrefillArgs a, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
@@ -254,8 +246,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   constexpr int VOFF = NB * BLKB;           // byte offset of the V slots
   constexpr int OOFF = 2 * NB * BLKB;       // byte offset of the output staging (8 rows per wave)
   constexpr int QOFF = OOFF + NW * 8 * ROWO * 2;  // byte offset of the per-sequence query-block counts
-  constexpr int IOFF = QOFF + max_persist_seqs(NW) * 2;  // byte offset of the published item index
-  constexpr int SMEM = IOFF + 16;
+  constexpr int SMEM = QOFF + max_persist_seqs(NW) * 2;
   static_assert(IPW >= 1 && IPW * NW == 2 * (32 / RPI), "a block step is a whole number of loads per wave");
   static_assert((A > 1 ? A - 1 : 0) * IPW <= 63, "outstanding loads fit the vmcnt field");
   // A row's running max only moves when it grows by more than this (log2
@@ -264,25 +255,25 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   constexpr float kRescale = 8.0f;
   __shared__ __align__(16) char smem[SMEM];
   uint16_t* const nqb_s = reinterpret_cast<uint16_t*>(smem + QOFF);  // query blocks of each sequence
-  int* const item_s = reinterpret_cast<int*>(smem + IOFF);           // the next item, published to all waves
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nseq = a.nseq, Hkv = a.Hkv;
   const float cs = a.scale_log2;  // > 0 on this path
-  unsigned int* const queue = g_prefill_queue[a.queue];
 
   // ---- Work items: (query block, sequence, kv head) with a non-empty query
   // block, heaviest (latest) query blocks first: level Q holds query block Q
-  // of every sequence that has one, in sequence order, kv head fastest. Items
-  // are handed out one at a time through an atomic counter, so workgroups
-  // that run fast take more; the per-sequence counts live in LDS.
+  // of every sequence that has one, in sequence order, kv head fastest.
+  // Workgroup w takes items w, w + grid, w + 2 grid, ...: with the heaviest
+  // first, that deals the work out evenly. (No work-queue atomic: a returning
+  // atomic holds up every load the wave issues after it until it completes,
+  // and under load that took longer than the imbalance it would remove.) The
+  // per-sequence counts live in LDS.
   for (int b = tid; b < nseq; b += 64 * NW) {
     int64_t qs, ql;
     seq_range(cu_q, a.cuq_s, b, a.total_q, qs, ql);
     nqb_s[b] = static_cast<uint16_t>((ql + 31) / 32);
   }
-  if (tid == 0) item_s[0] = static_cast<int>(atomicAdd(queue, 1u));
   __syncthreads();
   // Items above level Q: Hkv * sum_b max(0, nqb_b - Q - 1) (wave reduction).
   auto items_above = [&](int Q) {
@@ -600,11 +591,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
   };
 
-  // ---- The item loop. While item X computes, the atomic that claims the
-  // next item is in flight; it is read once X's last loads have landed, and
-  // the next item's K/V blocks and Q are fetched while X's last block and its
-  // output are finished, so its first block is usually in LDS when it starts.
-  int idx = item_s[0];
+  // ---- The item loop. The next item's K/V blocks and Q are fetched while
+  // X's last block and its output are finished, so its first block is
+  // usually in LDS when it starts.
+  int idx = blockIdx.x;
   Item X;
   if (idx < n_items) {
     resolve(idx, X);
@@ -613,10 +603,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   }
   int g = 0;  // slot counter: X's block 0 is the workgroup's g-th block
   while (idx < n_items) {
-    // (item_s is rewritten below only after this loop's barriers, so every
-    // wave has read the current value by then.)
-    unsigned int next_raw = 0;
-    if (tid == 0) next_raw = atomicAdd(queue, 1u);
 #pragma unroll
     for (int u = 0; u < NU; ++u)
 #pragma unroll
@@ -628,10 +614,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     else wait_loads(std::integral_constant<int, 0>{});
     lds_barrier();
     f32x16 sca, scb;  // S of the even / odd blocks
-    if (X.nblk > 0) {
-      kread(g % NB);
-      qk(sca);
-    }
+    // Unconditional, also for an item without keys (whose scores are never
+    // used): every path into the block loop then consumes Q here, so the
+    // compiler's wait for X's Q loads is placed here and not in the loop,
+    // where it would also drain the K/V loads in flight.
+    kread(g % NB);
+    qk(sca);
     // Iteration 0's loads overwrite K(0)'s slot: every wave must have read it.
     lds_barrier();
     int j = 0;
@@ -644,12 +632,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
       sca = scb;  // the last block's scores, in one place
       ++j;
     }
-    // X's last block j, after all of X's loads have landed (and the claim
-    // with them): publish the next item, fetch its blocks and Q behind X's
-    // last block, then store X's output.
-    if (tid == 0) item_s[0] = static_cast<int>(next_raw);
-    lds_barrier();
-    const int nidx = item_s[0];
+    // X's last block j, after all of X's loads have landed: fetch the next
+    // item's blocks and Q behind X's last block, then store X's output. (The
+    // next item's loads go to slots no wave reads any more: X's last V slot is
+    // not among them, and every other slot was last read before the block
+    // loop's final barrier.)
+    const int nidx = idx + static_cast<int>(gridDim.x);
     Item Y;
     if (nidx < n_items) resolve(nidx, Y);
     // (An item without keys has no block: its output is 0/0, as the
@@ -667,14 +655,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     g += X.nblk;
     X = Y;
     idx = nidx;
-  }
-  // The last workgroup to finish resets this call's queue slot.
-  if (tid == 0) {
-    const unsigned int done = atomicAdd(queue + 1, 1u);
-    if (done == gridDim.x - 1) {
-      queue[0] = 0;
-      queue[1] = 0;
-    }
   }
 }
 
@@ -775,8 +755,6 @@ static int launch_prefill(PrefillArgs& a, bool mfma, int64_t total_q, int64_t ma
     const int64_t kMaxStride = int64_t{1} << 24;
     if ((a.G == 2 || a.G == 4 || a.G == 8) && a.scale_log2 > 0.f && a.k_st < kMaxStride && a.v_st < kMaxStride &&
         a.nseq <= max_persist_seqs(a.G)) {
-      static std::atomic<unsigned int> calls{0};
-      a.queue = static_cast<int32_t>(calls.fetch_add(1, std::memory_order_relaxed) % kQueueSlots);
       if (a.D == 128) {
         if (a.G == 2) return launch_persistent<T, 128, 2>(a, stream);
         if (a.G == 4) return launch_persistent<T, 128, 4>(a, stream);
