@@ -416,10 +416,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   };
   // Wait until at most n of this wave's loads are in flight (they complete
   // in issue order; other memory operations issued among them only make the
-  // wait stricter).
+  // wait stricter). Written as assembly: the compiler cannot see the loads,
+  // so it could drop a wait of its own making as redundant.
   auto wait_loads = [&](auto n) {
     constexpr int N = decltype(n)::value;
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
   };
   constexpr int kInFlight = (A - 1) * IPW;  // loads of the later steps, still in flight at a block's end
 
