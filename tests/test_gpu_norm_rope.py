@@ -101,3 +101,52 @@ def test_fused_store(mode):
         ok.store_kv_cache(p0, torch.tensor(lst), kg.cpu()[sl].transpose(0, 1), w.v[sl].transpose(0, 1), ke, ve)
     assert_bitexact(kc, ke, "k_cache")
     assert_bitexact(vc, ve, "v_cache")
+
+
+def _repage(w, bs, seed):
+    """The workload's sequences on a pool of bs-token pages: fresh shuffled
+    block tables and a random pool (the contents before the store)."""
+    g = torch.Generator().manual_seed(seed)
+    ctx = [int(n) for n in (w.ctx_lens if hasattr(w, "ctx_lens") and w.ctx_lens is not None else w.seq_lens)]
+    npages = [max(1, -(-n // bs)) for n in ctx]
+    nb = sum(npages) + 2
+    perm = torch.randperm(nb, generator=g)
+    tables, lists, cur = torch.zeros(len(ctx), max(npages), dtype=torch.int32), [], 0
+    for i, n in enumerate(npages):
+        lst = perm[cur:cur + n].tolist()
+        tables[i, :n] = torch.tensor(lst, dtype=torch.int32)
+        lists.append(lst)
+        cur += n
+    hkv, d = w.k_cache.shape[1], w.k_cache.shape[3]
+    kc = torch.randn(nb, hkv, bs, d, generator=g).to(w.k_cache.dtype)
+    vc = torch.randn(nb, hkv, bs, d, generator=g).to(w.v_cache.dtype)
+    return tables, lists, kc, vc
+
+
+@pytest.mark.parametrize("mode", ["decode", "prefill"])
+def test_fused_store_page_256(mode):
+    """The fused norm/RoPE/store on 256-token pages (the server's default page size)."""
+    if mode == "decode":
+        w = W.make("qwen3-0.6b-decode-bs4", poison=True)
+        b = len(w.ctx_lens)
+        cu, pos = torch.arange(b + 1, dtype=torch.int32), w.positions
+    else:
+        w = W.make("qwen3-4b-mixed-prefill", poison=True)
+        cu, pos = w.cu_seqlens, None
+    tables, lists, kc0, vc0 = _repage(w, 256, seed=5)
+    kc, vc = kc0.to(DEV), vc0.to(DEV)
+    qg, kg = qk_norm_rope_store(w.q.to(DEV), w.k.to(DEV), w.v.to(DEV), w.q_weight.to(DEV), w.k_weight.to(DEV),
+                                w.cos.to(DEV), w.sin.to(DEV), w.eps, kc, vc, tables.to(DEV), cu.to(DEV),
+                                None if pos is None else pos.to(DEV))
+    torch.cuda.synchronize()
+    qr, kr = _oracle(w.q, w.k, w)
+    _check(qg, qr, "q")
+    _check(kg, kr, "k")
+    ke, ve = kc0.clone(), vc0.clone()
+    cul = cu.tolist()
+    for s, lst in enumerate(lists):
+        p0 = 0 if pos is None else int(pos[s])
+        sl = slice(cul[s], cul[s + 1])
+        ok.store_kv_cache(p0, torch.tensor(lst), kg.cpu()[sl].transpose(0, 1), w.v[sl].transpose(0, 1), ke, ve)
+    assert_bitexact(kc, ke, "k_cache")
+    assert_bitexact(vc, ve, "v_cache")

@@ -116,8 +116,9 @@ def test_gqa_groups(group, head_dim):
     assert_close(out, ref, what=f"G={group} D={head_dim}")
 
 
-@pytest.mark.parametrize("block_size", [4, 8, 32, 64])
+@pytest.mark.parametrize("block_size", [4, 8, 32, 64, 128, 256])
 def test_page_sizes(block_size):
+    """Page sizes up to the server's default of 256 tokens."""
     q, kc, vc, bt, sl = _random_paged_inputs([3, 50, 129, 16], 16, 4, 128, block_size, torch.bfloat16, seed=7)
     out = _run(q, kc, vc, bt, block_size, sl)
     ref = op.paged_attention_forward(q, kc, vc, bt, block_size, sl)
