@@ -2,7 +2,8 @@
 
 * the device metadata matches the reference's per-layer construction
   (server/model/patches/qwen3.py:296-310, 388-400): zero-padded int32 block
-  tables, cu_seqlens over num_tokens, seq_lens = position + 1;
+  tables, cu_seqlens over num_tokens, seq_lens = position + 1; tables and
+  cu_seqlens share one packed buffer (one transfer);
 * the reference's ValueErrors (:182-187, :329-330);
 * one build per forward: layers that get the same position_ids reuse it, a
   new step's tensor rebuilds it;
@@ -26,6 +27,8 @@ def test_prefill_metadata():
     assert m.block_tables.dtype == torch.int32 and m.block_tables.tolist() == [[4, 9, 0], [2, 0, 0], [0, 1, 7]]
     assert m.cu_seqlens.tolist() == [0, 3, 4, 9] and m.max_seqlen == 5
     assert m.positions is None and m.seq_lens is None
+    # one packed buffer, so one host-to-device transfer
+    assert m.block_tables.untyped_storage().data_ptr() == m.cu_seqlens.untyped_storage().data_ptr()
 
 
 def test_decode_metadata():

@@ -77,8 +77,9 @@ class DeviceMetadata:
 def device_metadata(ctx: InferenceContext, position_ids: torch.Tensor | None, num_tokens: int,
                     device: torch.device) -> DeviceMetadata:
     """Build the padded block tables, cu_seqlens and, for a decode step, the
-    positions and sequence lengths, with the reference's checks, on the host,
-    copied in one transfer each. The layers of one forward share the build:
+    positions and sequence lengths, with the reference's checks. The tables
+    and cu_seqlens are packed into one int32 buffer on the host and copied in
+    one transfer; the device tensors are views of it. The layers of one forward share the build:
     HF hands every layer the same position_ids tensor, and the context keeps a
     reference to it (so a later step's tensor is a different object). The
     context's sequences must not be changed in place during a forward."""
@@ -99,20 +100,22 @@ def device_metadata(ctx: InferenceContext, position_ids: torch.Tensor | None, nu
         if len(seqs) != num_tokens:
             raise ValueError(f"Decode step has {num_tokens} tokens for {len(seqs)} sequences")
         lengths = [1] * len(seqs)
-    max_blocks = max((len(s["block_table"]) for s in seqs), default=0)
-    tables = torch.zeros(len(seqs), max(max_blocks, 1), dtype=torch.int32)
+    width = max(max((len(s["block_table"]) for s in seqs), default=0), 1)
+    n_tab = len(seqs) * width
+    packed = torch.zeros(n_tab + len(seqs) + 1, dtype=torch.int32)  # [tables | cu_seqlens]
+    tables = packed[:n_tab].view(len(seqs), width)
     for i, s in enumerate(seqs):
         bt = s["block_table"]
         if len(bt):
             tables[i, : len(bt)] = torch.as_tensor(bt, dtype=torch.int32)
-    cu = torch.zeros(len(seqs) + 1, dtype=torch.int32)
-    cu[1:] = torch.as_tensor(lengths, dtype=torch.int32).cumsum(0)
+    packed[n_tab + 1:] = torch.as_tensor(lengths, dtype=torch.int32).cumsum(0)
     positions = seq_lens = None
     if ctx.mode != "prefill":
         positions = position_ids.reshape(-1).to(device=device, dtype=torch.int32)
         seq_lens = positions + 1
-    meta = DeviceMetadata(tables.to(device, non_blocking=False), cu.to(device, non_blocking=False),
-                          max(lengths, default=0), positions, seq_lens)
+    dev = packed.to(device)
+    meta = DeviceMetadata(dev[:n_tab].view(len(seqs), width), dev[n_tab:], max(lengths, default=0), positions,
+                          seq_lens)
     ctx._device_meta = (position_ids, (ctx.mode, num_tokens, str(device), getattr(position_ids, "_version", None)),
                         meta)
     return meta
