@@ -210,3 +210,13 @@ def test_qwen3_8b_bs64_sampled():
 def test_qwen3_32b_bs32_sampled():
     w = W.make("qwen3-32b-decode-bs32", device=DEV)
     _sampled_check(w, [0, 31])
+
+
+def test_many_sequences():
+    """A 1000-sequence decode batch of 1-300 tokens (many small units) against the oracle."""
+    g = torch.Generator().manual_seed(45)
+    lens = torch.randint(1, 301, (1000,), generator=g).tolist()
+    q, kc, vc, bt, sl = _random_paged_inputs(lens, 32, 8, 128, 16, torch.bfloat16, seed=46)
+    out = _run(q, kc, vc, bt, 16, sl).cpu()
+    ref = op.paged_attention_forward(q, kc, vc, bt, 16, sl)
+    assert_close(out, ref, what="1000 sequences")

@@ -163,3 +163,33 @@ def test_qwen3_8b_prefill_sampled():
         c1 = torch.tensor([0, b - a], dtype=torch.int32)
         ref = ov.flash_attn_varlen_func(sub_q, sub_k, sub_v, c1, c1, b - a, b - a, True)
         assert_close(out[a:b, heads], ref, what=f"seq {s} len {b - a}")
+
+
+def test_long_sequence_sampled_rows():
+    """An 8192-token causal sequence (256 query tiles, up to 256 key blocks
+    each) beside a short one, checked on sampled query rows against fp64
+    softmax attention over the row's visible keys."""
+    lens = [8192, 100]
+    q, k, v, cq, _ = _inputs(lens, lens, 32, 8, 128, torch.bfloat16, seed=41)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cq.to(DEV), cq.to(DEV), max(lens), max(lens),
+                                 True).cpu().double()
+    scale = 128 ** -0.5
+    got, want = [], []
+    for r, start in [(0, 0), (31, 0), (32, 0), (4095, 0), (8160, 0), (8191, 0), (8192, 8192), (8291, 8192)]:
+        for h in (0, 17, 31):
+            kk, vv = k[start:r + 1, h // 4].double(), v[start:r + 1, h // 4].double()
+            p = torch.softmax((kk @ q[r, h].double()) * scale, 0)
+            want.append(p @ vv)
+            got.append(out[r, h])
+    assert_close(torch.stack(got), torch.stack(want), what="long sequence, sampled rows")
+
+
+def test_many_short_sequences():
+    """1000 sequences of 1-64 tokens (a wide, shallow batch) against the oracle."""
+    g = torch.Generator().manual_seed(43)
+    lens = torch.randint(1, 65, (1000,), generator=g).tolist()
+    q, k, v, cq, ck = _inputs(lens, lens, 32, 8, 128, torch.bfloat16, seed=44)
+    out = flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cq.to(DEV), ck.to(DEV), max(lens), max(lens),
+                                 True).cpu()
+    ref = ov.flash_attn_varlen_func(q, k, v, cq, ck, max(lens), max(lens), True)
+    assert_close(out, ref, what="1000 short sequences")
