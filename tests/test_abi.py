@@ -99,6 +99,13 @@ def test_decode_validation():
     kcb = _v((10, 2, 16, 1024))
     rc, msg = _call("tsa_paged_decode", R(big), R(big), R(kcb), R(kcb), R(bt), R(sl), 0.1, None, 0, 0, None)
     assert rc == _lib.TSA_ERR_UNSUPPORTED
+    # 60000 sequences x 2^20-token tables: more 16-token tiles than the
+    # kernel's 32-bit tile prefix holds, rejected before any device work.
+    n = 60000
+    qn, btn, sln = _v((n, 8, 128)), _v((n, 1 << 16), torch.int32), _v((n,), torch.int32)
+    kcn = _v((10, 2, 16, 128))
+    rc, msg = _call("tsa_paged_decode", R(qn), R(qn), R(kcn), R(kcn), R(btn), R(sln), 0.1, None, 0, 0, None)
+    assert rc == _lib.TSA_ERR_INVALID and "2^31" in msg
 
 
 def test_prefill_validation():

@@ -665,6 +665,8 @@ extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, cons
               "block_tables and seq_lens must have num_seqs (%lld) rows", (long long)B);
   TSA_REQUIRE(B < 65536 && Hq < 65536, "num_seqs and num_heads must be below 65536");
   TSA_REQUIRE(block_tables->size[1] * BS < (int64_t(1) << 31) / 16, "block table too long");
+  TSA_REQUIRE(B * ((block_tables->size[1] * BS + 15) / 16) < (int64_t(1) << 31),
+              "num_seqs x block-table capacity exceeds 2^31 16-token tiles");
   TSA_UNSUPPORTED(D <= 512, "head_dim %lld > 512 is not implemented", (long long)D);
   TSA_REQUIRE(num_workgroups >= 0, "num_workgroups must be non-negative");
 

@@ -754,8 +754,10 @@ static int launch_prefill(PrefillArgs& a, bool mfma, int64_t total_q, int64_t ma
   if constexpr (sizeof(T) == 2) {
     // The LDS-staged kernel keeps 32 rows of K/V byte offsets in 32 bits.
     const int64_t kMaxStride = int64_t{1} << 24;
+    // (Per-sequence query-block counts are 16-bit in LDS: every sequence's
+    // length is at most total_q.)
     if ((a.G == 2 || a.G == 4 || a.G == 8) && a.scale_log2 > 0.f && a.k_st < kMaxStride && a.v_st < kMaxStride &&
-        a.nseq <= max_persist_seqs(a.G)) {
+        a.nseq <= max_persist_seqs(a.G) && total_q <= int64_t{65535} * 32) {
       if (a.D == 128) {
         if (a.G == 2) return launch_persistent<T, 128, 2>(a, stream);
         if (a.G == 4) return launch_persistent<T, 128, 4>(a, stream);
