@@ -86,7 +86,7 @@ def _spread(ev):
 
 def bench_decode(name, steps, warmup, num_workgroups=0, copies=3, with_block=False):
     from tinyserver_amd import workloads as W
-    from tinyserver_amd.kernels import paged_attention_forward, qk_norm_rope_store
+    from tinyserver_amd.kernels import paged_attention_forward, paged_decode_step, qk_norm_rope_store
 
     dev = torch.device("cuda:0")
     w = W.make(name, device=dev)
@@ -134,6 +134,13 @@ def bench_decode(name, steps, warmup, num_workgroups=0, copies=3, with_block=Fal
                                     out=out)
 
         res["block_us_per_call"] = time_region(block, steps, warmup)[0] * 1e3
+
+        def block_fused(i):  # the same step as one fused call (two launches)
+            kc, vc = pools[i % copies]
+            paged_decode_step(w.q, w.k, w.v, qw, kw, cos, sin, w.eps, kc, vc, w.block_tables, seq_lens,
+                              num_workgroups=num_workgroups, out=out)
+
+        res["block_fused_us_per_call"] = time_region(block_fused, steps, warmup)[0] * 1e3
     return res, w
 
 
@@ -310,6 +317,7 @@ def main():
         "pct_peak_hbm": round(head["pct_peak_hbm"], 2),
         "tokens_per_s": round(head["tokens_per_s"], 1),
         "decode_block_us_per_layer": round(head["block_us_per_call"], 2),
+        "decode_block_fused_us_per_layer": round(head["block_fused_us_per_call"], 2),
         "roofline": {
             "bound": "hbm",
             "achieved": round(head["achieved_gbs"], 1),

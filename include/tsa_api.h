@@ -26,6 +26,8 @@
  *   tsa_qk_norm_rope_store  the same, fused with tsa_store_kv_paged
  *   tsa_paged_decode        server/model/kernels/paged_attention.py:124-192
  *                           (paged_attention_forward)
+ *   tsa_paged_decode_step   the decode call site (qwen3.py:268-287, 335-409):
+ *                           norm/RoPE, store and paged attention, fused
  *   tsa_varlen_prefill      server/model/kernels/varlen_attention.py:145-218
  *                           (flash_attn_varlen_func)
  */
@@ -142,6 +144,24 @@ int tsa_paged_decode(const tsa_view* out, const tsa_view* query, const tsa_view*
                      const tsa_view* v_cache, const tsa_view* block_tables,
                      const tsa_view* seq_lens, double softmax_scale, void* workspace,
                      size_t workspace_bytes, int32_t num_workgroups, void* stream);
+
+/* The decode step of the Qwen3 call site, fused (qwen3.py:268-287 norm and
+ * RoPE of q and of the new k, :335-357 the store of the new token's k and v,
+ * :359-409 paged_attention_forward), in the two launches of tsa_paged_decode:
+ * query (B, Hq, D) and k / v (B, Hkv, D) are the raw projections of each
+ * sequence's new token, at position seq_lens[s] - 1; q_weight, k_weight (D);
+ * cos / sin (B, D) for those positions. The rotated k and the raw v are
+ * written to the token's cache slot; out is the attention over the first
+ * seq_lens[s] tokens, the new one included. Same rounding as
+ * tsa_qk_norm_rope_store followed by tsa_paged_decode. TSA_ERR_UNSUPPORTED
+ * unless: bf16/f16, head_dim 128, pages a multiple of 16 tokens, contiguous
+ * cache rows, at most 8 q-heads per kv head; callers then use those two. */
+int tsa_paged_decode_step(const tsa_view* out, const tsa_view* query, const tsa_view* k_new,
+                          const tsa_view* v_new, const tsa_view* q_weight, const tsa_view* k_weight,
+                          const tsa_view* cos, const tsa_view* sin, double eps, const tsa_view* k_cache,
+                          const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
+                          double softmax_scale, void* workspace, size_t workspace_bytes,
+                          int32_t num_workgroups, void* stream);
 
 /* flash_attn_varlen_func (varlen_attention.py:145-218): per sequence b and
  * q-head h, softmax(q k^T * softmax_scale) v over keys cu_seqlens_k[b] ..

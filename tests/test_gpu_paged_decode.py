@@ -21,7 +21,7 @@ from oracle import norm_rope as onr
 from oracle import paged as op
 from tests.helpers import assert_close
 from tinyserver_amd import workloads as W
-from tinyserver_amd.kernels import paged_attention_forward, qk_norm_rope_store
+from tinyserver_amd.kernels import paged_attention_forward, paged_decode_step, qk_norm_rope_store
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -220,3 +220,35 @@ def test_many_sequences():
     out = _run(q, kc, vc, bt, 16, sl).cpu()
     ref = op.paged_attention_forward(q, kc, vc, bt, 16, sl)
     assert_close(out, ref, what="1000 sequences")
+
+
+@pytest.mark.parametrize("name", ["qwen3-0.6b-decode-bs4", "qwen3-8b-decode-bs64"])
+def test_fused_decode_step(name):
+    """paged_decode_step (norm/RoPE + store + attention, fused) against the
+    two-launch path (qk_norm_rope_store, then paged_attention_forward): the
+    same rounding and the same operands, so the cache and the output are
+    bit-identical; and the output against the oracle."""
+    w = W.make(name, poison=True)
+    b = len(w.ctx_lens)
+    g = w.to(DEV)
+    sl = g.ctx_lens.to(torch.int32)
+    kc_a, vc_a = g.k_cache.clone(), g.v_cache.clone()
+    cu = torch.arange(b + 1, dtype=torch.int32, device=DEV)
+    qa, _ = qk_norm_rope_store(g.q, g.k, g.v, g.q_weight, g.k_weight, g.cos, g.sin, g.eps, kc_a, vc_a,
+                               g.block_tables, cu, g.positions, return_k=False)
+    out_a = paged_attention_forward(qa, kc_a, vc_a, g.block_tables, 16, sl)
+    kc_b, vc_b = g.k_cache.clone(), g.v_cache.clone()
+    out_b = paged_decode_step(g.q, g.k, g.v, g.q_weight, g.k_weight, g.cos, g.sin, g.eps, kc_b, vc_b,
+                              g.block_tables, sl)
+    torch.cuda.synchronize()
+    assert torch.equal(kc_b, kc_a) and torch.equal(vc_b, vc_a), "cache differs from the two-launch path"
+    assert torch.equal(out_b, out_a), "output differs from the two-launch path"
+    if b <= 8:  # the oracle on the small batch
+        qr, kr = onr.qk_norm_rope(w.q[None], w.k[None], w.q_weight, w.k_weight, w.cos[None], w.sin[None], w.eps)
+        kc, vc = w.k_cache.clone(), w.v_cache.clone()
+        for i in range(b):
+            ok.store_kv_cache(int(w.positions[i]), torch.tensor(w.block_lists[i]), kr[0][:, i : i + 1],
+                              w.v[i][:, None], kc, vc)
+        ref = op.paged_attention_forward(qr[0].transpose(0, 1).contiguous(), kc, vc, w.block_tables, 16,
+                                         w.ctx_lens.to(torch.int32))
+        assert_close(out_b, ref, what=f"{name} fused step")

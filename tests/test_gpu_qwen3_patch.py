@@ -79,3 +79,33 @@ def test_bf16_as_accurate_as_stock_model(steps=4):
         for s, t in zip(seqs, nxt):
             s.append(t)
         logits = patched_decode_logits(patched, nxt, positions, tables, DEV)
+
+
+def test_fused_decode_route_matches_two_launches(monkeypatch):
+    """Small decode steps take the single-launch fused step; larger ones the
+    norm/store launch followed by paged attention. Both routes give the same
+    logits, bit for bit, and leave the same caches."""
+    from tinyserver_amd.patches import qwen3 as glue
+
+    block_size, steps = 16, 3
+    tables = allocate_block_tables([len(p) + steps + 1 for p in PROMPTS], block_size)
+    runs = []
+    for max_tiles in (glue.FUSED_DECODE_MAX_TILES, -1):  # -1: every step takes the two-launch route
+        monkeypatch.setattr(glue, "FUSED_DECODE_MAX_TILES", max_tiles)
+        _, patched = tiny_models(torch.bfloat16, DEV, block_size, sum(len(t) for t in tables) + 2)
+        logits = patched_prefill_logits(patched, PROMPTS, tables, DEV)
+        seqs = [list(p) for p in PROMPTS]
+        out = []
+        for _ in range(steps):
+            nxt = [int(logits[i].argmax()) for i in range(len(seqs))]
+            positions = [len(s) for s in seqs]
+            for s, t in zip(seqs, nxt):
+                s.append(t)
+            logits = patched_decode_logits(patched, nxt, positions, tables, DEV)
+            out.append(logits.clone())
+        layer = patched.model.layers[0].self_attn
+        runs.append((out, layer.k_cache.clone(), layer.v_cache.clone()))
+    (a, ka, va), (b, kb, vb) = runs
+    for step, (x, y) in enumerate(zip(a, b)):
+        assert torch.equal(x, y), f"decode step {step}: fused and two-launch logits differ"
+    assert torch.equal(ka, kb) and torch.equal(va, vb)

@@ -38,6 +38,7 @@ def test_decode_metadata():
     assert m.cu_seqlens.tolist() == [0, 1, 2]
     assert m.positions.tolist() == [15, 16] and m.seq_lens.tolist() == [16, 17]
     assert m.seq_lens.dtype == torch.int32
+    assert m.table_slots == 3  # the KV size the glue uses to choose the fused decode step
 
 
 def test_reference_errors():

@@ -79,7 +79,96 @@ struct DecodeArgs {
   float scale_log2;
   float* part;      // [B * Hkv + NW][G * (D + 2)]: per (unit, worker) acc[G][D], m[G], l[G]
   int32_t* pref_out;  // [B + 1] tile prefix over the sequences, for the merge
+  // The fused decode step only: query is the raw projection, and the new
+  // token's raw k/v rows (B, Hkv, D), the norm weights (D) and the cos/sin
+  // rows (B, D) come in here; eps is the RMSNorm epsilon.
+  const void* kn; const void* vn; const void* qw; const void* kw; const void* cos; const void* sin;
+  void* kc_out; void* vc_out;  // the caches, written (the new token's rows)
+  int64_t kn_ss, kn_sh, vn_ss, vn_sh, cs_ss, sn_ss;
+  float eps;
 };
+
+template <typename T>
+__device__ __forceinline__ u32x4 pack8(const float (&v)[8]) {
+  u32x4 w;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = pack2<T>(v[2 * i], v[2 * i + 1]);
+  return w;
+}
+
+// Norm + RoPE of a 128-dim head row held the way the stream kernel holds its
+// Q and K operands: the four lanes g = 0..3 of a column c own the 8-dim
+// chunks g + 4j (j = 0..3). row, w and cs are LDS byte addresses of the row,
+// the weights and the cos row (the sin row follows it). The rounding points
+// and the order of the mean-square sum are the standalone norm/RoPE
+// kernel's (the CPU reduction: chunk accumulators k = chunk % 4 over the
+// 32-element strides in order, then the four accumulators in order, then the
+// 8 elements in order): lane g holds accumulator g, and the RoPE partner
+// (+-64 dims, chunk +-8) is chunk j +- 2 of the same lane. Three passes over
+// LDS keep few values live; z is rounded to T, so it packs exactly. Inlined:
+// as a called function the kernel's ring registers spill across the call.
+struct RowOperand {
+  u32x4 v[4];
+};
+typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+template <typename T>
+__device__ __forceinline__ void lds8f(uint32_t addr, float (&out)[8]) {
+  const u32x4 w = *(lds_u32x4*)(uintptr_t)addr;  // an LDS byte address as a pointer
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = lo_f<T>(w[i]);
+    out[2 * i + 1] = hi_f<T>(w[i]);
+  }
+}
+template <typename T>
+__device__ __forceinline__ RowOperand norm_rope_row128(uint32_t row, uint32_t w, uint32_t cs, float eps) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  float acc[8], x[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    lds8f<T>(row + 16 * (g + 4 * j), x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = j == 0 ? __fmul_rn(x[e], x[e]) : __fadd_rn(acc[e], __fmul_rn(x[e], x[e]));
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float v = __shfl(acc[e], c, 64);
+    v = __fadd_rn(v, __shfl(acc[e], c + 16, 64));
+    v = __fadd_rn(v, __shfl(acc[e], c + 32, 64));
+    v = __fadd_rn(v, __shfl(acc[e], c + 48, 64));
+    ss = __fadd_rn(ss, v);
+  }
+  const float rinv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, 128.0f), eps)));
+  u32x4 zp[4];  // z = T(w T(x rinv)), packed
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float wf[8], z[8];
+    lds8f<T>(row + 16 * (g + 4 * j), x);
+    lds8f<T>(w + 16 * (g + 4 * j), wf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) z[e] = __fmul_rn(wf[e], to_float(from_float<T>(__fmul_rn(x[e], rinv))));
+    zp[j] = pack8<T>(z);
+  }
+  RowOperand r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float csf[8], snf[8], o[8];
+    lds8f<T>(cs + 16 * (g + 4 * j), csf);
+    lds8f<T>(cs + 256 + 16 * (g + 4 * j), snf);
+    const int jp = j < 2 ? j + 2 : j - 2;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t wz = zp[j][e >> 1], wp = zp[jp][e >> 1];
+      const float zv = (e & 1) ? hi_f<T>(wz) : lo_f<T>(wz);
+      const float pv = (e & 1) ? hi_f<T>(wp) : lo_f<T>(wp);
+      const float rot = j < 2 ? -pv : pv;
+      o[e] = __fadd_rn(to_float(from_float<T>(__fmul_rn(zv, csf[e]))), to_float(from_float<T>(__fmul_rn(rot, snf[e]))));
+    }
+    r.v[j] = pack8<T>(o);
+  }
+  return r;
+}
 
 // Waves per stream-kernel workgroup, and workgroups per CU of the default
 // grid (TSA_DECODE_WAVES * TSA_DECODE_WG_PER_CU waves per CU in all).
@@ -103,6 +192,13 @@ constexpr float kNegInf = -INFINITY;
 #define TSA_DECODE_RING 3
 #endif
 constexpr int RING = TSA_DECODE_RING;
+
+// Fused decode step: per wave, 1 KB of norm weights and RING unit buffers of
+// kUnitBytes in LDS after the tile prefixes. A unit buffer holds the raw q
+// rows of its G <= 8 heads (2 KB), then the cos, sin, raw k and raw v rows of
+// the sequence's new token (256 B each at head_dim 128).
+constexpr int kUnitBytes = 3072;
+constexpr int kFusedWaveBytes = 1024 + RING * kUnitBytes;
 
 // K/V are read exactly once per call. Non-temporal loads (the streaming
 // hint) reach about 6.8 TB/s on this chip against about 6.0 for ordinary
@@ -192,7 +288,7 @@ struct TileCursor {
 // __restrict__ parameters: with the partial stores inside the loop, that is
 // what lets the compiler read block-table entries and lengths with scalar
 // loads.
-template <typename T, int D, bool PAGE16, bool CONTIG>
+template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TSA_DECODE_WAVES_PER_EU)))
 void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ sl,
                          float* __restrict__ part) {
@@ -211,6 +307,21 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   if (blockIdx.x == 0 && wave == 0)
     for (int i = lane; i <= a.B; i += 64) a.pref_out[i] = pref[i];
 
+  // Fused step: this wave's LDS area (weights, then the unit ring). Data
+  // arrives by LDS DMA (global_load_lds_dwordx4: lane l's 16 bytes land at
+  // M0 + 16 l), issued before the tile loads that need it: loads complete in
+  // issue order, so once a tile's K/V registers are waited for, the unit data
+  // issued before them is in LDS.
+  typedef __attribute__((address_space(3))) void lds_void;
+  const int fused_off = ((kWaves * (a.B + 1) * 4 + 15) & ~15) + wave * kFusedWaveBytes;
+  char* const fbuf = reinterpret_cast<char*>(lds_i) + fused_off;
+  const uint32_t fbuf_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)fbuf));  // address-space cast
+  auto dma64 = [&](const void* src, uint32_t lds_byte) __attribute__((always_inline)) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_byte))
+                 : "memory", "m0");
+  };
+
   const int64_t total = static_cast<int64_t>(Hkv) * pref[a.B];
   const int64_t share = (total + a.NW - 1) / a.NW;
   const int v = blockIdx.x * kWaves + wave;
@@ -218,6 +329,10 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   const int64_t hi = min(total, lo + share);
   if (lo >= hi) return;  // no barrier follows: waves leave independently
   const int n_tiles = static_cast<int>(hi - lo);
+  if constexpr (FUSED) {  // weights: lanes 0-15 q_weight, 16-31 k_weight (32-63 repeat them)
+    const T* wsrc = static_cast<const T*>((lane & 16) ? a.kw : a.qw) + 8 * (lane & 15);
+    dma64(wsrc, fbuf_lds);
+  }
 
   // Locate tile lo: the last sequence with Hkv * pref[s] <= lo (that skips
   // empty sequences), then the kv head and the tile inside it.
@@ -255,9 +370,11 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   auto load_tile = [&](const TileCursor& tc, u32x4 (&qo)[KJ], u32x4 (&ko)[KJ], u32x4 (&vo)[4], auto nt) {
     constexpr bool NT = decltype(nt)::value;
     const int32_t* bt_row = a.bt + tc.s * a.bt_s0;
-    const T* qrow = static_cast<const T*>(a.q) + tc.s * a.q_ss + (tc.kvh * G + cq) * a.q_sh + 8 * g;
+    if constexpr (!FUSED) {  // (fused: Q is made once per unit, from LDS)
+      const T* qrow = static_cast<const T*>(a.q) + tc.s * a.q_ss + (tc.kvh * G + cq) * a.q_sh + 8 * g;
 #pragma unroll
-    for (int j = 0; j < KJ; ++j) qo[j] = *reinterpret_cast<const u32x4*>(qrow + 32 * j);
+      for (int j = 0; j < KJ; ++j) qo[j] = *reinterpret_cast<const u32x4*>(qrow + 32 * j);
+    }
     const T* kbase = static_cast<const T*>(a.kc) + tc.kvh * a.kc_h;
     const T* vbase = static_cast<const T*>(a.vc) + tc.kvh * a.vc_h;
     const int64_t tok0 = static_cast<int64_t>(tc.t) * 16;
@@ -390,15 +507,80 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   // compute cursor and stops on the wave's last tile (repeats hit the cache),
   // so every load is unconditional and each compute waits for its own tile.
   u32x4 qbuf[RING][KJ], kbuf[RING][KJ], vbuf[RING][4];
+
+  // ---- Fused step. unit_dma: a unit's raw q rows, and the cos/sin/raw k/raw v
+  // rows of its sequence's new token, into unit buffer ub (issued before the
+  // unit's first tile loads). make_q: the unit's normalised, rotated Q
+  // operand. new_token: in the unit's last tile, the new token's rotated K
+  // and raw V replace the cache rows that do not hold them yet, and are
+  // stored to the cache after the tile.
+  u32x4 qn[KJ];  // the current unit's Q operand (fused)
+  auto unit_dma = [&](const TileCursor& tc, int ub) __attribute__((always_inline)) {
+    const uint32_t base = fbuf_lds + 1024 + ub * kUnitBytes;
+    for (int i = 0; 4 * i < G; ++i) {  // heads 4i .. 4i+3, 16 lanes each
+      const int hh = min(4 * i + (lane >> 4), G - 1);
+      dma64(static_cast<const T*>(a.q) + tc.s * a.q_ss + (tc.kvh * G + hh) * a.q_sh + 8 * (lane & 15),
+            base + 1024 * i);
+    }
+    const int part = lane >> 4, ch = 8 * (lane & 15);
+    const T* src = part == 0   ? static_cast<const T*>(a.cos) + tc.s * a.cs_ss + ch
+                   : part == 1 ? static_cast<const T*>(a.sin) + tc.s * a.sn_ss + ch
+                   : part == 2 ? static_cast<const T*>(a.kn) + tc.s * a.kn_ss + tc.kvh * a.kn_sh + ch
+                               : static_cast<const T*>(a.vn) + tc.s * a.vn_ss + tc.kvh * a.vn_sh + ch;
+    dma64(src, base + 2048);
+  };
+  // Norm + RoPE of the row at byte offset row_off of this wave's fused area,
+  // with the weights at w_off and the cos/sin of unit buffer ub.
+  auto norm_row = [&](int row_off, int w_off, int ub, u32x4 (&outp)[KJ]) __attribute__((always_inline)) {
+    const RowOperand r = norm_rope_row128<T>(fbuf_lds + row_off, fbuf_lds + w_off,
+                                             fbuf_lds + 1024 + ub * kUnitBytes + 2048, a.eps);
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) outp[j] = r.v[j];
+  };
+  auto make_q = [&](int ub) __attribute__((always_inline)) {
+    norm_row(1024 + ub * kUnitBytes + 256 * cq, 0, ub, qn);
+  };
+  // The new token (position L - 1) in the tile starting at tok0.
+  auto new_token = [&](const TileCursor& tc, int ub, u32x4 (&ko)[KJ], u32x4 (&vo)[4], u32x4 (&kn)[KJ], u32x4& vnew,
+                       int& cn) __attribute__((always_inline)) {
+    const int64_t L = clamp_len(a, tc.s);
+    cn = static_cast<int>(L - 1 - static_cast<int64_t>(tc.t) * 16);  // 0..15
+    const int ubo = 1024 + ub * kUnitBytes;
+    norm_row(ubo + 2048 + 512, 256, ub, kn);
+    vnew = *reinterpret_cast<const u32x4*>(fbuf + ubo + 2048 + 768 + 16 * c);
+#pragma unroll
+    for (int j = 0; j < KJ; ++j)
+      if (c == cn) ko[j] = kn[j];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (4 * g + r == cn) vo[r] = vnew;
+  };
+  auto store_new_token = [&](const TileCursor& tc, const u32x4 (&kn)[KJ], const u32x4& vnew, int cn) {
+    int64_t phys, slot;
+    if (!page_of(a.bt + tc.s * a.bt_s0, clamp_len(a, tc.s) - 1, phys, slot)) return;  // (as the standalone store)
+    T* kd = static_cast<T*>(a.kc_out) + tc.kvh * a.kc_h + phys * a.kc_b + slot * ks;
+    T* vd = static_cast<T*>(a.vc_out) + tc.kvh * a.vc_h + phys * a.vc_b + slot * vs;
+    if (c == cn) {
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) *reinterpret_cast<u32x4*>(kd + 8 * (g + 4 * j)) = kn[j];
+    }
+    if (4 * g <= cn && cn < 4 * g + 4 && v_lane) *reinterpret_cast<u32x4*>(vd + 8 * c) = vnew;
+  };
+
   auto stream = [&](auto nt) {
     TileCursor ld = cur;
     int ld_left = n_tiles - 1;  // advances the load cursor may still make
+    int ld_unit = 0, cu_unit = 0;  // units entered by the load / compute cursor (fused)
     auto advance_load = [&]() {
       if (ld_left > 0) {
         ld.advance(pref, a.B, Hkv);
         --ld_left;
+        if constexpr (FUSED) {
+          if (ld.t == 0) unit_dma(ld, ++ld_unit % RING);
+        }
       }
     };
+    if constexpr (FUSED) unit_dma(ld, 0);
 #pragma unroll
     for (int d = 0; d < RING; ++d) {
       load_tile(ld, qbuf[d], kbuf[d], vbuf[d], nt);
@@ -409,7 +591,27 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
 #pragma unroll
       for (int d = 0; d < RING; ++d) {
         if (i + d < n_tiles) {
-          compute_tile(cur, qbuf[d], kbuf[d], vbuf[d]);
+          if constexpr (FUSED) {
+            const bool ustart = cur.t == 0 && i + d > 0;
+            if (ustart) ++cu_unit;
+            const bool ulast = cur.t + 1 == cur.n;
+            if (ustart || i + d == 0 || ulast) {
+              // The tile's K/V have landed, so has this unit's LDS data.
+              asm volatile("" ::"v"(kbuf[d][0]), "v"(vbuf[d][0]));
+              if (ustart || i + d == 0) make_q(cu_unit % RING);
+            }
+            if (ulast) {
+              u32x4 kn[KJ], vnew;
+              int cn;
+              new_token(cur, cu_unit % RING, kbuf[d], vbuf[d], kn, vnew, cn);
+              compute_tile(cur, qn, kbuf[d], vbuf[d]);
+              store_new_token(cur, kn, vnew, cn);
+            } else {
+              compute_tile(cur, qn, kbuf[d], vbuf[d]);
+            }
+          } else {
+            compute_tile(cur, qbuf[d], kbuf[d], vbuf[d]);
+          }
           if (cur.t + 1 == cur.n || i + d + 1 == n_tiles) flush(cur);
           cur.advance(pref, a.B, Hkv);
         }
@@ -591,7 +793,7 @@ static DecodePlan make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int32
 }
 
 template <typename T>
-static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream) {
+static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream, bool fused = false) {
   if (a.B == 0 || a.Hq == 0) return TSA_OK;
   if (!mfma) {
     paged_decode_generic<T><<<dim3(a.Hq, a.B), dim3(64), 0, stream>>>(a);
@@ -603,8 +805,12 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream) {
     const bool contig = a.kc_s == a.D && a.vc_s == a.D;
     const dim3 grid(a.W);
 #define TSA_DECODE_LAUNCH(DD, P16, CT) \
-  paged_decode_stream<T, DD, P16, CT><<<grid, dim3(kThreads), lds, stream>>>(a, a.bt, a.seq_lens, a.part)
-    if (a.D == 128) {
+  paged_decode_stream<T, DD, P16, CT, false><<<grid, dim3(kThreads), lds, stream>>>(a, a.bt, a.seq_lens, a.part)
+    if (fused) {  // checked by the caller: head_dim 128, 16-token pages, contiguous rows
+      const size_t lds_f = ((lds + 15) & ~size_t(15)) + static_cast<size_t>(kWaves) * kFusedWaveBytes;
+      paged_decode_stream<T, 128, true, true, true><<<grid, dim3(kThreads), lds_f, stream>>>(a, a.bt, a.seq_lens,
+                                                                                           a.part);
+    } else if (a.D == 128) {
       if (page16 && contig) TSA_DECODE_LAUNCH(128, true, true);
       else if (page16) TSA_DECODE_LAUNCH(128, true, false);
       else TSA_DECODE_LAUNCH(128, false, false);
@@ -638,10 +844,12 @@ extern "C" size_t tsa_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num
   return make_plan(num_seqs, num_heads, num_kv_heads, head_dim, num_workgroups).total;
 }
 
-extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache,
-                                const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
-                                double softmax_scale, void* workspace, size_t workspace_bytes,
-                                int32_t num_workgroups, void* stream) {
+namespace tsa {
+// Checks shared by both decode entry points; fills a (and mfma: whether the
+// stream kernel serves the call).
+static int prepare_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache, const tsa_view* v_cache,
+                          const tsa_view* block_tables, const tsa_view* seq_lens, double softmax_scale, void* workspace,
+                          size_t workspace_bytes, int32_t num_workgroups, DecodeArgs& a, bool& mfma) {
   TSA_REQUIRE(view_ok(query, 3), "query must be a 3D tensor (num_seqs, num_heads, head_dim)");
   TSA_REQUIRE(view_ok(out, 3), "out must be a 3D tensor shaped like query");
   TSA_REQUIRE(view_ok(k_cache, 4) && view_ok(v_cache, 4),
@@ -670,7 +878,7 @@ extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, cons
   TSA_UNSUPPORTED(D <= 512, "head_dim %lld > 512 is not implemented", (long long)D);
   TSA_REQUIRE(num_workgroups >= 0, "num_workgroups must be non-negative");
 
-  DecodeArgs a{};
+  a = DecodeArgs{};
   a.out = out->data; a.q = query->data; a.kc = k_cache->data; a.vc = v_cache->data;
   a.bt = static_cast<const int32_t*>(block_tables->data);
   a.seq_lens = static_cast<const int32_t*>(seq_lens->data);
@@ -686,7 +894,7 @@ extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, cons
   a.scale_log2 = static_cast<float>(softmax_scale * 1.4426950408889634);
 
   // The MFMA path keeps a per-wave tile prefix of B + 1 ints in LDS.
-  const bool mfma = (dt == TSA_BF16 || dt == TSA_F16) && (D == 64 || D == 128) && a.G <= 16 &&
+  mfma = (dt == TSA_BF16 || dt == TSA_F16) && (D == 64 || D == 128) && a.G <= 16 &&
                     static_cast<int64_t>(kWaves) * (B + 1) * 4 <= 64 * 1024 &&
                     rows_vec16(query) && rows_vec16(k_cache) && rows_vec16(v_cache) && out->stride[2] == 1;
   if (mfma) {
@@ -700,6 +908,20 @@ extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, cons
     a.part = reinterpret_cast<float*>(ws);
     a.pref_out = reinterpret_cast<int32_t*>(ws + plan.part_bytes);
   }
+  return TSA_OK;
+}
+}  // namespace tsa
+
+extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache,
+                                const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
+                                double softmax_scale, void* workspace, size_t workspace_bytes,
+                                int32_t num_workgroups, void* stream) {
+  DecodeArgs a;
+  bool mfma = false;
+  if (int rc = prepare_decode(out, query, k_cache, v_cache, block_tables, seq_lens, softmax_scale, workspace,
+                              workspace_bytes, num_workgroups, a, mfma))
+    return rc;
+  const int dt = query->dtype;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dt) {
     case TSA_BF16: return launch_decode<bf16_t>(a, mfma, st);
@@ -708,4 +930,49 @@ extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, cons
   }
   set_error("unsupported dtype");
   return TSA_ERR_UNSUPPORTED;
+}
+
+extern "C" int tsa_paged_decode_step(const tsa_view* out, const tsa_view* query, const tsa_view* k_new,
+                                     const tsa_view* v_new, const tsa_view* q_weight, const tsa_view* k_weight,
+                                     const tsa_view* cos, const tsa_view* sin, double eps, const tsa_view* k_cache,
+                                     const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
+                                     double softmax_scale, void* workspace, size_t workspace_bytes,
+                                     int32_t num_workgroups, void* stream) {
+  DecodeArgs a;
+  bool mfma = false;
+  if (int rc = prepare_decode(out, query, k_cache, v_cache, block_tables, seq_lens, softmax_scale, workspace,
+                              workspace_bytes, num_workgroups, a, mfma))
+    return rc;
+  const int dt = query->dtype;
+  const int64_t B = a.B, Hkv = a.Hkv, D = a.D;
+  TSA_REQUIRE(view_ok(k_new, 3) && view_ok(v_new, 3) && k_new->dtype == dt && v_new->dtype == dt,
+              "k and v must be 3D tensors (num_seqs, num_kv_heads, head_dim) of query's dtype");
+  TSA_REQUIRE(k_new->size[0] == B && k_new->size[1] == Hkv && k_new->size[2] == D && v_new->size[0] == B &&
+                  v_new->size[1] == Hkv && v_new->size[2] == D,
+              "k and v must be (num_seqs, num_kv_heads, head_dim)");
+  TSA_REQUIRE(view_ok(q_weight, 1) && view_ok(k_weight, 1) && q_weight->size[0] == D && k_weight->size[0] == D &&
+                  q_weight->dtype == dt && k_weight->dtype == dt,
+              "q_weight and k_weight must be (head_dim,) of query's dtype");
+  TSA_REQUIRE(view_ok(cos, 2) && view_ok(sin, 2) && cos->size[0] == B && cos->size[1] == D && sin->size[0] == B &&
+                  sin->size[1] == D && cos->dtype == dt && sin->dtype == dt,
+              "cos and sin must be (num_seqs, head_dim) of query's dtype");
+  // The fused kernel covers the Qwen3 decode shape; other calls go through
+  // tsa_qk_norm_rope_store + tsa_paged_decode.
+  const size_t lds = ((static_cast<size_t>(kWaves) * (B + 1) * 4 + 15) & ~size_t(15)) +
+                     static_cast<size_t>(kWaves) * kFusedWaveBytes;
+  TSA_UNSUPPORTED(mfma && D == 128 && a.BS % 16 == 0 && a.kc_s == D && a.vc_s == D && a.G <= 8 &&
+                      rows_vec16(k_new) && rows_vec16(v_new) && rows_vec16(q_weight) && rows_vec16(k_weight) &&
+                      rows_vec16(cos) && rows_vec16(sin) && lds <= 64 * 1024,
+                  "the fused decode step needs a 16-bit dtype, head_dim 128, 16-token-multiple pages, contiguous "
+                  "cache rows, at most 8 q-heads per kv head and unit-stride 16-byte-aligned rows");
+  a.kn = k_new->data; a.vn = v_new->data; a.qw = q_weight->data; a.kw = k_weight->data;
+  a.cos = cos->data; a.sin = sin->data;
+  a.kn_ss = k_new->stride[0]; a.kn_sh = k_new->stride[1];
+  a.vn_ss = v_new->stride[0]; a.vn_sh = v_new->stride[1];
+  a.cs_ss = cos->stride[0]; a.sn_ss = sin->stride[0];
+  a.eps = static_cast<float>(eps);
+  a.kc_out = k_cache->data; a.vc_out = v_cache->data;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dt == TSA_BF16) return launch_decode<bf16_t>(a, true, st, true);
+  return launch_decode<f16_t>(a, true, st, true);
 }

@@ -7,7 +7,7 @@ eager PyTorch.
 """
 
 from .kv_cache import store_kv_cache, store_kv_cache_batched, store_kv_cache_paged
-from .paged_attention import paged_attention_forward
+from .paged_attention import paged_attention_forward, paged_decode_step
 from .qk_norm_rope import qk_norm_rope, qk_norm_rope_store
 from .varlen_attention import flash_attn_varlen_func
 
@@ -16,6 +16,7 @@ __all__ = [
     "store_kv_cache_batched",
     "store_kv_cache_paged",
     "paged_attention_forward",
+    "paged_decode_step",
     "flash_attn_varlen_func",
     "qk_norm_rope",
     "qk_norm_rope_store",

@@ -54,7 +54,7 @@ def paged_attention_forward(
     ``seq_lens[s]`` tokens gathered through ``block_tables[s]``; q-head h reads
     kv head ``h // (Hq / Hkv)``. query: (B, Hq, D); caches (NB, Hkv, BS, D);
     block_tables (B, max_blocks) int32; seq_lens (B,) int32.
-    ``num_workgroups`` (workgroups sharing the tile list, 0 = two per CU) and
+    ``num_workgroups`` (workgroups sharing the tile list, 0 = one per CU) and
     ``out`` are extensions; the defaults reproduce the reference call.
     """
     if query.dim() != 3:
@@ -90,4 +90,61 @@ def paged_attention_forward(
         stream,
     )
     _lib.check(rc, "paged_attention_forward")
+    return out
+
+
+def paged_decode_step(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    eps: float,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    *,
+    num_workgroups: int = 0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One decode step of the Qwen3 attention layer: QK RMSNorm + RoPE of the
+    new token, its paged K/V store, and paged attention, in two launches.
+
+    q (B, Hq, D), k and v (B, Hkv, D) are the raw projections of each
+    sequence's new token, at position ``seq_lens[s] - 1``; cos/sin (B, D) are
+    for those positions. Same results as ``qk_norm_rope_store`` followed by
+    ``paged_attention_forward``. Raises NotImplementedError for shapes the
+    fused kernel does not cover (head_dim != 128, fp32, pages not a multiple
+    of 16 tokens, strided cache rows, more than 8 q-heads per kv head).
+    """
+    dev = _lib.require_device(q, k, v, q_weight, k_weight, cos, sin, k_cache, v_cache, block_tables, seq_lens)
+    if block_tables.dtype != torch.int32:
+        block_tables = block_tables.to(torch.int32)
+    if seq_lens.dtype != torch.int32:
+        seq_lens = seq_lens.to(torch.int32)
+    num_seqs, num_heads, head_dim = q.shape
+    num_kv_heads = k_cache.shape[1]
+    if out is None:
+        out = torch.empty_like(q)
+    lib = _lib.load()
+    stream = _lib.stream_of(dev)
+    nbytes = int(lib.tsa_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim,
+                                                      block_tables.shape[1], k_cache.shape[2], num_workgroups))
+    ws = _workspace(dev, stream, nbytes)
+    v8 = [_lib.view(t) for t in (out, q, k, v, q_weight, k_weight, cos, sin)]
+    v4 = [_lib.view(t) for t in (k_cache, v_cache, block_tables, seq_lens)]
+    rc = lib.tsa_paged_decode_step(
+        *map(_lib.ref, v8),
+        float(eps),
+        *map(_lib.ref, v4),
+        1.0 / math.sqrt(head_dim),
+        ws.data_ptr() if ws is not None else None,
+        ws.numel() if ws is not None else 0,
+        int(num_workgroups),
+        stream,
+    )
+    _lib.check(rc, "paged_decode_step")
     return out

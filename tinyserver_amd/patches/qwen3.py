@@ -32,7 +32,7 @@ from typing import Callable
 import torch
 
 from ..inference_context import InferenceContext, get_inference_context
-from ..kernels import flash_attn_varlen_func, paged_attention_forward, qk_norm_rope_store
+from ..kernels import flash_attn_varlen_func, paged_attention_forward, paged_decode_step, qk_norm_rope_store
 
 
 def _available_memory(memory_utilization: float) -> int:
@@ -72,6 +72,7 @@ class DeviceMetadata:
     max_seqlen: int
     positions: torch.Tensor | None  # decode: (B,) int32 position of each new token
     seq_lens: torch.Tensor | None   # decode: (B,) int32 = positions + 1
+    table_slots: int = 0            # sum of the block tables' lengths (host-side size of the step's KV)
 
 
 def device_metadata(ctx: InferenceContext, position_ids: torch.Tensor | None, num_tokens: int,
@@ -115,10 +116,21 @@ def device_metadata(ctx: InferenceContext, position_ids: torch.Tensor | None, nu
         seq_lens = positions + 1
     dev = packed.to(device)
     meta = DeviceMetadata(dev[:n_tab].view(len(seqs), width), dev[n_tab:], max(lengths, default=0), positions,
-                          seq_lens)
+                          seq_lens, sum(len(s["block_table"]) for s in seqs))
     ctx._device_meta = (position_ids, (ctx.mode, num_tokens, str(device), getattr(position_ids, "_version", None)),
                         meta)
     return meta
+
+
+# A decode step whose KV spans at most this many 16-token tiles (per kv head
+# summed over the heads) takes the single-launch fused step; larger ones take
+# the norm/store launch followed by paged attention. The fused kernel saves a
+# launch (a few microseconds) but each of its waves normalises its units' rows
+# while its own loads drain, a fixed cost per wave that outweighs the launch
+# once the waves stream dozens of tiles each. Measured at head_dim 128 on 256
+# CUs: Qwen3-0.6B batch 4 (550 tiles) 27 us fused vs 47 us; Qwen3-8B batch 64
+# (74k tiles) 136 us fused vs 131 us.
+FUSED_DECODE_MAX_TILES = 16384
 
 
 def _patch_single_layer(layer: torch.nn.Module,
@@ -156,6 +168,16 @@ def _patch_single_layer(layer: torch.nn.Module,
                                               meta.block_tables, meta.cu_seqlens)
             out = flash_attn_varlen_func(q_rot, k_rot, v, meta.cu_seqlens, meta.cu_seqlens, meta.max_seqlen,
                                          meta.max_seqlen, causal=True, softmax_scale=head_dim**-0.5)
+        elif (getattr(attn, "_tsa_fused_decode", True)
+              and meta.table_slots * block_size // 16 * num_kv_heads <= FUSED_DECODE_MAX_TILES):
+            try:
+                out = paged_decode_step(q, k, v, attn.q_norm.weight, attn.k_norm.weight, cos, sin,
+                                        attn.q_norm.variance_epsilon, attn.k_cache, attn.v_cache,
+                                        meta.block_tables, meta.seq_lens)
+            except NotImplementedError:  # a shape the fused kernel does not cover: stop trying it
+                attn._tsa_fused_decode = False
+                return _page_attention_forward(hidden_states, attention_mask, position_ids, past_key_values,
+                                               use_cache, position_embeddings, **kwargs)
         else:
             q_rot, _ = qk_norm_rope_store(q, k, v, attn.q_norm.weight, attn.k_norm.weight, cos, sin,
                                           attn.q_norm.variance_epsilon, attn.k_cache, attn.v_cache,
