@@ -191,6 +191,35 @@ def bench_prefill(name, steps, warmup):
     }
 
 
+def bench_sampling(steps, warmup, batch=64, vocab=151936):
+    """sample_tokens over a Qwen3-vocab batch: bf16 logits (N(0, 2.5) plus a
+    few boosted tokens per row), temperature 0.8, top_k 50, top_p 0.9 (the
+    engine's usual settings), seeded uniforms. One launch per call."""
+    from tinyserver_amd.kernels import sample_tokens
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(21)
+    logits = torch.randn(batch, vocab, generator=g) * 2.5
+    logits.scatter_add_(1, torch.randint(0, vocab, (batch, 8), generator=g), torch.rand(batch, 8, generator=g) * 12)
+    logits = logits.to(dev, torch.bfloat16)
+    temperature = torch.full((batch,), 0.8, device=dev)
+    top_k = torch.full((batch,), 50, dtype=torch.int64, device=dev)
+    top_p = torch.full((batch,), 0.9, device=dev)
+    uniforms = torch.rand(batch, generator=g).to(dev)
+    out = torch.empty(batch, dtype=torch.int64, device=dev)
+    cases = {}
+    for label, k, p in (("topk50_topp0.9", 50, 0.9), ("topp0.9", 0, 0.9), ("full", 0, 1.0)):
+        top_k.fill_(k)
+        top_p.fill_(p)
+
+        def call(i):
+            sample_tokens(logits, temperature, top_k, top_p, uniforms, out=out)
+
+        us = time_region(call, steps, warmup)[0] * 1e3
+        cases[label] = {"us_per_call": us, "logits_gbs": batch * vocab * 2 / (us * 1e-6) / 1e9}
+    return {"workload": f"sample_tokens bs{batch} vocab{vocab} bf16", "batch": batch, "vocab": vocab, **cases}
+
+
 def cpu_baseline(w, target_seconds=10.0, max_reps=50):
     """The reference's CPU decode path (gather loop + repeat_interleave + SDPA) on
     the whole batch, timed on this host: repeated for about `target_seconds` of
@@ -249,7 +278,8 @@ def measured_traffic():
 
 
 def _round(d):
-    return {k: (round(v, 3) if isinstance(v, float) else v) for k, v in d.items()}
+    return {k: (round(v, 3) if isinstance(v, float) else _round(v) if isinstance(v, dict) else v)
+            for k, v in d.items()}
 
 
 def main():
@@ -347,6 +377,7 @@ def main():
         sec["qwen3-4b-mixed-decode"] = _round(s)
         for name in ("qwen3-8b-prefill-16seq", "qwen3-4b-mixed-prefill"):
             sec[name] = _round(bench_prefill(name, n2, 3))
+        sec["sampling-qwen3-vocab-bs64"] = _round(bench_sampling(n2, 3))
         line["secondary"] = sec
     print(json.dumps(line), flush=True)
 

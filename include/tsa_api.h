@@ -30,6 +30,7 @@
  *                           norm/RoPE, store and paged attention, fused
  *   tsa_varlen_prefill      server/model/kernels/varlen_attention.py:145-218
  *                           (flash_attn_varlen_func)
+ *   tsa_sample_tokens       server/model/sampling.py:119-194 (sample_tokens)
  */
 #ifndef TSA_API_H
 #define TSA_API_H
@@ -172,6 +173,19 @@ int tsa_varlen_prefill(const tsa_view* out, const tsa_view* q, const tsa_view* k
                        const tsa_view* v, const tsa_view* cu_seqlens_q,
                        const tsa_view* cu_seqlens_k, int64_t max_seqlen_q, int64_t max_seqlen_k,
                        int32_t causal, double softmax_scale, void* stream);
+
+/* sample_tokens (server/model/sampling.py:119-194): one token per row of
+ * logits (B, V) (bf16, f16 or f32): x = logits / max(temperature, 1e-5), in
+ * rank order (x descending, index ascending, the stable sort's order) keep
+ * the first top_k ranks (0 or >= V: all), then the ranks whose preceding mass
+ * is at most top_p (rank 0 always), and pick the first kept rank whose
+ * cumulative mass reaches uniforms * (kept mass); rows with temperature <= 0
+ * take the first index of the maximum. temperature, top_p, uniforms: (B,)
+ * f32; top_k: (B,) int32 or int64; out: (B,) int64. One launch, no host
+ * sync, no workspace. */
+int tsa_sample_tokens(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature,
+                      const tsa_view* top_k, const tsa_view* top_p, const tsa_view* uniforms,
+                      void* stream);
 
 #ifdef __cplusplus
 }

@@ -139,6 +139,19 @@ def test_stream_partition(num_workgroups):
         assert_close(out[keep], ref[keep], what=f"W={num_workgroups} call {call}")
 
 
+def test_workspace_reuse_across_shapes():
+    """Calls of different shapes and worker counts alternating on one
+    workspace: nothing a call leaves in it (partials over a wide range from a
+    small call with many workers) can disturb a later call."""
+    big = _random_paged_inputs([3000, 17, 900, 64, 2500, 1, 4000, 333], 32, 8, 128, 16, torch.bfloat16, seed=41)
+    small = _random_paged_inputs([700, 5], 16, 4, 128, 16, torch.bfloat16, seed=42)
+    refs = [op.paged_attention_forward(*x[:4], 16, x[4]) for x in (big, small)]
+    for call, (x, ref, nwg) in enumerate([(big, refs[0], 0), (small, refs[1], 4096), (big, refs[0], 7),
+                                          (small, refs[1], 1), (big, refs[0], 0)]):
+        out = _run(*x[:4], 16, x[4], num_workgroups=nwg).cpu()
+        assert_close(out, ref, what=f"call {call} (num_workgroups={nwg})")
+
+
 def test_repeated_calls_are_identical():
     """More calls than the stream kernel's work-queue slots, two shapes
     interleaved: whichever wave streams a chunk, its partial lands in the same

@@ -1,0 +1,161 @@
+"""Batched sampling on the GPU (tsa_sample_tokens) vs the oracle.
+
+The kernel returns token indices, so the bar is equality with the oracle's
+(the reference's sort/softmax/cumsum/searchsorted in fp32). The reference
+sums fp32 probabilities in sort order; the kernel sums the same masses
+exactly. A row may therefore differ only where one of its decisions lies
+within fp32 cumsum rounding of its threshold: the oracle's fp64
+decision_margin below MARGIN, which these tests check for every differing
+row. Cases: the reference's known answers and allowed-set rule
+(tests/model/test_batch_sampling.py); a Qwen3-vocab batch (151936 tokens)
+with mixed temperatures, top-k, top-p and greedy rows in bf16, f16 and f32;
+all-equal and few-valued rows (ties resolved in index order, buckets split
+again); rows half masked to -inf; strided logits; repeat calls; a row alone
+vs inside a batch.
+"""
+
+import pytest
+import torch
+
+from oracle import sampling as osm
+from tinyserver_amd.kernels import sample_tokens
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+MARGIN = 2e-4  # fp32 cumsum rounding over a 151936-token row, with room
+
+
+def _gpu(rows, temperature, top_k, top_p, uniforms, dtype=torch.float32):
+    t = lambda v, dt: torch.tensor(v, dtype=dt, device=DEV)
+    logits = rows.to(DEV, dtype) if torch.is_tensor(rows) else t(rows, dtype)
+    out = sample_tokens(logits, t(temperature, torch.float32), t(top_k, torch.int64), t(top_p, torch.float32),
+                        t(uniforms, torch.float32))
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _oracle(rows, temperature, top_k, top_p, uniforms, dtype=torch.float32):
+    t = lambda v, dt: torch.tensor(v, dtype=dt)
+    logits = (rows if torch.is_tensor(rows) else t(rows, torch.float32)).to(dtype)
+    return osm.sample_tokens(logits, t(temperature, torch.float32), t(top_k, torch.int64), t(top_p, torch.float32),
+                             t(uniforms, torch.float32))
+
+
+def _compare(rows, temperature, top_k, top_p, uniforms, dtype=torch.float32, what=""):
+    got = _gpu(rows, temperature, top_k, top_p, uniforms, dtype)
+    ref = _oracle(rows, temperature, top_k, top_p, uniforms, dtype)
+    logits = (rows if torch.is_tensor(rows) else torch.tensor(rows)).to(dtype).float()
+    diff = (got != ref).nonzero().flatten().tolist()
+    for i in diff:
+        m = osm.decision_margin(logits[i], temperature[i], top_k[i], top_p[i], uniforms[i])
+        assert m < MARGIN, f"{what} row {i}: kernel {got[i].item()} vs oracle {ref[i].item()}, margin {m:.3e}"
+    print(f"{what}: {len(diff)} of {len(got)} rows differ, all within fp32 rounding of a threshold", flush=True)
+    return got, diff
+
+
+def test_reference_known_answers():
+    assert _gpu([[0.0] * 4] * 4, [1.0] * 4, [0] * 4, [1.0] * 4, [0.1, 0.4, 0.6, 0.9]).tolist() == [0, 1, 2, 3]
+    assert _gpu([[0.0, 5.0, 5.0, 1.0]], [0.0], [0], [1.0], [0.99]).tolist() == [1]
+    assert _gpu([[1.0, 9.0, 3.0, 7.0]], [1.0], [0], [1.0], [0.0]).tolist() == [1]
+    row = [5.0, 4.0, 3.0, 2.0, 1.0, 0.0]
+    assert _gpu([row] * 3, [1.0] * 3, [1, 2, 3], [1.0] * 3, [0.999] * 3).tolist() == [0, 1, 2]
+    rows = [[-10.0] * 10 for _ in range(3)]
+    rows[0][2], rows[1][7], rows[2][0] = 10.0, 10.0, 10.0
+    assert _gpu(rows, [1.0] * 3, [0] * 3, [1e-6] * 3, [0.9] * 3).tolist() == [2, 7, 0]
+    out = _gpu(torch.randn(3, 10), [1.0] * 3, [0] * 3, [1.0] * 3, [0.5] * 3)
+    assert out.shape == (3,) and out.dtype == torch.int64
+
+
+@pytest.mark.parametrize("top_k,top_p", [(0, 1.0), (5, 1.0), (0, 0.6), (5, 0.6), (1, 1.0), (1000, 1.0), (3, 0.3)])
+def test_picks_inside_allowed_set(top_k, top_p):
+    g = torch.Generator().manual_seed(4)
+    logits = torch.randn(4, 60, generator=g)
+    allowed = [osm.allowed_set(logits[i], 0.9, top_k, top_p) for i in range(4)]
+    for step in range(40):
+        u = [(step * 4 + i) / 160.0 for i in range(4)]
+        got = _gpu(logits, [0.9] * 4, [top_k] * 4, [top_p] * 4, u)
+        assert all(t in allowed[i] for i, t in enumerate(got.tolist())), (step, got.tolist())
+
+
+def _qwen3_batch(seed, b=64, v=151936):
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(b, v, generator=g) * 2.5
+    hot = torch.randint(0, v, (b, 8), generator=g)
+    logits.scatter_add_(1, hot, torch.rand(b, 8, generator=g) * 12)  # a few likely tokens per row
+    temperature = [[0.0, 0.6, 1.0, 1.3][i % 4] for i in range(b)]
+    top_k = [[0, 1, 20, 50, 1000, 0, 200][i % 7] for i in range(b)]
+    top_p = [[1.0, 0.9, 0.5, 0.95, 0.8][i % 5] for i in range(b)]
+    uniforms = torch.rand(b, generator=g).tolist()
+    return logits, temperature, top_k, top_p, uniforms
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_qwen3_vocab_batch(dtype):
+    logits, temperature, top_k, top_p, uniforms = _qwen3_batch(11)
+    _, diff = _compare(logits, temperature, top_k, top_p, uniforms, dtype, what=f"qwen3 vocab {dtype}")
+    assert len(diff) <= 2
+
+
+def test_ties_and_few_values():
+    v = 151936
+    g = torch.Generator().manual_seed(12)
+    equal = torch.zeros(4, v)
+    levels = (torch.randint(0, 6, (4, v), generator=g).float() - 3.0) * 0.5  # six values: buckets far past LDS
+    rows = torch.cat([equal, levels])
+    temperature = [1.0] * 8
+    top_k = [0, 1000, 7, 0, 0, 5000, 100000, 0]
+    top_p = [1.0, 1.0, 1.0, 0.3, 1.0, 0.9, 0.5, 0.99]
+    uniforms = [0.37, 0.999, 0.0, 0.71, 0.5, 0.25, 0.62, 0.9]
+    got, _ = _compare(rows, temperature, top_k, top_p, uniforms, what="ties")
+    assert got[0].item() == int(0.37 * v)  # all equal: rank = index, uniform over the vocab
+    # Thousands of equal probabilities: the fp32 cumsum drifts by more than one
+    # of them, so hold the kernel to the same steps in fp64 instead.
+    t = lambda vals, dt: torch.tensor(vals, dtype=dt)
+    exact = osm.sample_tokens(rows, t(temperature, torch.float32), t(top_k, torch.int64), t(top_p, torch.float32),
+                              t(uniforms, torch.float32), dtype=torch.float64)
+    assert got.tolist() == exact.tolist()
+
+
+def test_masked_rows():
+    v = 151936
+    g = torch.Generator().manual_seed(13)
+    logits = torch.randn(6, v, generator=g) * 2
+    logits[:, ::2] = float("-inf")
+    temperature = [1.0, 0.7, 1.0, 1.0, 0.0, 1.2]
+    top_k = [0, 100000, 50, 0, 0, 80000]
+    top_p = [1.0, 1.0, 0.9, 0.5, 1.0, 0.99]
+    uniforms = [0.5, 0.999, 0.1, 0.3, 0.7, 0.0]
+    got, _ = _compare(logits, temperature, top_k, top_p, uniforms, what="masked")
+    assert all(t % 2 == 1 for t in got.tolist())
+
+
+def test_strided_logits_and_repeat_calls():
+    logits, temperature, top_k, top_p, uniforms = _qwen3_batch(14, b=16)
+    wide = torch.zeros(16, 2, logits.shape[1] + 64)
+    wide[:, 1, :-64] = logits
+    view = wide.to(DEV, torch.bfloat16)[:, 1, :-64]  # row stride 2 * (V + 64), like out.logits[0, :B, :]
+    t = lambda v, dt: torch.tensor(v, dtype=dt, device=DEV)
+    args = (t(temperature, torch.float32), t(top_k, torch.int64), t(top_p, torch.float32), t(uniforms, torch.float32))
+    first = sample_tokens(view, *args)
+    for _ in range(20):
+        assert torch.equal(sample_tokens(view, *args), first)
+    assert torch.equal(first.cpu(), _gpu(logits, temperature, top_k, top_p, uniforms, torch.bfloat16))
+
+
+def test_row_alone_matches_row_in_batch():
+    logits, temperature, top_k, top_p, uniforms = _qwen3_batch(15, b=16, v=4096)
+    batched = _gpu(logits, temperature, top_k, top_p, uniforms)
+    for i in range(16):
+        assert _gpu(logits[i : i + 1], temperature[i : i + 1], top_k[i : i + 1], top_p[i : i + 1],
+                    uniforms[i : i + 1]).item() == batched[i].item()
+
+
+def test_rejects_bad_shapes():
+    with pytest.raises(ValueError, match="Expected logits shape"):
+        sample_tokens(torch.randn(10, device=DEV), torch.ones(1, device=DEV),
+                      torch.zeros(1, dtype=torch.int64, device=DEV), torch.ones(1, device=DEV),
+                      torch.ones(1, device=DEV) * 0.5)
+    with pytest.raises(ValueError, match="Expected top_k shape"):
+        sample_tokens(torch.randn(2, 10, device=DEV), torch.ones(2, device=DEV),
+                      torch.zeros(3, dtype=torch.int64, device=DEV), torch.ones(2, device=DEV),
+                      torch.ones(2, device=DEV) * 0.5)
