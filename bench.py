@@ -308,7 +308,9 @@ def main():
 
     _lib.load()
     if args.workload:
-        if "prefill" in args.workload:
+        if args.workload == "sampling-qwen3-vocab-bs64":
+            res = bench_sampling(args.steps, args.warmup)
+        elif "prefill" in args.workload:
             res = bench_prefill(args.workload, args.steps, args.warmup)
         else:
             res, _ = bench_decode(args.workload, args.steps, args.warmup, args.num_workgroups)

@@ -24,6 +24,10 @@
 // integers, so every sum is exact and order-free: the kernel is deterministic
 // and its decisions differ from the reference's fp32 cumsum only where a
 // target lies within fp32 rounding of a cumulative sum.
+// The usual path builds one histogram (counts and masses of every element)
+// and reads all three decisions from it, gathering only the buckets where a
+// cut or the pick falls; a bucket too large for LDS sends the row to the
+// per-decision path above.
 // Greedy rows (temperature <= 0) take the first index of the row's maximum,
 // which is the stable sort's rank 0, as the reference does.
 #include <cmath>
@@ -36,6 +40,7 @@ constexpr int kSampThreads = 1024;
 constexpr int kSampWaves = kSampThreads / 64;
 constexpr int kBuckets = 2048;
 constexpr int kCap = 8192;  // elements of one bucket sorted in LDS
+constexpr int kPrefixMax = 1024;  // top ranks worth one gather + sort + scans instead of per-bucket gathers
 constexpr int kMaxLevels = 4;
 constexpr float kMassOne = 1099511627776.0f;  // 2^40: the row maximum's mass
 
@@ -65,6 +70,8 @@ __device__ __forceinline__ uint64_t rank_key(float x, int64_t i) {
 struct SampleLds {
   uint32_t cnt[kBuckets];
   uint64_t wsum[kBuckets];  // weight per bucket, then its exclusive prefix
+  uint32_t pcnt[kBuckets];   // shared histogram: exclusive prefixes of cnt
+  uint64_t pmass[kBuckets];  // and of the masses
   uint64_t keys[kCap];
   uint64_t wave_u64[kSampWaves];
   float wave_f[kSampWaves];
@@ -86,6 +93,25 @@ struct RowSampler {
   int tid, lane, wave;
 
   __device__ float x_at(int64_t i) const { return __fdiv_rn(to_float(row[i * a.ls1]), t); }
+  // The value the single-histogram path orders by. For 16-bit logits it is
+  // the logit itself: distinct 16-bit values differ by at least 2^-8
+  // relatively, so dividing them by one t keeps them distinct and in order,
+  // and ties in x are exactly ties in the logit. fp32 logits order by x.
+  static constexpr bool kByLogit = sizeof(T) == 2;
+  __device__ float key_at(int64_t i) const { return kByLogit ? to_float(row[i * a.ls1]) : x_at(i); }
+  __device__ float key_to_x(float k) const { return kByLogit ? __fdiv_rn(k, t) : k; }
+  float kmax;  // row maximum of key_at
+  float kc;    // log2(e) / t for 16-bit logits, log2(e) for fp32 (keys are x)
+  // 2^40 exp(x - xmax) from a key, as exp2((key - kmax) * kc) on v_exp_f32,
+  // truncated to an integer in two 32-bit halves (exact: the value has at
+  // most 24 significant bits). The single-histogram path's mass; the row
+  // maximum weighs exactly 2^40.
+  __device__ uint64_t mass_key(float kv) const {
+    const float v = fast_exp2((kv - kmax) * kc) * kMassOne;
+    const uint32_t hi = static_cast<uint32_t>(v * 2.3283064365386963e-10f);  // v / 2^32
+    const uint32_t lo = static_cast<uint32_t>(v - static_cast<float>(hi) * 4294967296.0f);
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+  }
   __device__ uint64_t mass(float x) const {
     return static_cast<uint64_t>(rintf(expf(x - xmax) * kMassOne));
   }
@@ -141,6 +167,218 @@ struct RowSampler {
         }
         __syncthreads();
       }
+  }
+
+  __device__ static int bucket0(float x, float h, float sc) {
+    if (x == -INFINITY) return kBuckets - 1;
+    const float f = (h - x) * sc;
+    return f >= static_cast<float>(kBuckets - 1) ? kBuckets - 1 : static_cast<int>(f);
+  }
+
+  // Exclusive prefix over the buckets (two per thread) of in[] into out[].
+  template <typename U>
+  __device__ void scan2(const U* in, U* out) {
+    const U w0 = in[2 * tid], w1 = in[2 * tid + 1];
+    uint64_t incl = static_cast<uint64_t>(w0) + w1;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t up = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += up;
+    }
+    __syncthreads();
+    if (lane == 63) s.wave_u64[wave] = incl;
+    __syncthreads();
+    uint64_t before = 0;
+    for (int w = 0; w < wave; ++w) before += s.wave_u64[w];
+    const uint64_t excl = before + incl - (static_cast<uint64_t>(w0) + w1);
+    out[2 * tid] = static_cast<U>(excl);
+    out[2 * tid + 1] = static_cast<U>(excl + w0);
+    __syncthreads();
+  }
+
+  // The smallest non-empty bucket b <= last whose running mass through b
+  // (the full bucket, or last_incl for bucket `last`) reaches the target.
+  __device__ int first_bucket(int last, uint64_t last_incl, bool ge, double target) {
+    if (tid == 0) s.found_bucket = kBuckets;
+    __syncthreads();
+    for (int b = tid; b < kBuckets; b += kSampThreads) {
+      if (b > last || s.cnt[b] == 0) continue;
+      const double incl = static_cast<double>(b == last ? last_incl : s.pmass[b] + s.wsum[b]);
+      if (ge ? incl >= target : incl > target) atomicMin(&s.found_bucket, b);
+    }
+    __syncthreads();
+    const int fb = s.found_bucket;
+    __syncthreads();
+    return fb;
+  }
+
+  // Gathers bucket b of the shared histogram into s.keys in rank order.
+  __device__ void gather_sorted(int b, float scale, int& cached) {
+    if (cached == b) return;
+    if (tid == 0) s.n_gather = 0;
+    __syncthreads();
+    for (int64_t i = tid; i < a.V; i += kSampThreads) {
+      const float kv = key_at(i);
+      if (bucket0(kv, kmax, scale) == b) s.keys[atomicAdd(&s.n_gather, 1u)] = rank_key(kv, i);
+    }
+    __syncthreads();
+    sort_keys(static_cast<int>(s.cnt[b]));
+    cached = b;
+  }
+
+  // Gathers every bucket up to nb (the top ranks of the row) into s.keys in
+  // rank order: position e of the sorted list is rank e of the row.
+  __device__ void gather_prefix(int nb, float scale) {
+    if (tid == 0) s.n_gather = 0;
+    __syncthreads();
+    for (int64_t i = tid; i < a.V; i += kSampThreads) {
+      const float kv = key_at(i);
+      if (bucket0(kv, kmax, scale) <= nb) s.keys[atomicAdd(&s.n_gather, 1u)] = rank_key(kv, i);
+    }
+    __syncthreads();
+    sort_keys(static_cast<int>(s.pcnt[nb] + s.cnt[nb]));
+  }
+
+  // The decisions on the sorted top ranks [0, n): top-k keeps the first
+  // lim_k, top-p the ranks through the first whose running mass exceeds
+  // p * Z (z: the kept mass when known from the histogram, else summed
+  // here), the pick is the first kept rank reaching u * (kept mass).
+  __device__ int64_t decide_on_prefix(int n, int lim_k, bool z_known, uint64_t z, double p, double u) {
+    uint64_t cum, tot;
+    const int lk = lim_k >= 0 ? lim_k : n;
+    if (!z_known) {
+      scan_sorted(lk, 0, true, -1.0, cum, tot);
+      z = tot;
+    }
+    int lim = lk;
+    uint64_t kept = z;
+    const int pos_p = scan_sorted(lk, 0, false, p * static_cast<double>(z), cum, tot);
+    if (pos_p >= 0) {
+      lim = pos_p + 1;
+      kept = cum;
+    }
+    const int pos = scan_sorted(lim, 0, true, u * static_cast<double>(kept), cum, tot);
+    if (pos < 0) return -1;
+    const int64_t token = static_cast<uint32_t>(s.keys[pos]);
+    __syncthreads();
+    return token;
+  }
+
+  // Over the first `limit` sorted elements, with `base` before them: the
+  // position of the one element that reaches the target (see select), its
+  // running mass through it, and the mass of all `limit` elements.
+  __device__ int scan_sorted(int limit, uint64_t base, bool ge, double target, uint64_t& cum_at, uint64_t& total) {
+    const int per = (limit + kSampThreads - 1) / kSampThreads;
+    const int e0 = min(limit, tid * per), e1 = min(limit, e0 + per);
+    uint64_t mine = 0;
+    for (int e = e0; e < e1; ++e) mine += mass_key(key_at(static_cast<uint32_t>(s.keys[e])));
+    uint64_t incl = mine;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t up = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += up;
+    }
+    __syncthreads();
+    if (lane == 63) s.wave_u64[wave] = incl;
+    if (tid == 0) s.found_index = -1;
+    __syncthreads();
+    uint64_t cum = base + incl - mine;
+    for (int w = 0; w < wave; ++w) cum += s.wave_u64[w];
+    uint64_t all = base;
+    for (int w = 0; w < kSampWaves; ++w) all += s.wave_u64[w];
+    for (int e = e0; e < e1; ++e) {
+      const uint64_t excl = cum;
+      cum += mass_key(key_at(static_cast<uint32_t>(s.keys[e])));
+      const bool r = ge ? static_cast<double>(cum) >= target : static_cast<double>(cum) > target;
+      const bool rx = ge ? static_cast<double>(excl) >= target : static_cast<double>(excl) > target;
+      if (r && (e == 0 || !rx)) {
+        s.found_index = e;
+        s.found_cum = cum;
+        break;
+      }
+    }
+    __syncthreads();
+    const int pos = static_cast<int>(s.found_index);
+    cum_at = s.found_cum;
+    total = all;
+    __syncthreads();
+    return pos;
+  }
+
+  // All three decisions from one histogram of every element (count and
+  // mass): each decision's kept set is a prefix in rank order -- full buckets,
+  // then a known prefix of one sorted bucket -- so only the buckets where a
+  // cut or the pick falls are gathered. False if such a bucket is larger
+  // than LDS holds (the caller then runs the per-decision path).
+  __device__ bool fast(float lo, int64_t k, bool cut_k, double p, double u, int64_t& token) {
+    // lo: the smallest finite key
+    const float scale = kmax > lo ? static_cast<float>(kBuckets - 1) / (kmax - lo) : 0.f;
+    for (int b = tid; b < kBuckets; b += kSampThreads) {
+      s.cnt[b] = 0;
+      s.wsum[b] = 0;
+    }
+    __syncthreads();
+    for (int64_t i = tid; i < a.V; i += kSampThreads) {
+      const float kv = key_at(i);
+      const int b = bucket0(kv, kmax, scale);
+      atomicAdd(&s.cnt[b], 1u);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&s.wsum[b]), static_cast<unsigned long long>(mass_key(kv)));
+    }
+    __syncthreads();
+    scan2(s.cnt, s.pcnt);
+    scan2(s.wsum, s.pmass);
+    int cached = -1;
+    uint64_t cum, tot;
+    // top-k: bucket bk holds rank k - 1; its first need_k sorted elements stay.
+    int bk = kBuckets - 1, lim_k = -1;
+    uint64_t z = s.pmass[kBuckets - 1] + s.wsum[kBuckets - 1];
+    if (cut_k) {
+      if (tid == 0) s.found_bucket = kBuckets;
+      __syncthreads();
+      for (int b = tid; b < kBuckets; b += kSampThreads)
+        if (s.cnt[b] > 0 && static_cast<int64_t>(s.pcnt[b]) + s.cnt[b] >= k) atomicMin(&s.found_bucket, b);
+      __syncthreads();
+      bk = s.found_bucket;
+      __syncthreads();
+      if (s.pcnt[bk] + s.cnt[bk] <= kPrefixMax) {  // every decision lies in the few top ranks: one gather
+        gather_prefix(bk, scale);
+        token = decide_on_prefix(static_cast<int>(s.pcnt[bk] + s.cnt[bk]), static_cast<int>(k), false, 0, p, u);
+        return token >= 0;
+      }
+      if (s.cnt[bk] > kCap) return false;
+      lim_k = static_cast<int>(k - s.pcnt[bk]);
+      gather_sorted(bk, scale, cached);
+      scan_sorted(lim_k, s.pmass[bk], true, -1.0, cum, tot);
+      z = tot;  // mass of every kept rank
+    }
+    // top-p: the first rank whose running mass exceeds p * Z is the last kept.
+    int last = bk, lim_last = lim_k;
+    uint64_t kept = z;
+    const int bp = first_bucket(bk, z, false, p * static_cast<double>(z));
+    if (!cut_k && bp < kBuckets && s.pcnt[bp] + s.cnt[bp] <= kPrefixMax) {  // few kept ranks: one gather
+      gather_prefix(bp, scale);
+      token = decide_on_prefix(static_cast<int>(s.pcnt[bp] + s.cnt[bp]), -1, true, z, p, u);
+      return token >= 0;
+    }
+    if (bp < kBuckets) {
+      if (s.cnt[bp] > kCap) return false;
+      gather_sorted(bp, scale, cached);
+      const int lim = bp == bk && lim_k >= 0 ? lim_k : static_cast<int>(s.cnt[bp]);
+      const int pos = scan_sorted(lim, s.pmass[bp], false, p * static_cast<double>(z), cum, tot);
+      if (pos < 0) return false;
+      last = bp;
+      lim_last = pos + 1;
+      kept = cum;
+    }
+    // pick: the first kept rank whose running mass reaches u * (kept mass).
+    const double tu = u * static_cast<double>(kept);
+    const int bu = first_bucket(last, kept, true, tu);
+    if (bu == kBuckets || s.cnt[bu] > kCap) return false;
+    gather_sorted(bu, scale, cached);
+    const int lim = bu == last && lim_last >= 0 ? lim_last : static_cast<int>(s.cnt[bu]);
+    const int pos = scan_sorted(lim, s.pmass[bu], true, tu, cum, tot);
+    if (pos < 0) return false;
+    token = static_cast<uint32_t>(s.keys[pos]);
+    __syncthreads();
+    return true;
   }
 
   // The first candidate (keep(i, x)) in rank order whose running weight
@@ -338,14 +576,14 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float temp = a.temp[r * a.temp_s];
-  RowSampler<T> rs{a, s, static_cast<const T*>(a.logits) + r * a.ls0, fmaxf(temp, 1e-5f), 0.f, tid, lane, wave};
+  RowSampler<T> rs{a, s, static_cast<const T*>(a.logits) + r * a.ls0, fmaxf(temp, 1e-5f), 0.f, tid, lane, wave, 0.f, 0.f};
 
   // Row maximum and its first index (rank 0), the finite minimum, and the
   // last index of the minimum (the last rank).
   float mx = -INFINITY, mn = INFINITY, fmn = INFINITY;
   int64_t imx = a.V, imn = -1;
   for (int64_t i = tid; i < a.V; i += kSampThreads) {
-    const float x = rs.x_at(i);
+    const float x = rs.key_at(i);  // x, or for 16-bit logits the logit (same order, same ties)
     if (x > mx || (x == mx && i < imx)) { mx = x; imx = i; }
     if (x < mn || (x == mn && i > imn)) { mn = x; imn = i; }
     if (x != -INFINITY) fmn = fminf(fmn, x);
@@ -375,29 +613,38 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
     if (tid == 0) *out = imx;
     return;
   }
-  rs.xmax = mx;
-  const float lo0 = fminf(fmn, mx);
-
-  // top-k: the element at rank k - 1 bounds the kept set.
+  rs.kmax = mx;
+  rs.kc = RowSampler<T>::kByLogit ? 1.4426950408889634f / rs.t : 1.4426950408889634f;
+  const float klo = fminf(fmn, mx);
+  rs.xmax = rs.key_to_x(mx);  // division never decreases, so these are x's maximum and finite minimum
+  const float lo0 = rs.key_to_x(klo);
   const int64_t k = load_int(a.topk, a.topk_dt, r * a.topk_s);
   const bool cut_k = k > 0 && k < a.V;
+  const double p = a.topp[r * a.topp_s];
+  const double u = a.unif[r * a.unif_s];
+  int64_t token;
+  if (rs.fast(klo, k, cut_k, p, u, token)) {
+    if (tid == 0) *out = token;
+    return;
+  }
+
+  // The per-decision path. top-k: the element at rank k - 1 bounds the kept set.
   float xk = -INFINITY;
   int64_t ik = a.V;
   uint64_t dummy;
   if (cut_k) {
     auto all = [](int64_t, float) { return true; };
-    rs.select(all, false, true, false, 0.0, static_cast<double>(k), lo0, mx, xk, ik, dummy);
+    rs.select(all, false, true, false, 0.0, static_cast<double>(k), lo0, rs.xmax, xk, ik, dummy);
   }
   auto keep_k = [&](int64_t i, float x) { return !cut_k || x > xk || (x == xk && i <= ik); };
 
   // top-p: the first rank whose running mass exceeds top_p * Z is the last
   // kept one (every rank before it has at most top_p before it).
-  const double p = a.topp[r * a.topp_s];
   float xp = -INFINITY;
   int64_t ip = a.V;
   uint64_t kept_mass = 0;
   const float lo1 = cut_k ? fmaxf(lo0, xk) : lo0;
-  const bool cut_p = rs.select(keep_k, true, false, true, p, 0.0, lo1, mx, xp, ip, kept_mass);
+  const bool cut_p = rs.select(keep_k, true, false, true, p, 0.0, lo1, rs.xmax, xp, ip, kept_mass);
   if (!cut_p) {
     uint64_t part = 0;
     for (int64_t i = tid; i < a.V; i += kSampThreads) {
@@ -411,13 +658,12 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   };
 
   // Inverse-CDF pick: the first kept rank whose running mass reaches u * S.
-  const double u = a.unif[r * a.unif_s];
   float xs;
   int64_t is = -1;
   uint64_t cs;
   const float lo2 = cut_p ? fmaxf(lo1, xp) : lo1;
-  const bool ok = rs.select(keep_kp, true, true, false, 0.0, u * static_cast<double>(kept_mass), lo2, mx, xs, is,
-                            cs);
+  const bool ok = rs.select(keep_kp, true, true, false, 0.0, u * static_cast<double>(kept_mass), lo2, rs.xmax, xs,
+                            is, cs);
   if (tid == 0) *out = ok ? is : imn;  // past the end: the reference clamps to the last rank
 }
 
