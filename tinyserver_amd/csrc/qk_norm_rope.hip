@@ -65,6 +65,40 @@ __device__ __forceinline__ void load8(const T* p, int64_t stride, float (&out)[8
 }
 
 // Values are already representable in T, so the conversion here is exact.
+// Unit-stride 8-element row chunk with non-temporal loads / stores: for data
+// read or written once whose lines are not wanted in the caches afterwards.
+template <typename T>
+__device__ __forceinline__ void load8_nt(const T* p, float (&out)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = lo_f<T>(w[i]);
+      out[2 * i + 1] = hi_f<T>(w[i]);
+    }
+  } else {
+    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p) + 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { out[i] = a[i]; out[4 + i] = b[i]; }
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store8_nt(T* p, const float (&v)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack2<T>(v[2 * i], v[2 * i + 1]);
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+  } else {
+    f32x4 a, b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { a[i] = v[i]; b[i] = v[4 + i]; }
+    __builtin_nontemporal_store(a, reinterpret_cast<f32x4*>(p));
+    __builtin_nontemporal_store(b, reinterpret_cast<f32x4*>(p) + 1);
+  }
+}
+
 template <typename T, bool VEC>
 __device__ __forceinline__ void store8(T* p, int64_t stride, const float (&v)[8]) {
   if constexpr (VEC && sizeof(T) == 2) {
@@ -221,7 +255,11 @@ static bool vec_ok(const tsa_view* v) { return v == nullptr || v->data == nullpt
 // takes the token's rows (heads, q first then k) g, g + 16, ..., at most R of
 // them. The token is workgroup-uniform, so its cos/sin are loaded once per
 // lane and its cache slot is found with scalar loads, and the rows of a lane
-// differ only by a head stride.
+// differ only by a head stride. The q/k/v rows are read once and the cache
+// rows are not read back here, so those go non-temporal; the rotated q and k
+// stay ordinary stores (the attention reads them next). One short-lived
+// workgroup per token keeps more loads in flight than resident workgroups
+// walking the tokens with a prefetch (measured 109 vs 157 us at 17794 tokens).
 template <typename T, int R>
 __global__ __launch_bounds__(256) void qk_norm_rope_token(NormRopeArgs<T> a) {
   constexpr int D = 128;
@@ -244,9 +282,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_token(NormRopeArgs<T> a) {
 #pragma unroll
   for (int j = 0; j < R; ++j) {
     const int hh = min(g + 16 * j, H - 1);  // rows past the token's last head redo it (never stored)
-    if (hh < Hq) load8<T, true>(qrow + hh * a.q_sh, 1, x[j]);
-    else load8<T, true>(krow + (hh - Hq) * a.k_sh, 1, x[j]);
-    if (placed && hh >= Hq) load8<T, true>(vrow + (hh - Hq) * a.v_sh, 1, vv[j]);
+    if (hh < Hq) load8_nt<T>(qrow + hh * a.q_sh, x[j]);
+    else load8_nt<T>(krow + (hh - Hq) * a.k_sh, x[j]);
+    if (placed && hh >= Hq) load8_nt<T>(vrow + (hh - Hq) * a.v_sh, vv[j]);
   }
 #pragma unroll
   for (int j = 0; j < R; ++j) {
@@ -262,8 +300,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_token(NormRopeArgs<T> a) {
     const int h = hh - Hq;
     if (a.k_out) store8<T, true>(a.k_out + t * a.ko_st + h * a.ko_sh + d0, 1, o);
     if (placed) {
-      store8<T, true>(a.k_cache + blk * a.kc_b + h * a.kc_h + slot * a.kc_s + d0, 1, o);
-      store8<T, true>(a.v_cache + blk * a.vc_b + h * a.vc_h + slot * a.vc_s + d0, 1, vv[j]);
+      store8_nt<T>(a.k_cache + blk * a.kc_b + h * a.kc_h + slot * a.kc_s + d0, o);
+      store8_nt<T>(a.v_cache + blk * a.vc_b + h * a.vc_h + slot * a.vc_s + d0, vv[j]);
     }
   }
 }
