@@ -205,7 +205,10 @@ constexpr int kFusedWaveBytes = 1024 + RING * kUnitBytes;
 // ones, but a short run pays for them: a wave whose run has fewer than
 // kStreamNtMin tiles uses ordinary loads. Q, reread for every tile of a unit,
 // always uses ordinary loads.
-constexpr int kStreamNtMin = 128;
+#ifndef TSA_DECODE_NT_MIN_TILES
+#define TSA_DECODE_NT_MIN_TILES 128
+#endif
+constexpr int kStreamNtMin = TSA_DECODE_NT_MIN_TILES;
 template <bool NT, typename T>
 __device__ __forceinline__ u32x4 load_stream(const T* p) {
   if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
