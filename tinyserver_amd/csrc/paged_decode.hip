@@ -57,6 +57,7 @@
 #include <type_traits>
 
 #include "tsa_common.h"
+#include "norm_rope_row.h"
 
 namespace tsa {
 
@@ -96,78 +97,40 @@ __device__ __forceinline__ u32x4 pack8(const float (&v)[8]) {
   return w;
 }
 
-// Norm + RoPE of a 128-dim head row held the way the stream kernel holds its
-// Q and K operands: the four lanes g = 0..3 of a column c own the 8-dim
-// chunks g + 4j (j = 0..3). row, w and cs are LDS byte addresses of the row,
-// the weights and the cos row (the sin row follows it). The rounding points
-// and the order of the mean-square sum are the standalone norm/RoPE
-// kernel's (the CPU reduction: chunk accumulators k = chunk % 4 over the
-// 32-element strides in order, then the four accumulators in order, then the
-// 8 elements in order): lane g holds accumulator g, and the RoPE partner
-// (+-64 dims, chunk +-8) is chunk j +- 2 of the same lane. Three passes over
-// LDS keep few values live; z is rounded to T, so it packs exactly. Inlined:
-// as a called function the kernel's ring registers spill across the call.
-struct RowOperand {
-  u32x4 v[4];
-};
-typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+// An LDS byte address (of this wave's fused area) as a 16-byte pointer.
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+__device__ __forceinline__ lds_u32x4* lds16(uint32_t addr) { return (lds_u32x4*)(uintptr_t)addr; }
+
+// In place, norm + RoPE of the 128-dim rows at LDS byte address rows (256 B
+// apart): lane l takes row first + l / 16, 8-dim chunk l % 16 (a DPP row of
+// 16 lanes per head row), with the weights at w and the cos/sin rows at cs
+// (sin follows at cs + 256). The arithmetic is the norm/RoPE kernels' own
+// norm_rope_row, so the rounding is identical to theirs. Rows past last are
+// not written (their lanes redo row last).
 template <typename T>
-__device__ __forceinline__ void lds8f(uint32_t addr, float (&out)[8]) {
-  const u32x4 w = *(lds_u32x4*)(uintptr_t)addr;  // an LDS byte address as a pointer
+__device__ __forceinline__ void norm_rope_rows_lds(uint32_t rows, int first, int last, uint32_t w, uint32_t cs,
+                                                   float eps) {
+  const int lane = threadIdx.x & 63, r = first + (lane >> 4), ch = lane & 15;
+  const int rr = min(r, last);
+  float x[8], wf[8], csf[8], snf[8], o[8];
+  auto get = [](uint32_t addr, float (&out)[8]) {
+    const u32x4 v = *lds16(addr);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    out[2 * i] = lo_f<T>(w[i]);
-    out[2 * i + 1] = hi_f<T>(w[i]);
-  }
-}
-template <typename T>
-__device__ __forceinline__ RowOperand norm_rope_row128(uint32_t row, uint32_t w, uint32_t cs, float eps) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  float acc[8], x[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    lds8f<T>(row + 16 * (g + 4 * j), x);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = j == 0 ? __fmul_rn(x[e], x[e]) : __fadd_rn(acc[e], __fmul_rn(x[e], x[e]));
-  }
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float v = __shfl(acc[e], c, 64);
-    v = __fadd_rn(v, __shfl(acc[e], c + 16, 64));
-    v = __fadd_rn(v, __shfl(acc[e], c + 32, 64));
-    v = __fadd_rn(v, __shfl(acc[e], c + 48, 64));
-    ss = __fadd_rn(ss, v);
-  }
-  const float rinv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, 128.0f), eps)));
-  u32x4 zp[4];  // z = T(w T(x rinv)), packed
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float wf[8], z[8];
-    lds8f<T>(row + 16 * (g + 4 * j), x);
-    lds8f<T>(w + 16 * (g + 4 * j), wf);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) z[e] = __fmul_rn(wf[e], to_float(from_float<T>(__fmul_rn(x[e], rinv))));
-    zp[j] = pack8<T>(z);
-  }
-  RowOperand r;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float csf[8], snf[8], o[8];
-    lds8f<T>(cs + 16 * (g + 4 * j), csf);
-    lds8f<T>(cs + 256 + 16 * (g + 4 * j), snf);
-    const int jp = j < 2 ? j + 2 : j - 2;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t wz = zp[j][e >> 1], wp = zp[jp][e >> 1];
-      const float zv = (e & 1) ? hi_f<T>(wz) : lo_f<T>(wz);
-      const float pv = (e & 1) ? hi_f<T>(wp) : lo_f<T>(wp);
-      const float rot = j < 2 ? -pv : pv;
-      o[e] = __fadd_rn(to_float(from_float<T>(__fmul_rn(zv, csf[e]))), to_float(from_float<T>(__fmul_rn(rot, snf[e]))));
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = lo_f<T>(v[i]);
+      out[2 * i + 1] = hi_f<T>(v[i]);
     }
-    r.v[j] = pack8<T>(o);
-  }
-  return r;
+  };
+  get(rows + 256 * rr + 16 * ch, x);
+  get(w + 16 * ch, wf);
+  get(cs + 16 * ch, csf);
+  get(cs + 256 + 16 * ch, snf);
+  norm_rope_row<T, 128>(x, wf, csf, snf, eps, ch, o);
+  if (r <= last) *lds16(rows + 256 * r + 16 * ch) = pack8<T>(o);
+  // Keep the wave's later LDS reads after these writes (LDS runs a wave's
+  // accesses in order; this stops the compiler from moving them).
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
 }
 
 // Waves per stream-kernel workgroup, and workgroups per CU of the default
@@ -532,16 +495,15 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
                                : static_cast<const T*>(a.vn) + tc.s * a.vn_ss + tc.kvh * a.vn_sh + ch;
     dma64(src, base + 2048);
   };
-  // Norm + RoPE of the row at byte offset row_off of this wave's fused area,
-  // with the weights at w_off and the cos/sin of unit buffer ub.
-  auto norm_row = [&](int row_off, int w_off, int ub, u32x4 (&outp)[KJ]) __attribute__((always_inline)) {
-    const RowOperand r = norm_rope_row128<T>(fbuf_lds + row_off, fbuf_lds + w_off,
-                                             fbuf_lds + 1024 + ub * kUnitBytes + 2048, a.eps);
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) outp[j] = r.v[j];
-  };
+  // The unit's G q rows normalised and rotated in place (four rows per
+  // pass of the wave), then read back in the operand layout: lane (g, c)
+  // takes chunks g + 4j of head c % G.
   auto make_q = [&](int ub) __attribute__((always_inline)) {
-    norm_row(1024 + ub * kUnitBytes + 256 * cq, 0, ub, qn);
+    const uint32_t base = fbuf_lds + 1024 + ub * kUnitBytes;
+    for (int first = 0; first < G; first += 4)
+      norm_rope_rows_lds<T>(base, first, G - 1, fbuf_lds, base + 2048, a.eps);
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) qn[j] = *lds16(base + 256 * cq + 16 * (g + 4 * j));
   };
   // The new token (position L - 1) in the tile starting at tok0.
   auto new_token = [&](const TileCursor& tc, int ub, u32x4 (&ko)[KJ], u32x4 (&vo)[4], u32x4 (&kn)[KJ], u32x4& vnew,
@@ -549,7 +511,10 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
     const int64_t L = clamp_len(a, tc.s);
     cn = static_cast<int>(L - 1 - static_cast<int64_t>(tc.t) * 16);  // 0..15
     const int ubo = 1024 + ub * kUnitBytes;
-    norm_row(ubo + 2048 + 512, 256, ub, kn);
+    const uint32_t ubase = fbuf_lds + ubo;
+    norm_rope_rows_lds<T>(ubase + 2048 + 512, 0, 0, fbuf_lds + 256, ubase + 2048, a.eps);  // the new k row
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) kn[j] = *lds16(ubase + 2048 + 512 + 16 * (g + 4 * j));
     vnew = *reinterpret_cast<const u32x4*>(fbuf + ubo + 2048 + 768 + 16 * c);
 #pragma unroll
     for (int j = 0; j < KJ; ++j)
