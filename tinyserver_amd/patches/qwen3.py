@@ -125,11 +125,11 @@ def device_metadata(ctx: InferenceContext, position_ids: torch.Tensor | None, nu
 # A decode step whose KV spans at most this many 16-token tiles (per kv head
 # summed over the heads) takes the single-launch fused step; larger ones take
 # the norm/store launch followed by paged attention. The fused kernel saves a
-# launch (a few microseconds) but each of its waves normalises its units' rows
-# while its own loads drain, a fixed cost per wave that outweighs the launch
+# launch (a few microseconds), but its extra per-step state costs it scalar
+# registers, and the spill reloads in its tile loop outweigh the saved launch
 # once the waves stream dozens of tiles each. Measured at head_dim 128 on 256
 # CUs: Qwen3-0.6B batch 4 (550 tiles) 27 us fused vs 47 us; Qwen3-8B batch 64
-# (74k tiles) 136 us fused vs 131 us.
+# (74k tiles) 135 us fused vs 130 us.
 FUSED_DECODE_MAX_TILES = 16384
 
 
