@@ -161,7 +161,18 @@ constexpr int RING = TSA_DECODE_RING;
 // rows of its G <= 8 heads (2 KB), then the cos, sin, raw k and raw v rows of
 // the sequence's new token (256 B each at head_dim 128).
 constexpr int kUnitBytes = 3072;
-constexpr int kFusedWaveBytes = 1024 + RING * kUnitBytes;
+// The fused step's per-step values, kept in the wave's LDS area and read at
+// the unit events: held in scalar registers through the tile loop they
+// overflow them, and the spill reloads land in the loop.
+struct FusedState {
+  const void* q; const void* cos; const void* sin; const void* kn; const void* vn;
+  void* kc_out; void* vc_out;
+  int64_t q_ss, q_sh, cs_ss, sn_ss, kn_ss, kn_sh, vn_ss, vn_sh;
+  float eps;
+};
+constexpr int kStateOff = 1024 + RING * kUnitBytes;
+constexpr int kFusedWaveBytes = kStateOff + 128;
+static_assert(sizeof(FusedState) <= 128, "fused state exceeds its LDS slot");
 
 // K/V are read exactly once per call. Non-temporal loads (the streaming
 // hint) reach about 6.8 TB/s on this chip against about 6.0 for ordinary
@@ -298,6 +309,12 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   if constexpr (FUSED) {  // weights: lanes 0-15 q_weight, 16-31 k_weight (32-63 repeat them)
     const T* wsrc = static_cast<const T*>((lane & 16) ? a.kw : a.qw) + 8 * (lane & 15);
     dma64(wsrc, fbuf_lds);
+    if (lane == 0)
+      *reinterpret_cast<FusedState*>(fbuf + kStateOff) =
+          FusedState{a.q, a.cos, a.sin, a.kn, a.vn, a.kc_out, a.vc_out, a.q_ss, a.q_sh,
+                     a.cs_ss, a.sn_ss, a.kn_ss, a.kn_sh, a.vn_ss, a.vn_sh, a.eps};
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
   }
 
   // Locate tile lo: the last sequence with Hkv * pref[s] <= lo (that skips
@@ -482,37 +499,40 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   // stored to the cache after the tile.
   u32x4 qn[KJ];  // the current unit's Q operand (fused)
   auto unit_dma = [&](const TileCursor& tc, int ub) __attribute__((always_inline)) {
+    const FusedState fs = *reinterpret_cast<const FusedState*>(fbuf + kStateOff);
     const uint32_t base = fbuf_lds + 1024 + ub * kUnitBytes;
     for (int i = 0; 4 * i < G; ++i) {  // heads 4i .. 4i+3, 16 lanes each
       const int hh = min(4 * i + (lane >> 4), G - 1);
-      dma64(static_cast<const T*>(a.q) + tc.s * a.q_ss + (tc.kvh * G + hh) * a.q_sh + 8 * (lane & 15),
+      dma64(static_cast<const T*>(fs.q) + tc.s * fs.q_ss + (tc.kvh * G + hh) * fs.q_sh + 8 * (lane & 15),
             base + 1024 * i);
     }
     const int part = lane >> 4, ch = 8 * (lane & 15);
-    const T* src = part == 0   ? static_cast<const T*>(a.cos) + tc.s * a.cs_ss + ch
-                   : part == 1 ? static_cast<const T*>(a.sin) + tc.s * a.sn_ss + ch
-                   : part == 2 ? static_cast<const T*>(a.kn) + tc.s * a.kn_ss + tc.kvh * a.kn_sh + ch
-                               : static_cast<const T*>(a.vn) + tc.s * a.vn_ss + tc.kvh * a.vn_sh + ch;
+    const T* src = part == 0   ? static_cast<const T*>(fs.cos) + tc.s * fs.cs_ss + ch
+                   : part == 1 ? static_cast<const T*>(fs.sin) + tc.s * fs.sn_ss + ch
+                   : part == 2 ? static_cast<const T*>(fs.kn) + tc.s * fs.kn_ss + tc.kvh * fs.kn_sh + ch
+                               : static_cast<const T*>(fs.vn) + tc.s * fs.vn_ss + tc.kvh * fs.vn_sh + ch;
     dma64(src, base + 2048);
   };
   // The unit's G q rows normalised and rotated in place (four rows per
   // pass of the wave), then read back in the operand layout: lane (g, c)
   // takes chunks g + 4j of head c % G.
   auto make_q = [&](int ub) __attribute__((always_inline)) {
+    const FusedState fs = *reinterpret_cast<const FusedState*>(fbuf + kStateOff);
     const uint32_t base = fbuf_lds + 1024 + ub * kUnitBytes;
     for (int first = 0; first < G; first += 4)
-      norm_rope_rows_lds<T>(base, first, G - 1, fbuf_lds, base + 2048, a.eps);
+      norm_rope_rows_lds<T>(base, first, G - 1, fbuf_lds, base + 2048, fs.eps);
 #pragma unroll
     for (int j = 0; j < KJ; ++j) qn[j] = *lds16(base + 256 * cq + 16 * (g + 4 * j));
   };
   // The new token (position L - 1) in the tile starting at tok0.
   auto new_token = [&](const TileCursor& tc, int ub, u32x4 (&ko)[KJ], u32x4 (&vo)[4], u32x4 (&kn)[KJ], u32x4& vnew,
                        int& cn) __attribute__((always_inline)) {
+    const FusedState fs = *reinterpret_cast<const FusedState*>(fbuf + kStateOff);
     const int64_t L = clamp_len(a, tc.s);
     cn = static_cast<int>(L - 1 - static_cast<int64_t>(tc.t) * 16);  // 0..15
     const int ubo = 1024 + ub * kUnitBytes;
     const uint32_t ubase = fbuf_lds + ubo;
-    norm_rope_rows_lds<T>(ubase + 2048 + 512, 0, 0, fbuf_lds + 256, ubase + 2048, a.eps);  // the new k row
+    norm_rope_rows_lds<T>(ubase + 2048 + 512, 0, 0, fbuf_lds + 256, ubase + 2048, fs.eps);  // the new k row
 #pragma unroll
     for (int j = 0; j < KJ; ++j) kn[j] = *lds16(ubase + 2048 + 512 + 16 * (g + 4 * j));
     vnew = *reinterpret_cast<const u32x4*>(fbuf + ubo + 2048 + 768 + 16 * c);
@@ -524,10 +544,11 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
       if (4 * g + r == cn) vo[r] = vnew;
   };
   auto store_new_token = [&](const TileCursor& tc, const u32x4 (&kn)[KJ], const u32x4& vnew, int cn) {
+    const FusedState fs = *reinterpret_cast<const FusedState*>(fbuf + kStateOff);
     int64_t phys, slot;
     if (!page_of(a.bt + tc.s * a.bt_s0, clamp_len(a, tc.s) - 1, phys, slot)) return;  // (as the standalone store)
-    T* kd = static_cast<T*>(a.kc_out) + tc.kvh * a.kc_h + phys * a.kc_b + slot * ks;
-    T* vd = static_cast<T*>(a.vc_out) + tc.kvh * a.vc_h + phys * a.vc_b + slot * vs;
+    T* kd = static_cast<T*>(fs.kc_out) + tc.kvh * a.kc_h + phys * a.kc_b + slot * ks;
+    T* vd = static_cast<T*>(fs.vc_out) + tc.kvh * a.vc_h + phys * a.vc_b + slot * vs;
     if (c == cn) {
 #pragma unroll
       for (int j = 0; j < KJ; ++j) *reinterpret_cast<u32x4*>(kd + 8 * (g + 4 * j)) = kn[j];

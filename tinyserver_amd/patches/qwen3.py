@@ -125,11 +125,12 @@ def device_metadata(ctx: InferenceContext, position_ids: torch.Tensor | None, nu
 # A decode step whose KV spans at most this many 16-token tiles (per kv head
 # summed over the heads) takes the single-launch fused step; larger ones take
 # the norm/store launch followed by paged attention. The fused kernel saves a
-# launch (a few microseconds), but its extra per-step state costs it scalar
-# registers, and the spill reloads in its tile loop outweigh the saved launch
-# once the waves stream dozens of tiles each. Measured at head_dim 128 on 256
-# CUs: Qwen3-0.6B batch 4 (550 tiles) 27 us fused vs 47 us; Qwen3-8B batch 64
-# (74k tiles) 135 us fused vs 130 us.
+# launch (a few microseconds) but pays at every (sequence, kv head) unit it
+# enters (the unit's loads into LDS, its norm, a wait for them), which
+# outweighs the saved launch on large steps. Measured at head_dim 128 on 256
+# CUs: Qwen3-0.6B batch 4 (550 tiles) 29 us fused vs 50 us; Qwen3-8B batch 64
+# (74k tiles) 131 us vs 132 us; a 120-sequence batch (257k tiles) 394 us vs
+# 357 us.
 FUSED_DECODE_MAX_TILES = 16384
 
 
