@@ -265,3 +265,36 @@ def test_fused_decode_step(name):
         ref = op.paged_attention_forward(qr[0].transpose(0, 1).contiguous(), kc, vc, w.block_tables, 16,
                                          w.ctx_lens.to(torch.int32))
         assert_close(out_b, ref, what=f"{name} fused step")
+
+
+@pytest.mark.parametrize("group,block_size", [(8, 32), (1, 16), (4, 64)])
+def test_fused_decode_step_shapes(group, block_size):
+    """The single-launch step on GQA groups 8 (two norm passes per unit) and 1
+    and on 32- and 64-token pages, with a sequence whose only token is the new
+    one: cache and output bit-identical to the two-launch path."""
+    gen = torch.Generator().manual_seed(40 + group)
+    hkv, d = 2, 128
+    hq = group * hkv
+    ctx = [1, 17, 300, 1024, 64]
+    b = len(ctx)
+    q, kc, vc, bt, sl = _random_paged_inputs(ctx, hq, hkv, d, block_size, torch.bfloat16, seed=50 + group)
+    k = torch.randn(b, hkv, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, hkv, d, generator=gen).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(d, generator=gen)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(d, generator=gen)).to(torch.bfloat16)
+    pos = torch.tensor(ctx) - 1
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    emb = torch.cat([pos[:, None].float() * inv, pos[:, None].float() * inv], dim=-1)
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    t = [x.to(DEV) for x in (q, k, v, qw, kw, cos, sin, bt)]
+    slg = sl.to(DEV)
+    kc_a, vc_a = kc.to(DEV), vc.to(DEV)
+    cu = torch.arange(b + 1, dtype=torch.int32, device=DEV)
+    qa, _ = qk_norm_rope_store(t[0], t[1], t[2], t[3], t[4], t[5], t[6], 1e-6, kc_a, vc_a, t[7], cu,
+                               pos.to(DEV, torch.int32), return_k=False)
+    out_a = paged_attention_forward(qa, kc_a, vc_a, t[7], block_size, slg)
+    kc_b, vc_b = kc.to(DEV), vc.to(DEV)
+    out_b = paged_decode_step(t[0], t[1], t[2], t[3], t[4], t[5], t[6], 1e-6, kc_b, vc_b, t[7], slg)
+    torch.cuda.synchronize()
+    assert torch.equal(kc_b, kc_a) and torch.equal(vc_b, vc_a), "cache differs from the two-launch path"
+    assert torch.equal(out_b, out_a), "output differs from the two-launch path"
