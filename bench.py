@@ -295,7 +295,7 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: this build's attention path is benchmarked on a single MI355X "
+        print("bench.py measures one GPU: the attention path is benchmarked on a single MI355X "
               "(sharding is described, not run); use --gpus 1", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():

@@ -1,9 +1,9 @@
 """CPU oracle for the Qwen3 attention hot path of tinyserver.
 
 TEST INFRASTRUCTURE ONLY. This package restates, op for op on the CPU in
-PyTorch, what the reference computes on this path. It is the checker the HIP
-kernels are compared against and the CPU baseline that bench.py times beside
-them. Only ``tests/``, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline
+PyTorch, what the reference computes on this path. It is what the HIP kernels
+are compared against in the tests, and the CPU baseline that bench.py times
+beside them. Only ``tests/``, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline
 leg may import it. The product path (``tinyserver_amd``) never imports it and
 has no CPU fallback: without the HIP library it raises.
 
@@ -18,10 +18,12 @@ paged       Paged decode attention (server/model/kernels/paged_attention.py)
             and the reference's CPU decode branch (patches/qwen3.py:359-385).
 varlen      Varlen causal prefill (server/model/kernels/varlen_attention.py)
             and the reference's CPU prefill branch (patches/qwen3.py:132-171).
+sampling    The batched sampler (server/model/sampling.py:119-194), the
+            reference test's allowed-set rule, and a decision-margin helper.
 
 How each function is pinned (known answers, closed forms, transformers on the
 CPU, the reference tests' own cases) is listed in the tests that check it:
 tests/test_oracle_*.py. No function here is unpinned.
 """
 
-from . import kv_store, norm_rope, paged, varlen  # noqa: F401
+from . import kv_store, norm_rope, paged, sampling, varlen  # noqa: F401
