@@ -159,3 +159,24 @@ def test_rejects_bad_shapes():
         sample_tokens(torch.randn(2, 10, device=DEV), torch.ones(2, device=DEV),
                       torch.zeros(3, dtype=torch.int64, device=DEV), torch.ones(2, device=DEV),
                       torch.ones(2, device=DEV) * 0.5)
+
+
+def test_nonfinite_logits_stay_in_range():
+    """Rows with NaN or infinite logits (whose sampling the reference leaves
+    undefined) complete, and every returned index lies in [0, vocab]: a NaN
+    never becomes a histogram index."""
+    v = 4096
+    g = torch.Generator().manual_seed(16)
+    rows = torch.randn(6, v, generator=g)
+    rows[0, 7] = float("nan")
+    rows[1, ::3] = float("nan")
+    rows[2, 100] = float("inf")
+    rows[3, :] = float("nan")
+    rows[4, 5] = float("-inf")
+    rows[5, 9] = float("inf")
+    rows[5, 10] = float("nan")
+    got = _gpu(rows, [1.0, 0.7, 1.0, 1.0, 1.0, 0.9], [0, 50, 0, 0, 10, 0], [1.0, 0.9, 0.5, 1.0, 0.9, 0.8],
+               [0.3, 0.6, 0.9, 0.1, 0.5, 0.7])
+    assert ((got >= 0) & (got <= v)).all(), got.tolist()
+    # a finite row with one -inf logit is an ordinary row
+    assert got[4].item() == _oracle(rows[4:5], [1.0], [10], [0.9], [0.5]).item()

@@ -172,7 +172,8 @@ struct RowSampler {
   __device__ static int bucket0(float x, float h, float sc) {
     if (x == -INFINITY) return kBuckets - 1;
     const float f = (h - x) * sc;
-    return f >= static_cast<float>(kBuckets - 1) ? kBuckets - 1 : static_cast<int>(f);
+    if (!(f < static_cast<float>(kBuckets - 1))) return kBuckets - 1;  // also NaN: never an index from it
+    return f > 0.f ? static_cast<int>(f) : 0;
   }
 
   // Exclusive prefix over the buckets (two per thread) of in[] into out[].
@@ -396,7 +397,10 @@ struct RowSampler {
     auto bucket_of = [](float x, float h, float sc) -> int {
       if (x == -INFINITY) return kBuckets - 1;
       const float f = (h - x) * sc;
-      return f >= static_cast<float>(kBuckets - 1) ? kBuckets - 1 : static_cast<int>(f);
+      // NaN (a NaN logit, or +inf - +inf) fails the test and takes the last
+      // bucket, so no index is ever formed from it.
+      if (!(f < static_cast<float>(kBuckets - 1))) return kBuckets - 1;
+      return f > 0.f ? static_cast<int>(f) : 0;
     };
     auto in_levels = [&](float x) {
       for (int l = 0; l < levels; ++l)
