@@ -83,7 +83,7 @@ struct SampleLds {
   float found_x;
 };
 
-template <typename T>
+template <typename T, bool UNIT>  // UNIT: the row's elements are adjacent (stride 1)
 struct RowSampler {
   const SampleArgs& a;
   SampleLds& s;
@@ -92,13 +92,39 @@ struct RowSampler {
   float xmax;  // row maximum of x
   int tid, lane, wave;
 
-  __device__ float x_at(int64_t i) const { return __fdiv_rn(to_float(row[i * a.ls1]), t); }
+  __device__ float logit(int64_t i) const { return to_float(UNIT ? row[static_cast<int>(i)] : row[i * a.ls1]); }
+  __device__ float x_at(int64_t i) const { return __fdiv_rn(logit(i), t); }
   // The value the single-histogram path orders by. For 16-bit logits it is
   // the logit itself: distinct 16-bit values differ by at least 2^-8
   // relatively, so dividing them by one t keeps them distinct and in order,
   // and ties in x are exactly ties in the logit. fp32 logits order by x.
   static constexpr bool kByLogit = sizeof(T) == 2;
-  __device__ float key_at(int64_t i) const { return kByLogit ? to_float(row[i * a.ls1]) : x_at(i); }
+  __device__ float key_at(int64_t i) const { return kByLogit ? logit(i) : x_at(i); }
+  // f(i, key_at(i)) for every element of the row, each thread taking its
+  // elements in an order of its own (every use is order-free). A 16-bit row
+  // that is 16-byte aligned with a multiple of 8 elements is read 8 logits
+  // per lane per load, so each load moves 1 KB per wave and several are in
+  // flight; other rows one element at a time.
+  template <typename F>
+  __device__ void each_key(F f) const {
+    if constexpr (UNIT && sizeof(T) == 2) {
+      if ((reinterpret_cast<uintptr_t>(row) & 15) == 0 && (a.V & 7) == 0) {
+        const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
+        const int n8 = static_cast<int>(a.V >> 3);
+#pragma unroll 4
+        for (int ch = tid; ch < n8; ch += kSampThreads) {
+          const u32x4 w = r4[ch];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float l = (e & 1) ? hi_f<T>(w[e >> 1]) : lo_f<T>(w[e >> 1]);
+            f(8 * ch + e, kByLogit ? l : __fdiv_rn(l, t));
+          }
+        }
+        return;
+      }
+    }
+    for (int i = tid; i < static_cast<int>(a.V); i += kSampThreads) f(i, key_at(i));
+  }
   __device__ float key_to_x(float k) const { return kByLogit ? __fdiv_rn(k, t) : k; }
   float kmax;  // row maximum of key_at
   float kc;    // log2(e) / t for 16-bit logits, log2(e) for fp32 (keys are x)
@@ -217,10 +243,9 @@ struct RowSampler {
     if (cached == b) return;
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
-    for (int64_t i = tid; i < a.V; i += kSampThreads) {
-      const float kv = key_at(i);
+    each_key([&](int i, float kv) {
       if (bucket0(kv, kmax, scale) == b) s.keys[atomicAdd(&s.n_gather, 1u)] = rank_key(kv, i);
-    }
+    });
     __syncthreads();
     sort_keys(static_cast<int>(s.cnt[b]));
     cached = b;
@@ -231,10 +256,9 @@ struct RowSampler {
   __device__ void gather_prefix(int nb, float scale) {
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
-    for (int64_t i = tid; i < a.V; i += kSampThreads) {
-      const float kv = key_at(i);
+    each_key([&](int i, float kv) {
       if (bucket0(kv, kmax, scale) <= nb) s.keys[atomicAdd(&s.n_gather, 1u)] = rank_key(kv, i);
-    }
+    });
     __syncthreads();
     sort_keys(static_cast<int>(s.pcnt[nb] + s.cnt[nb]));
   }
@@ -317,12 +341,11 @@ struct RowSampler {
       s.wsum[b] = 0;
     }
     __syncthreads();
-    for (int64_t i = tid; i < a.V; i += kSampThreads) {
-      const float kv = key_at(i);
+    each_key([&](int, float kv) {
       const int b = bucket0(kv, kmax, scale);
       atomicAdd(&s.cnt[b], 1u);
       atomicAdd(reinterpret_cast<unsigned long long*>(&s.wsum[b]), static_cast<unsigned long long>(mass_key(kv)));
-    }
+    });
     __syncthreads();
     scan2(s.cnt, s.pcnt);
     scan2(s.wsum, s.pmass);
@@ -418,7 +441,7 @@ struct RowSampler {
         s.wsum[b] = 0;
       }
       __syncthreads();
-      for (int64_t i = tid; i < a.V; i += kSampThreads) {
+      for (int i = tid; i < static_cast<int>(a.V); i += kSampThreads) {
         const float x = x_at(i);
         if (!keep(i, x) || !in_levels(x)) continue;
         const int b = bucket_of(x, hi, scale);
@@ -451,7 +474,7 @@ struct RowSampler {
         // Gather the bucket, sort it in rank order, prefix-sum its weights.
         if (tid == 0) s.n_gather = 0;
         __syncthreads();
-        for (int64_t i = tid; i < a.V; i += kSampThreads) {
+        for (int i = tid; i < static_cast<int>(a.V); i += kSampThreads) {
           const float x = x_at(i);
           if (!keep(i, x) || !in_levels(x) || bucket_of(x, hi, scale) != fb) continue;
           s.keys[atomicAdd(&s.n_gather, 1u)] = rank_key(x, i);
@@ -499,7 +522,7 @@ struct RowSampler {
       // Too many for LDS: the bucket's value range, then split it again or,
       // if all its elements hold one value, resolve in index order.
       float bmin = INFINITY, bmax = -INFINITY;
-      for (int64_t i = tid; i < a.V; i += kSampThreads) {
+      for (int i = tid; i < static_cast<int>(a.V); i += kSampThreads) {
         const float x = x_at(i);
         if (!keep(i, x) || !in_levels(x) || bucket_of(x, hi, scale) != fb) continue;
         bmin = fminf(bmin, x);
@@ -573,25 +596,24 @@ struct RowSampler {
   }
 };
 
-template <typename T>
+template <typename T, bool UNIT>
 __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   SampleLds& s = *reinterpret_cast<SampleLds*>(lds_raw);
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float temp = a.temp[r * a.temp_s];
-  RowSampler<T> rs{a, s, static_cast<const T*>(a.logits) + r * a.ls0, fmaxf(temp, 1e-5f), 0.f, tid, lane, wave, 0.f, 0.f};
+  RowSampler<T, UNIT> rs{a, s, static_cast<const T*>(a.logits) + r * a.ls0, fmaxf(temp, 1e-5f), 0.f, tid, lane, wave, 0.f, 0.f};
 
   // Row maximum and its first index (rank 0), the finite minimum, and the
   // last index of the minimum (the last rank).
   float mx = -INFINITY, mn = INFINITY, fmn = INFINITY;
   int64_t imx = a.V, imn = -1;
-  for (int64_t i = tid; i < a.V; i += kSampThreads) {
-    const float x = rs.key_at(i);  // x, or for 16-bit logits the logit (same order, same ties)
+  rs.each_key([&](int i, float x) {  // x, or for 16-bit logits the logit (same order, same ties)
     if (x > mx || (x == mx && i < imx)) { mx = x; imx = i; }
     if (x < mn || (x == mn && i > imn)) { mn = x; imn = i; }
     if (x != -INFINITY) fmn = fminf(fmn, x);
-  }
+  });
   for (int o = 32; o > 0; o >>= 1) {
     const float omx = __shfl_xor(mx, o, 64), omn = __shfl_xor(mn, o, 64), ofm = __shfl_xor(fmn, o, 64);
     const int64_t oimx = __shfl_xor(imx, o, 64), oimn = __shfl_xor(imn, o, 64);
@@ -618,7 +640,7 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
     return;
   }
   rs.kmax = mx;
-  rs.kc = RowSampler<T>::kByLogit ? 1.4426950408889634f / rs.t : 1.4426950408889634f;
+  rs.kc = RowSampler<T, UNIT>::kByLogit ? 1.4426950408889634f / rs.t : 1.4426950408889634f;
   const float klo = fminf(fmn, mx);
   rs.xmax = rs.key_to_x(mx);  // division never decreases, so these are x's maximum and finite minimum
   const float lo0 = rs.key_to_x(klo);
@@ -651,7 +673,7 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   const bool cut_p = rs.select(keep_k, true, false, true, p, 0.0, lo1, rs.xmax, xp, ip, kept_mass);
   if (!cut_p) {
     uint64_t part = 0;
-    for (int64_t i = tid; i < a.V; i += kSampThreads) {
+    for (int i = tid; i < static_cast<int>(a.V); i += kSampThreads) {
       const float x = rs.x_at(i);
       if (keep_k(i, x)) part += rs.mass(x);
     }
@@ -703,9 +725,18 @@ extern "C" int tsa_sample_tokens(const tsa_view* out, const tsa_view* logits, co
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t lds = sizeof(SampleLds);
   switch (logits->dtype) {
-    case TSA_BF16: sample_tokens_kernel<bf16_t><<<dim3(B), dim3(kSampThreads), lds, st>>>(a); break;
-    case TSA_F16: sample_tokens_kernel<f16_t><<<dim3(B), dim3(kSampThreads), lds, st>>>(a); break;
-    default: sample_tokens_kernel<float><<<dim3(B), dim3(kSampThreads), lds, st>>>(a); break;
+    case TSA_BF16:
+      if (a.ls1 == 1) sample_tokens_kernel<bf16_t, true><<<dim3(B), dim3(kSampThreads), lds, st>>>(a);
+      else sample_tokens_kernel<bf16_t, false><<<dim3(B), dim3(kSampThreads), lds, st>>>(a);
+      break;
+    case TSA_F16:
+      if (a.ls1 == 1) sample_tokens_kernel<f16_t, true><<<dim3(B), dim3(kSampThreads), lds, st>>>(a);
+      else sample_tokens_kernel<f16_t, false><<<dim3(B), dim3(kSampThreads), lds, st>>>(a);
+      break;
+    default:
+      if (a.ls1 == 1) sample_tokens_kernel<float, true><<<dim3(B), dim3(kSampThreads), lds, st>>>(a);
+      else sample_tokens_kernel<float, false><<<dim3(B), dim3(kSampThreads), lds, st>>>(a);
+      break;
   }
   return check_launch("tsa_sample_tokens");
 }
