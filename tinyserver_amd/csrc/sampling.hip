@@ -67,6 +67,12 @@ __device__ __forceinline__ uint64_t rank_key(float x, int64_t i) {
   return (static_cast<uint64_t>(~u) << 32) | static_cast<uint32_t>(i);
 }
 
+// The value a rank key was made from (-0 comes back as +0).
+__device__ __forceinline__ float key_of_rank(uint64_t rk) {
+  const uint32_t o = ~static_cast<uint32_t>(rk >> 32);
+  return __builtin_bit_cast(float, (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+
 struct SampleLds {
   uint32_t cnt[kBuckets];
   uint64_t wsum[kBuckets];  // weight per bucket, then its exclusive prefix
@@ -295,7 +301,7 @@ struct RowSampler {
     const int per = (limit + kSampThreads - 1) / kSampThreads;
     const int e0 = min(limit, tid * per), e1 = min(limit, e0 + per);
     uint64_t mine = 0;
-    for (int e = e0; e < e1; ++e) mine += mass_key(key_at(static_cast<uint32_t>(s.keys[e])));
+    for (int e = e0; e < e1; ++e) mine += mass_key(key_of_rank(s.keys[e]));  // no reload of the row
     uint64_t incl = mine;
     for (int o = 1; o < 64; o <<= 1) {
       const uint64_t up = __shfl_up(incl, o, 64);
@@ -311,7 +317,7 @@ struct RowSampler {
     for (int w = 0; w < kSampWaves; ++w) all += s.wave_u64[w];
     for (int e = e0; e < e1; ++e) {
       const uint64_t excl = cum;
-      cum += mass_key(key_at(static_cast<uint32_t>(s.keys[e])));
+      cum += mass_key(key_of_rank(s.keys[e]));
       const bool r = ge ? static_cast<double>(cum) >= target : static_cast<double>(cum) > target;
       const bool rx = ge ? static_cast<double>(excl) >= target : static_cast<double>(excl) > target;
       if (r && (e == 0 || !rx)) {
