@@ -117,7 +117,7 @@ struct RowSampler {
       if ((reinterpret_cast<uintptr_t>(row) & 15) == 0 && (a.V & 7) == 0) {
         const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
         const int n8 = static_cast<int>(a.V >> 3);
-#pragma unroll 4
+#pragma unroll 8
         for (int ch = tid; ch < n8; ch += kSampThreads) {
           const u32x4 w = r4[ch];
 #pragma unroll
