@@ -111,10 +111,13 @@ struct RowSampler {
   // that is 16-byte aligned with a multiple of 8 elements is read 8 logits
   // per lane per load, so each load moves 1 KB per wave and several are in
   // flight; other rows one element at a time.
+  __device__ bool chunked() const {
+    return UNIT && sizeof(T) == 2 && (reinterpret_cast<uintptr_t>(row) & 15) == 0 && (a.V & 7) == 0;
+  }
   template <typename F>
   __device__ void each_key(F f) const {
     if constexpr (UNIT && sizeof(T) == 2) {
-      if ((reinterpret_cast<uintptr_t>(row) & 15) == 0 && (a.V & 7) == 0) {
+      if (chunked()) {
         const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
         const int n8 = static_cast<int>(a.V >> 3);
 #pragma unroll 8
@@ -613,22 +616,71 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
 
   // Row maximum and its first index (rank 0), the finite minimum, and the
   // last index of the minimum (the last rank).
+  // A thread visits its elements in increasing index order, so a strict >
+  // keeps the first index of its maximum and <= the last of its minimum.
   float mx = -INFINITY, mn = INFINITY, fmn = INFINITY;
-  int64_t imx = a.V, imn = -1;
-  rs.each_key([&](int i, float x) {  // x, or for 16-bit logits the logit (same order, same ties)
-    if (x > mx || (x == mx && i < imx)) { mx = x; imx = i; }
-    if (x < mn || (x == mn && i > imn)) { mn = x; imn = i; }
-    if (x != -INFINITY) fmn = fminf(fmn, x);
-  });
+  int imx = static_cast<int>(a.V), imn = -1;
+  if constexpr (UNIT && sizeof(T) == 2) {
+    if (rs.chunked()) {  // per 8-logit chunk: its max and min first, indices only when they win
+      const u32x4* r4 = reinterpret_cast<const u32x4*>(rs.row);
+      const int n8 = static_cast<int>(a.V >> 3);
+#pragma unroll 8
+      for (int ch = tid; ch < n8; ch += kSampThreads) {
+        const u32x4 w = r4[ch];
+        float l[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          l[2 * e] = lo_f<T>(w[e]);
+          l[2 * e + 1] = hi_f<T>(w[e]);
+        }
+        float cmax = l[0], cmin = l[0], cfin = l[0] != -INFINITY ? l[0] : INFINITY;
+#pragma unroll
+        for (int e = 1; e < 8; ++e) {
+          cmax = fmaxf(cmax, l[e]);
+          cmin = fminf(cmin, l[e]);
+          cfin = fminf(cfin, l[e] != -INFINITY ? l[e] : INFINITY);
+        }
+        fmn = fminf(fmn, cfin);
+        if (cmax > mx) {  // (a NaN chunk maximum never passes)
+          int first = 0;
+#pragma unroll
+          for (int e = 7; e >= 0; --e)
+            if (l[e] == cmax) first = e;
+          mx = cmax;
+          imx = 8 * ch + first;
+        }
+        if (cmin <= mn) {
+          int last = 7;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (l[e] == cmin) last = e;
+          mn = cmin;
+          imn = 8 * ch + last;
+        }
+      }
+    } else {
+      rs.each_key([&](int i, float x) {
+        if (x > mx) { mx = x; imx = i; }
+        if (x <= mn) { mn = x; imn = i; }
+        if (x != -INFINITY) fmn = fminf(fmn, x);
+      });
+    }
+  } else {
+    rs.each_key([&](int i, float x) {  // x, or for 16-bit logits the logit (same order, same ties)
+      if (x > mx) { mx = x; imx = i; }
+      if (x <= mn) { mn = x; imn = i; }
+      if (x != -INFINITY) fmn = fminf(fmn, x);
+    });
+  }
   for (int o = 32; o > 0; o >>= 1) {
     const float omx = __shfl_xor(mx, o, 64), omn = __shfl_xor(mn, o, 64), ofm = __shfl_xor(fmn, o, 64);
-    const int64_t oimx = __shfl_xor(imx, o, 64), oimn = __shfl_xor(imn, o, 64);
+    const int oimx = __shfl_xor(imx, o, 64), oimn = __shfl_xor(imn, o, 64);
     if (omx > mx || (omx == mx && oimx < imx)) { mx = omx; imx = oimx; }
     if (omn < mn || (omn == mn && oimn > imn)) { mn = omn; imn = oimn; }
     fmn = fminf(fmn, ofm);
   }
   __shared__ float red_mx[kSampWaves], red_mn[kSampWaves], red_fm[kSampWaves];
-  __shared__ int64_t red_imx[kSampWaves], red_imn[kSampWaves];
+  __shared__ int red_imx[kSampWaves], red_imn[kSampWaves];
   if (lane == 0) {
     red_mx[wave] = mx; red_imx[wave] = imx;
     red_mn[wave] = mn; red_imn[wave] = imn;
