@@ -114,6 +114,55 @@ struct RowSampler {
   __device__ bool chunked() const {
     return UNIT && sizeof(T) == 2 && (reinterpret_cast<uintptr_t>(row) & 15) == 0 && (a.V & 7) == 0;
   }
+  // f(i, key) for the elements whose key may lie in [lo, hi]: in a chunked
+  // row an 8-logit chunk entirely outside the range is skipped after one
+  // comparison (the callers' ranges carry a margin, and f still tests each
+  // element exactly); otherwise every element.
+  template <typename F>
+  __device__ void each_key_in(float lo, float hi, F f) const {
+    if constexpr (UNIT && sizeof(T) == 2) {
+      if (chunked()) {
+        const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
+        const int n8 = static_cast<int>(a.V >> 3);
+#pragma unroll 8
+        for (int ch = tid; ch < n8; ch += kSampThreads) {
+          const u32x4 w = r4[ch];
+          float l[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            l[2 * e] = lo_f<T>(w[e]);
+            l[2 * e + 1] = hi_f<T>(w[e]);
+          }
+          float cmax = l[0], cmin = l[0];
+#pragma unroll
+          for (int e = 1; e < 8; ++e) {
+            cmax = fmaxf(cmax, l[e]);
+            cmin = fminf(cmin, l[e]);
+          }
+          if (cmax < lo || cmin > hi) continue;  // (kByLogit: keys are the logits)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f(8 * ch + e, l[e]);
+        }
+        return;
+      }
+    }
+    each_key(f);
+  }
+  // The key range that holds buckets [b0, b1] of the shared histogram, with
+  // a bucket's width of margin on each side; unbounded where that cannot be
+  // said (no spread, or the last bucket, which also takes -inf and NaN).
+  __device__ void bucket_range(int b0, int b1, float scale, float& lo, float& hi) const {
+    lo = -INFINITY;
+    hi = INFINITY;
+    if (!(scale > 0.f) || b1 >= kBuckets - 1) return;
+    lo = kmax - static_cast<float>(b1 + 2) / scale;
+    lo -= fabsf(lo) * 1e-6f;  // and at least 16 ulps, for rows of tiny spread
+    if (b0 > 0) {
+      hi = kmax - static_cast<float>(b0 - 1) / scale;
+      hi += fabsf(hi) * 1e-6f;
+    }
+  }
+
   template <typename F>
   __device__ void each_key(F f) const {
     if constexpr (UNIT && sizeof(T) == 2) {
@@ -248,28 +297,41 @@ struct RowSampler {
   }
 
   // Gathers bucket b of the shared histogram into s.keys in rank order.
-  __device__ void gather_sorted(int b, float scale, int& cached) {
-    if (cached == b) return;
+  __device__ bool gather_sorted(int b, float scale, int& cached) {
+    if (cached == b) return true;
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
+    // (a single bucket is a narrow range most chunks straddle: no skipping)
     each_key([&](int i, float kv) {
-      if (bucket0(kv, kmax, scale) == b) s.keys[atomicAdd(&s.n_gather, 1u)] = rank_key(kv, i);
+      if (bucket0(kv, kmax, scale) == b) {
+        const uint32_t at = atomicAdd(&s.n_gather, 1u);
+        if (at < kCap) s.keys[at] = rank_key(kv, i);
+      }
     });
     __syncthreads();
+    if (s.n_gather != s.cnt[b]) return false;  // (the histogram's own count: never expected to differ)
     sort_keys(static_cast<int>(s.cnt[b]));
     cached = b;
+    return true;
   }
 
   // Gathers every bucket up to nb (the top ranks of the row) into s.keys in
   // rank order: position e of the sorted list is rank e of the row.
-  __device__ void gather_prefix(int nb, float scale) {
+  __device__ bool gather_prefix(int nb, float scale) {
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
-    each_key([&](int i, float kv) {
-      if (bucket0(kv, kmax, scale) <= nb) s.keys[atomicAdd(&s.n_gather, 1u)] = rank_key(kv, i);
+    float lo, hi;
+    bucket_range(0, nb, scale, lo, hi);
+    each_key_in(lo, hi, [&](int i, float kv) {
+      if (bucket0(kv, kmax, scale) <= nb) {
+        const uint32_t at = atomicAdd(&s.n_gather, 1u);
+        if (at < kCap) s.keys[at] = rank_key(kv, i);
+      }
     });
     __syncthreads();
+    if (s.n_gather != s.pcnt[nb] + s.cnt[nb]) return false;  // (never expected)
     sort_keys(static_cast<int>(s.pcnt[nb] + s.cnt[nb]));
+    return true;
   }
 
   // The decisions on the sorted top ranks [0, n): top-k keeps the first
@@ -372,13 +434,13 @@ struct RowSampler {
       bk = s.found_bucket;
       __syncthreads();
       if (s.pcnt[bk] + s.cnt[bk] <= kPrefixMax) {  // every decision lies in the few top ranks: one gather
-        gather_prefix(bk, scale);
+        if (!gather_prefix(bk, scale)) return false;
         token = decide_on_prefix(static_cast<int>(s.pcnt[bk] + s.cnt[bk]), static_cast<int>(k), false, 0, p, u);
         return token >= 0;
       }
       if (s.cnt[bk] > kCap) return false;
       lim_k = static_cast<int>(k - s.pcnt[bk]);
-      gather_sorted(bk, scale, cached);
+      if (!gather_sorted(bk, scale, cached)) return false;
       scan_sorted(lim_k, s.pmass[bk], true, -1.0, cum, tot);
       z = tot;  // mass of every kept rank
     }
@@ -387,13 +449,13 @@ struct RowSampler {
     uint64_t kept = z;
     const int bp = first_bucket(bk, z, false, p * static_cast<double>(z));
     if (!cut_k && bp < kBuckets && s.pcnt[bp] + s.cnt[bp] <= kPrefixMax) {  // few kept ranks: one gather
-      gather_prefix(bp, scale);
+      if (!gather_prefix(bp, scale)) return false;
       token = decide_on_prefix(static_cast<int>(s.pcnt[bp] + s.cnt[bp]), -1, true, z, p, u);
       return token >= 0;
     }
     if (bp < kBuckets) {
       if (s.cnt[bp] > kCap) return false;
-      gather_sorted(bp, scale, cached);
+      if (!gather_sorted(bp, scale, cached)) return false;
       const int lim = bp == bk && lim_k >= 0 ? lim_k : static_cast<int>(s.cnt[bp]);
       const int pos = scan_sorted(lim, s.pmass[bp], false, p * static_cast<double>(z), cum, tot);
       if (pos < 0) return false;
@@ -405,7 +467,7 @@ struct RowSampler {
     const double tu = u * static_cast<double>(kept);
     const int bu = first_bucket(last, kept, true, tu);
     if (bu == kBuckets || s.cnt[bu] > kCap) return false;
-    gather_sorted(bu, scale, cached);
+    if (!gather_sorted(bu, scale, cached)) return false;
     const int lim = bu == last && lim_last >= 0 ? lim_last : static_cast<int>(s.cnt[bu]);
     const int pos = scan_sorted(lim, s.pmass[bu], true, tu, cum, tot);
     if (pos < 0) return false;
@@ -486,7 +548,8 @@ struct RowSampler {
         for (int i = tid; i < static_cast<int>(a.V); i += kSampThreads) {
           const float x = x_at(i);
           if (!keep(i, x) || !in_levels(x) || bucket_of(x, hi, scale) != fb) continue;
-          s.keys[atomicAdd(&s.n_gather, 1u)] = rank_key(x, i);
+          const uint32_t at = atomicAdd(&s.n_gather, 1u);
+          if (at < kCap) s.keys[at] = rank_key(x, i);
         }
         __syncthreads();
         sort_keys(static_cast<int>(n));
