@@ -15,7 +15,9 @@ Also measured (in "secondary"): the whole decode block (fused QK
 norm+RoPE+store, then attention), the varlen prefill at the Qwen3-8B
 16-sequence shape (TFLOP/s against 2.5 PFLOP/s bf16 dense), the fused QK
 norm+RoPE+store at that shape (GB/s), the Qwen3-32B bs32 32k-context decode,
-and the Qwen3-4B mixed batch (prefill+store then decode). The CPU baseline
+the Qwen3-4B mixed batch (prefill+store then decode), the decode block as
+one fused launch, and batched sampling over 64 rows of the Qwen3 vocabulary
+(three filter settings). The CPU baseline
 runs the reference's CPU decode path (per-token gather loop +
 repeat_interleave + SDPA, restated in the oracle) on a bounded sample of the
 same batch on this host's cores.
