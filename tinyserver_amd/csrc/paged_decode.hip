@@ -294,9 +294,7 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   char* const fbuf = reinterpret_cast<char*>(lds_i) + fused_off;
   const uint32_t fbuf_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)fbuf));  // address-space cast
   auto dma64 = [&](const void* src, uint32_t lds_byte) __attribute__((always_inline)) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
-                 "s"(__builtin_amdgcn_readfirstlane(lds_byte))
-                 : "memory", "m0");
+    dma16(src, __builtin_amdgcn_readfirstlane(lds_byte));
   };
 
   const int64_t total = static_cast<int64_t>(Hkv) * pref[a.B];

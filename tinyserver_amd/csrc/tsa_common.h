@@ -194,4 +194,38 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// ------------------------------------------------- global->LDS DMA loads --
+// global_load_lds_dwordx4: lane l's 16 bytes land at LDS byte address
+// M0 + 16 l, with no register staging. The LDS address is an operand bound
+// to M0 ("{m0}"), so the compiler sets M0 itself and knows the asm reads it;
+// the s_nop is the one wait state the DMA needs after an M0 write.
+//
+// They are written as assembly, not __builtin_amdgcn_global_load_lds, on
+// purpose. With the builtin, the compiler counts the loads as pending LDS
+// writes: every workgroup-scope release fence (lds_barrier) then becomes
+// s_waitcnt vmcnt(0), and it drains them before the first
+// ds_read_b64_tr_b16 of a block -- both empty the prefetch pipeline that
+// the staging exists for -- while it places no wait at all before an
+// ordinary ds_read of the staged data. So the kernels wait for these loads
+// themselves (wait_vmcnt), counting them in issue order; the compiler's own
+// vmcnt waits, which do not count them, are then only ever stricter than
+// needed, never too weak.
+//
+// dma16: a per-lane 64-bit address. dma16_sv: a wave-uniform base plus a
+// 32-bit lane offset (half the address registers).
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+
+// Wait until at most N of this wave's vector memory operations are in
+// flight (they complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is a 6-bit field");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 }  // namespace tsa

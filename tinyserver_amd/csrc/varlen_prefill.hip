@@ -22,9 +22,6 @@
 
 #include "tsa_common.h"
 
-// The K/V loads set M0 in inline assembly and list it as clobbered.
-#pragma clang diagnostic ignored "-Winline-asm"
-
 namespace tsa {
 
 struct PrefillArgs {
@@ -368,20 +365,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   uint32_t doff[IPW];  // lane byte offsets from the first row of load i (< 2^32: strides checked on the host)
 #pragma unroll
   for (int i = 0; i < IPW; ++i) doff[i] = static_cast<uint32_t>(lrow * st_b) + 16u * lane_chunk(i);
-  // The loads are written as assembly: the form with a uniform 64-bit base
-  // and a 32-bit lane offset reads half the address registers of the
-  // 64-bit-address form, and M0 (the LDS address) is set right before each,
-  // with the one wait state an LDS DMA needs after an M0 write. Nothing else
-  // in this file uses M0.
+  // A full block's loads take a wave-uniform base plus a 32-bit lane offset
+  // (dma16_sv), which reads half the address registers of the 64-bit
+  // per-lane form.
   const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)smem));  // address-space cast
   auto dma = [&](const char* sbase, uint32_t voff, int lds_byte) __attribute__((always_inline)) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
-                 "s"(smem_lds + lds_byte)
-                 : "memory", "m0");
+    dma16_sv(sbase, voff, smem_lds + lds_byte);
   };
   auto dma64 = [&](const char* src, int lds_byte) __attribute__((always_inline)) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(smem_lds + lds_byte)
-                 : "memory", "m0");
+    dma16(src, smem_lds + lds_byte);
   };
   // This wave's loads of block blk of item `it` (K if k_wave) into slot `slot`.
   auto load_block = [&](const Item& it, int blk, int slot) __attribute__((always_inline)) {
@@ -416,12 +408,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   };
   // Wait until at most n of this wave's loads are in flight (they complete
   // in issue order; other memory operations issued among them only make the
-  // wait stricter). Written as assembly: the compiler cannot see the loads,
-  // so it could drop a wait of its own making as redundant.
-  auto wait_loads = [&](auto n) {
-    constexpr int N = decltype(n)::value;
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-  };
+  // wait stricter). The compiler does not count the DMA loads, so the
+  // kernel places these waits itself.
+  auto wait_loads = [&](auto n) { wait_vmcnt<decltype(n)::value>(); };
   constexpr int kInFlight = (A - 1) * IPW;  // loads of the later steps, still in flight at a block's end
 
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
