@@ -161,22 +161,52 @@ def test_rejects_bad_shapes():
                       torch.ones(2, device=DEV) * 0.5)
 
 
-def test_nonfinite_logits_stay_in_range():
-    """Rows with NaN or infinite logits (whose sampling the reference leaves
-    undefined) complete, and every returned index lies in [0, vocab]: a NaN
-    never becomes a histogram index."""
-    v = 4096
+DEGENERATE = (0, 1, 2, 3, 5, 6, 7)  # rows of _nonfinite_rows whose softmax is NaN
+
+
+def _nonfinite_rows(v, dtype):
     g = torch.Generator().manual_seed(16)
-    rows = torch.randn(6, v, generator=g)
-    rows[0, 7] = float("nan")
-    rows[1, ::3] = float("nan")
-    rows[2, 100] = float("inf")
-    rows[3, :] = float("nan")
-    rows[4, 5] = float("-inf")
-    rows[5, 9] = float("inf")
+    rows = torch.randn(10, v, generator=g) * 2.5
+    rows[0, 7] = float("nan")              # one NaN among finite logits
+    rows[1, ::3] = float("nan")            # many NaNs
+    rows[2, 100] = float("inf")            # a +inf maximum
+    rows[3, :] = float("nan")              # every logit NaN
+    rows[4, 5] = float("-inf")             # one -inf: an ordinary row
+    rows[5, 9] = float("inf")              # +inf and NaN
     rows[5, 10] = float("nan")
-    got = _gpu(rows, [1.0, 0.7, 1.0, 1.0, 1.0, 0.9], [0, 50, 0, 0, 10, 0], [1.0, 0.9, 0.5, 1.0, 0.9, 0.8],
-               [0.3, 0.6, 0.9, 0.1, 0.5, 0.7])
-    assert ((got >= 0) & (got <= v)).all(), got.tolist()
-    # a finite row with one -inf logit is an ordinary row
-    assert got[4].item() == _oracle(rows[4:5], [1.0], [10], [0.9], [0.5]).item()
+    rows[6, :] = float("-inf")             # every logit -inf
+    rows[7, 50] = float("inf")             # two +inf, ties in index order
+    rows[7, 20] = float("inf")
+    rows[8, : v // 2] = float("-inf")      # half masked, finite rest: ordinary
+    rows[9, :] = float("-inf")             # one finite logit among -inf
+    rows[9, v - 3] = 1.0
+    return rows.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_nonfinite_rows_match_reference(dtype):
+    """Rows with NaN, +inf or only -inf logits at the Qwen3 vocabulary size.
+    The reference's formulation fixes the answer: a greedy row takes rank 0
+    of the stable descending sort (NaN first, so the first NaN; else the
+    first maximum; index 0 when every logit is -inf); any other row whose
+    softmax is NaN gets searchsorted's past-the-end rank clamped to the last
+    rank (the last index of the minimum, vocab-1 when all are NaN). Every
+    index lies in [0, vocab) and equals the oracle's, for greedy and sampled
+    rows, with and without top-k/top-p."""
+    v = 151936
+    rows = _nonfinite_rows(v, dtype)
+    n = rows.shape[0]
+    for temp, k, p, u in ((0.0, 0, 1.0, 0.5), (1.0, 0, 1.0, 0.3), (0.7, 50, 0.9, 0.6), (1.0, 0, 0.5, 0.9),
+                          (0.9, 10, 0.8, 0.0)):
+        args = ([temp] * n, [k] * n, [p] * n, [u] * n)
+        got, _ = _compare(rows, *args, dtype=dtype, what=f"non-finite T={temp} k={k} p={p} u={u}")
+        ref = _oracle(rows, *args, dtype=dtype)
+        assert ((got >= 0) & (got < v)).all(), (temp, k, p, u, got.tolist())
+        for i in DEGENERATE:  # fixed by the NaN/inf rules, not by rounding
+            assert got[i].item() == ref[i].item(), (i, temp, k, p, u, got.tolist(), ref.tolist())
+    # the hand-derived answers, for the greedy and one sampled setting
+    greedy = _gpu(rows, [0.0] * n, [0] * n, [1.0] * n, [0.5] * n, dtype=dtype).tolist()
+    assert greedy[0] == 7 and greedy[1] == 0 and greedy[2] == 100 and greedy[3] == 0
+    assert greedy[5] == 10 and greedy[6] == 0 and greedy[7] == 20 and greedy[9] == v - 3
+    sampled = _gpu(rows, [1.0] * n, [0] * n, [1.0] * n, [0.3] * n, dtype=dtype).tolist()
+    assert sampled[3] == v - 1 and sampled[6] == v - 1

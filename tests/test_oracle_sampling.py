@@ -136,3 +136,28 @@ def test_rejects_bad_shapes():
     with pytest.raises(ValueError, match="Expected top_k shape"):
         osm.sample_tokens(torch.randn(2, 10), torch.ones(2), torch.zeros(3, dtype=torch.int64), torch.ones(2),
                           torch.ones(2) * 0.5)
+
+
+def test_nonfinite_rows_follow_sort_and_searchsorted_rules():
+    """What the reference's formulation gives rows whose softmax is NaN,
+    derived by hand from torch's semantics: the stable descending sort puts
+    NaN first (ties by index); a greedy row takes rank 0; otherwise softmax
+    and cumsum are NaN, searchsorted's lower bound of a NaN target runs past
+    the end (its test, not (cdf >= target), is true for NaN), and the clamp
+    to vocab-1 picks the last rank: the last index of the minimum."""
+    v = 12
+    nan, inf = float("nan"), float("inf")
+    rows = torch.tensor([
+        [0.5, 1.0, nan, 2.0, -1.0, 0.0, -1.0, 3.0, nan, 0.1, 0.2, 0.3],  # NaN at 2 and 8; min -1 last at 6
+        [nan] * v,
+        [-inf] * v,
+        [0.0, inf, 1.0, inf, -2.0, -2.0, 5.0, 0.0, 0.0, 0.0, 0.0, 0.0],   # +inf at 1 and 3; min -2 last at 5
+    ])
+    n = rows.shape[0]
+    for k, p, u in ((0, 1.0, 0.5), (3, 0.9, 0.1), (0, 0.2, 0.99)):
+        greedy = osm.sample_tokens(rows, torch.zeros(n), torch.full((n,), k), torch.full((n,), p),
+                                   torch.full((n,), u)).tolist()
+        assert greedy == [2, 0, 0, 1]
+        sampled = osm.sample_tokens(rows, torch.ones(n), torch.full((n,), k), torch.full((n,), p),
+                                    torch.full((n,), u)).tolist()
+        assert sampled == [6, v - 1, v - 1, 5]

@@ -7,14 +7,25 @@
 * the reference's ValueErrors (:182-187, :329-330);
 * one build per forward: layers that get the same position_ids reuse it, a
   new step's tensor rebuilds it;
+* the glue takes the reference engine's own context: a plain
+  ``InferenceContext{mode, sequences}`` dataclass
+  (server/model/inference_context.py:18-21, decode entries holding only
+  "block_table" as engine.py:579-582 builds them), read through the engine
+  module's getter when that module imports;
 * the patched forward has no CPU path.
 """
+
+import sys
+import types
+from dataclasses import dataclass, field
+from typing import Any
 
 import pytest
 import torch
 
 from tinyserver_amd.inference_context import InferenceContext, get_inference_context, inference_context
 from tinyserver_amd.patches import device_metadata
+from tinyserver_amd.patches import qwen3 as patch_mod
 
 CPU = torch.device("cpu")
 
@@ -80,4 +91,81 @@ def test_patched_forward_has_no_cpu_path():
     _, patched = tiny_models(torch.float32, "cpu", 4, 8)
     ctx = InferenceContext("prefill", [{"num_tokens": 3, "block_table": [0]}])
     with torch.no_grad(), inference_context(ctx), pytest.raises(RuntimeError, match="GPU"):
+        patched(input_ids=torch.tensor([[1, 2, 3]]), position_ids=torch.tensor([[0, 1, 2]]), use_cache=False)
+
+
+@dataclass
+class EngineContext:
+    """The reference engine's context, field for field: nothing else on it."""
+
+    mode: str = "prefill"
+    sequences: list[dict[str, Any]] = field(default_factory=list)
+
+
+def test_reference_shaped_context():
+    assert set(EngineContext.__dataclass_fields__) == {"mode", "sequences"}
+    ctx = EngineContext("decode", [{"block_table": [3]}, {"block_table": [5, 6]}])  # engine.py:579-582
+    pos = torch.tensor([[15, 16]])
+    m = device_metadata(ctx, pos, 2, CPU)
+    assert m.block_tables.tolist() == [[3, 0], [5, 6]] and m.seq_lens.tolist() == [16, 17]
+    assert device_metadata(ctx, pos, 2, CPU) is m  # the next layer reuses the build
+    assert not hasattr(ctx, "_device_meta") and vars(ctx).keys() == {"mode", "sequences"}  # nothing stored on it
+    # the next step: a new context object, even with the same position_ids tensor
+    ctx2 = EngineContext("decode", [{"block_table": [4]}, {"block_table": [7, 8]}])
+    m2 = device_metadata(ctx2, pos, 2, CPU)
+    assert m2 is not m and m2.block_tables.tolist() == [[4, 0], [7, 8]]
+    pre = EngineContext("prefill", [{"num_tokens": 2, "block_table": [1]}, {"num_tokens": 1, "block_table": [2]}])
+    mp = device_metadata(pre, torch.tensor([[0, 1, 0]]), 3, CPU)
+    assert mp.cu_seqlens.tolist() == [0, 2, 3] and mp.max_seqlen == 2
+
+
+def test_context_without_weakref_support_is_rebuilt():
+    class Slotted:
+        __slots__ = ("mode", "sequences")
+
+        def __init__(self, mode, sequences):
+            self.mode, self.sequences = mode, sequences
+
+    ctx = Slotted("decode", [{"block_table": [3]}])
+    pos = torch.tensor([[7]])
+    a = device_metadata(ctx, pos, 1, CPU)
+    b = device_metadata(ctx, pos, 1, CPU)
+    assert a is not b and a.positions.tolist() == b.positions.tolist() == [7]
+
+
+@pytest.fixture
+def engine_module(monkeypatch):
+    """A module importable as server.model.inference_context with the
+    reference's getter/context-manager contract (this package's stand-in for
+    the engine; the reference itself is never imported)."""
+    mod = types.ModuleType("server.model.inference_context")
+    mod.InferenceContext = EngineContext
+    mod.current = EngineContext()
+    mod.get_inference_context = lambda: mod.current
+    pkg, sub = types.ModuleType("server"), types.ModuleType("server.model")
+    pkg.__path__, sub.__path__ = [], []
+    pkg.model, sub.inference_context = sub, mod
+    for name, m in (("server", pkg), ("server.model", sub), ("server.model.inference_context", mod)):
+        monkeypatch.setitem(sys.modules, name, m)
+    return mod
+
+
+def test_getter_is_the_engines_when_importable(engine_module):
+    assert patch_mod.engine_context_getter() is engine_module.get_inference_context
+
+
+def test_getter_falls_back_to_the_mirror(monkeypatch):
+    monkeypatch.setattr(patch_mod, "ENGINE_CONTEXT_MODULE", "no_such_engine_module.inference_context")
+    assert patch_mod.engine_context_getter() is get_inference_context
+
+
+def test_patched_forward_reads_the_engine_context(engine_module):
+    from tests.qwen3_tiny import tiny_models
+
+    _, patched = tiny_models(torch.float32, "cpu", 4, 8)
+    # The engine's context says 2 prefill tokens for a 3-token input: the
+    # reference's ValueError names the engine context's sum (this package's
+    # own current context, empty, would say 0).
+    engine_module.current = EngineContext("prefill", [{"num_tokens": 2, "block_table": [0]}])
+    with torch.no_grad(), pytest.raises(ValueError, match="sum to 2"):
         patched(input_ids=torch.tensor([[1, 2, 3]]), position_ids=torch.tensor([[0, 1, 2]]), use_cache=False)

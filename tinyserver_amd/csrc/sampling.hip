@@ -677,12 +677,12 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   const float temp = a.temp[r * a.temp_s];
   RowSampler<T, UNIT> rs{a, s, static_cast<const T*>(a.logits) + r * a.ls0, fmaxf(temp, 1e-5f), 0.f, tid, lane, wave, 0.f, 0.f};
 
-  // Row maximum and its first index (rank 0), the finite minimum, and the
-  // last index of the minimum (the last rank).
+  // Row maximum and its first index (rank 0), the finite minimum, the last
+  // index of the minimum (the last rank), and the first NaN.
   // A thread visits its elements in increasing index order, so a strict >
   // keeps the first index of its maximum and <= the last of its minimum.
   float mx = -INFINITY, mn = INFINITY, fmn = INFINITY;
-  int imx = static_cast<int>(a.V), imn = -1;
+  int imx = static_cast<int>(a.V), imn = -1, inan = static_cast<int>(a.V);
   if constexpr (UNIT && sizeof(T) == 2) {
     if (rs.chunked()) {  // per 8-logit chunk: its max and min first, indices only when they win
       const u32x4* r4 = reinterpret_cast<const u32x4*>(rs.row);
@@ -696,15 +696,24 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
           l[2 * e] = lo_f<T>(w[e]);
           l[2 * e + 1] = hi_f<T>(w[e]);
         }
+        // cmax propagates NaN (v_maximum3_f32): a chunk holding a NaN never
+        // passes cmax > mx, and records its first NaN instead.
         float cmax = l[0], cmin = l[0], cfin = l[0] != -INFINITY ? l[0] : INFINITY;
 #pragma unroll
         for (int e = 1; e < 8; ++e) {
-          cmax = fmaxf(cmax, l[e]);
+          cmax = __builtin_elementwise_maximum(cmax, l[e]);
           cmin = fminf(cmin, l[e]);
           cfin = fminf(cfin, l[e] != -INFINITY ? l[e] : INFINITY);
         }
         fmn = fminf(fmn, cfin);
-        if (cmax > mx) {  // (a NaN chunk maximum never passes)
+        if (cmax != cmax && inan == static_cast<int>(a.V)) {
+          int first = 7;
+#pragma unroll
+          for (int e = 7; e >= 0; --e)
+            if (l[e] != l[e]) first = e;
+          inan = 8 * ch + first;
+        }
+        if (cmax > mx) {
           int first = 0;
 #pragma unroll
           for (int e = 7; e >= 0; --e)
@@ -726,6 +735,7 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
         if (x > mx) { mx = x; imx = i; }
         if (x <= mn) { mn = x; imn = i; }
         if (x != -INFINITY) fmn = fminf(fmn, x);
+        if (x != x) inan = min(inan, i);
       });
     }
   } else {
@@ -733,6 +743,7 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
       if (x > mx) { mx = x; imx = i; }
       if (x <= mn) { mn = x; imn = i; }
       if (x != -INFINITY) fmn = fminf(fmn, x);
+      if (x != x) inan = min(inan, i);
     });
   }
   for (int o = 32; o > 0; o >>= 1) {
@@ -741,21 +752,39 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
     if (omx > mx || (omx == mx && oimx < imx)) { mx = omx; imx = oimx; }
     if (omn < mn || (omn == mn && oimn > imn)) { mn = omn; imn = oimn; }
     fmn = fminf(fmn, ofm);
+    inan = min(inan, __shfl_xor(inan, o, 64));
   }
   __shared__ float red_mx[kSampWaves], red_mn[kSampWaves], red_fm[kSampWaves];
-  __shared__ int red_imx[kSampWaves], red_imn[kSampWaves];
+  __shared__ int red_imx[kSampWaves], red_imn[kSampWaves], red_nan[kSampWaves];
   if (lane == 0) {
     red_mx[wave] = mx; red_imx[wave] = imx;
     red_mn[wave] = mn; red_imn[wave] = imn;
     red_fm[wave] = fmn;
+    red_nan[wave] = inan;
   }
   __syncthreads();
   for (int w = 0; w < kSampWaves; ++w) {
     if (red_mx[w] > mx || (red_mx[w] == mx && red_imx[w] < imx)) { mx = red_mx[w]; imx = red_imx[w]; }
     if (red_mn[w] < mn || (red_mn[w] == mn && red_imn[w] > imn)) { mn = red_mn[w]; imn = red_imn[w]; }
     fmn = fminf(fmn, red_fm[w]);
+    inan = min(inan, red_nan[w]);
   }
   int64_t* out = a.out + r * a.out_s;
+  // A row whose softmax is NaN: a NaN logit, a +inf maximum, or every logit
+  // -inf. The reference's stable descending sort puts NaN first; its softmax
+  // and cumsum are then NaN everywhere, searchsorted of the NaN target
+  // returns vocab_size and the clamp makes that the last rank: the last
+  // index of the minimum (NaN ignored), or vocab_size - 1 when every logit is
+  // NaN. A greedy row still takes rank 0: the first NaN, else the first index
+  // of the maximum (0 when every logit is -inf).
+  const bool has_nan = inan < static_cast<int>(a.V);
+  if (has_nan || !(fabsf(rs.key_to_x(mx)) < INFINITY)) {
+    if (tid == 0) {
+      if (temp <= 0.f) *out = has_nan ? inan : (imx < static_cast<int>(a.V) ? imx : 0);
+      else *out = imn >= 0 ? imn : a.V - 1;
+    }
+    return;
+  }
   if (temp <= 0.f) {  // greedy: rank 0
     if (tid == 0) *out = imx;
     return;

@@ -7,11 +7,9 @@ context, and ``inference_context(ctx)`` to swap it for the duration of a
 forward. As in the reference the global is unsynchronised: one engine thread
 drives the forward and the swap.
 
-A context also carries the device-side metadata (padded block tables,
-cu_seqlens, positions) built by the first patched layer of a forward and
-reused by the others (``device_metadata``), so the host work and the
-host-to-device copy happen once per step rather than once per layer and per
-sequence.
+The model patch reads the engine's own context module when it imports
+(server.model.inference_context); this mirror serves when it does not. The
+patch stores nothing on a context.
 """
 
 from __future__ import annotations
@@ -25,8 +23,6 @@ from typing import Any, Iterator
 class InferenceContext:
     mode: str = "prefill"
     sequences: list[dict[str, Any]] = field(default_factory=list)
-    # (position_ids, key, metadata) of the last device-metadata build
-    _device_meta: Any = field(default=None, repr=False, compare=False)
 
 
 _current = InferenceContext()

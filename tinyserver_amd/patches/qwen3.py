@@ -5,8 +5,14 @@ the per-layer attention forward (:67-418, ``_patch_single_layer`` /
 ``_page_attention_forward``), ``qwen3_model_patcher`` (:469-480) and
 ``qwen3_model_loader`` (:483-505). The model takes the reference's flattened
 input: ``input_ids``/``position_ids`` of shape (1, total_tokens), and the
-current ``InferenceContext`` (tinyserver_amd.inference_context) saying
-whether the step is a prefill or a decode and which pages each sequence owns.
+current ``InferenceContext`` saying whether the step is a prefill or a decode
+and which pages each sequence owns. The context is read through the engine's
+own getter, as the reference does (qwen3.py:14, :289): the patcher binds
+``server.model.inference_context.get_inference_context`` when that module
+imports, so the unchanged engine's ``with inference_context(ctx)`` is what
+the layers see; without it, ``tinyserver_amd.inference_context`` (the same
+contract) is used. Any object with ``mode`` and ``sequences`` works; nothing
+is stored on it.
 
 Per layer the reference runs q_norm, k_norm, apply_rotary_pos_emb and a store
 loop (one launch per sequence at decode, a Python mapping loop at prefill),
@@ -26,13 +32,27 @@ CPU tensors raise.
 
 from __future__ import annotations
 
+import importlib
+import weakref
 from dataclasses import dataclass
-from typing import Callable
+from typing import Any, Callable
 
 import torch
 
-from ..inference_context import InferenceContext, get_inference_context
+from .. import inference_context as _own_context
 from ..kernels import flash_attn_varlen_func, paged_attention_forward, paged_decode_step, qk_norm_rope_store
+
+ENGINE_CONTEXT_MODULE = "server.model.inference_context"
+
+
+def engine_context_getter() -> Callable[[], Any]:
+    """The getter of the engine's current InferenceContext: the reference
+    engine's module-global (server/model/inference_context.py:27-29) when that
+    module imports, else this package's mirror of it."""
+    try:
+        return importlib.import_module(ENGINE_CONTEXT_MODULE).get_inference_context
+    except ImportError:
+        return _own_context.get_inference_context
 
 
 def _available_memory(memory_utilization: float) -> int:
@@ -75,19 +95,34 @@ class DeviceMetadata:
     table_slots: int = 0            # sum of the block tables' lengths (host-side size of the step's KV)
 
 
-def device_metadata(ctx: InferenceContext, position_ids: torch.Tensor | None, num_tokens: int,
+# The last build: (weak reference to its context, position_ids, key, metadata).
+# One entry suffices: the layers of a forward run one after another on the
+# engine's single thread (the reference's own assumption for its context,
+# server/model/inference_context.py:7-10).
+_last_build: tuple | None = None
+
+
+def device_metadata(ctx: Any, position_ids: torch.Tensor | None, num_tokens: int,
                     device: torch.device) -> DeviceMetadata:
     """Build the padded block tables, cu_seqlens and, for a decode step, the
     positions and sequence lengths, with the reference's checks. The tables
     and cu_seqlens are packed into one int32 buffer on the host and copied in
-    one transfer; the device tensors are views of it. The layers of one forward share the build:
-    HF hands every layer the same position_ids tensor, and the context keeps a
-    reference to it (so a later step's tensor is a different object). The
-    context's sequences must not be changed in place during a forward."""
-    cached = ctx._device_meta
-    if (cached is not None and cached[0] is position_ids and cached[1] == (ctx.mode, num_tokens, str(device),
-                                                                           getattr(position_ids, "_version", None))):
-        return cached[2]
+    one transfer; the device tensors are views of it.
+
+    ``ctx`` is any object with ``mode`` and ``sequences`` (the reference's
+    InferenceContext, server/model/inference_context.py:18-21). The layers of
+    one forward share the build: they see the same context object and the
+    same position_ids tensor, which HF hands every layer; the engine makes a
+    new context every step (server/executor/engine.py:579-582), and the
+    cache holds only a weak reference to it, so a later step -- or a context
+    at a recycled address -- never hits a stale entry. A context that cannot
+    be weakly referenced is rebuilt per layer. The context's sequences must
+    not be changed in place during a forward."""
+    global _last_build
+    key = (ctx.mode, num_tokens, str(device), getattr(position_ids, "_version", None))
+    last = _last_build
+    if last is not None and last[0]() is ctx and last[1] is position_ids and last[2] == key:
+        return last[3]
     seqs = ctx.sequences
     if ctx.mode == "prefill":
         lengths = [int(s["num_tokens"]) for s in seqs]
@@ -117,8 +152,11 @@ def device_metadata(ctx: InferenceContext, position_ids: torch.Tensor | None, nu
     dev = packed.to(device)
     meta = DeviceMetadata(dev[:n_tab].view(len(seqs), width), dev[n_tab:], max(lengths, default=0), positions,
                           seq_lens, sum(len(s["block_table"]) for s in seqs))
-    ctx._device_meta = (position_ids, (ctx.mode, num_tokens, str(device), getattr(position_ids, "_version", None)),
-                        meta)
+    try:
+        ref = weakref.ref(ctx)
+    except TypeError:  # (e.g. a slotted class without __weakref__): no caching
+        ref = None
+    _last_build = (ref, position_ids, key, meta) if ref is not None else None
     return meta
 
 
@@ -135,7 +173,8 @@ FUSED_DECODE_MAX_TILES = 16384
 
 
 def _patch_single_layer(layer: torch.nn.Module,
-                        rotary_emb: Callable[[torch.Tensor, torch.Tensor], tuple[torch.Tensor, torch.Tensor]]) -> None:
+                        rotary_emb: Callable[[torch.Tensor, torch.Tensor], tuple[torch.Tensor, torch.Tensor]],
+                        get_context: Callable[[], Any]) -> None:
     """Replace layer.self_attn.forward by the paged forward on the kernels."""
     attn = layer.self_attn
     cfg = attn.config
@@ -160,7 +199,7 @@ def _patch_single_layer(layer: torch.nn.Module,
         cos = cos.reshape(-1, head_dim)
         sin = sin.reshape(-1, head_dim)
 
-        ctx = get_inference_context()
+        ctx = get_context()
         meta = device_metadata(ctx, position_ids, batch * seq_len, hidden_states.device)
         block_size = attn.k_cache.shape[2]
         if ctx.mode == "prefill":
@@ -190,16 +229,19 @@ def _patch_single_layer(layer: torch.nn.Module,
     attn.forward = _page_attention_forward
 
 
-def qwen3_model_patcher(model):
-    """Route every layer's attention through the paged kernels."""
+def qwen3_model_patcher(model, get_context: Callable[[], Any] | None = None):
+    """Route every layer's attention through the paged kernels. The layers
+    read the step's context through ``get_context`` (default: the engine's
+    getter, ``engine_context_getter()``)."""
+    getter = get_context if get_context is not None else engine_context_getter()
     for layer in model.model.layers:
-        _patch_single_layer(layer, model.model.rotary_emb)
+        _patch_single_layer(layer, model.model.rotary_emb, getter)
     return model
 
 
 def qwen3_model_loader(model, config, memory_utilization: float, block_size: int, dtype: torch.dtype,
-                       device: str) -> int:
+                       device: str, get_context: Callable[[], Any] | None = None) -> int:
     """Allocate the KV pool and patch the model; returns the block count."""
     num_blocks = qwen3_cache_allocator(model, config, memory_utilization, block_size, dtype, device)
-    qwen3_model_patcher(model)
+    qwen3_model_patcher(model, get_context)
     return num_blocks
