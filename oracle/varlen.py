@@ -118,3 +118,26 @@ def prefill_sdpa_block_mask(q, k, v, seq_lens, head_dim):
         start += n
     out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=head_dim**-0.5, enable_gqa=True)
     return out.transpose(1, 2).reshape(1, total, -1)
+
+
+def prefill_sdpa_per_sequence(q, k, v, cu_seqlens, head_dim=None):
+    """The same prefill math as the reference's CPU branch
+    (server/model/patches/qwen3.py:132-171: causal SDPA within each sequence,
+    GQA), vectorised per sequence instead of one block-diagonal mask over the
+    packed tokens: one causal SDPA per sequence, in the inputs' dtype.
+
+    q: (T, Hq, D), k/v: (T, Hkv, D) token-major; returns (T, Hq, D).
+    """
+    head_dim = head_dim or q.shape[-1]
+    out = torch.empty_like(q)
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    for b in range(len(cu) - 1):
+        a, e = cu[b], cu[b + 1]
+        if e <= a:
+            continue
+        qs = q[a:e].transpose(0, 1)[None]  # (1, Hq, L, D)
+        ks = k[a:e].transpose(0, 1)[None]
+        vs = v[a:e].transpose(0, 1)[None]
+        o = F.scaled_dot_product_attention(qs, ks, vs, is_causal=True, scale=head_dim**-0.5, enable_gqa=True)
+        out[a:e] = o[0].transpose(0, 1)
+    return out

@@ -62,7 +62,7 @@ def test_other_dtypes(dtype, head_dim):
 
 def test_strided_projection_views():
     """q/k as views of one fused projection output (1, T, (Hq+2Hkv)*D)."""
-    w = W.make("qwen3-4b-mixed-prefill")
+    w = W.make("qwen3-4b-prefill-8seq")
     T, hq, hkv, d = w.q.shape[0], w.q.shape[1], w.k.shape[1], w.q.shape[2]
     fused = torch.cat([w.q.reshape(T, -1), w.k.reshape(T, -1), w.v.reshape(T, -1)], dim=1).to(DEV)
     q = fused[:, : hq * d].view(T, hq, d)
@@ -82,7 +82,7 @@ def test_fused_store(mode):
         cu = torch.arange(b + 1, dtype=torch.int32)
         pos = w.positions
     else:
-        w = W.make("qwen3-4b-mixed-prefill", poison=True)
+        w = W.make("qwen3-4b-prefill-8seq", poison=True)
         cu, pos = w.cu_seqlens, None
     kc, vc = w.k_cache.to(DEV), w.v_cache.to(DEV)
     qg, kg = qk_norm_rope_store(w.q.to(DEV), w.k.to(DEV), w.v.to(DEV), w.q_weight.to(DEV), w.k_weight.to(DEV),
@@ -131,7 +131,7 @@ def test_fused_store_page_256(mode):
         b = len(w.ctx_lens)
         cu, pos = torch.arange(b + 1, dtype=torch.int32), w.positions
     else:
-        w = W.make("qwen3-4b-mixed-prefill", poison=True)
+        w = W.make("qwen3-4b-prefill-8seq", poison=True)
         cu, pos = w.cu_seqlens, None
     tables, lists, kc0, vc0 = _repage(w, 256, seed=5)
     kc, vc = kc0.to(DEV), vc0.to(DEV)

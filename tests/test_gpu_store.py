@@ -64,7 +64,7 @@ def test_reference_cases(case, dtype):
 
 @pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64])
 def test_mapped_matches_oracle_prefill_shape(index_dtype):
-    w = W.make("qwen3-4b-mixed-prefill")
+    w = W.make("qwen3-4b-prefill-8seq")
     blocks, slots = ok.build_block_slot_mappings(
         [{"num_tokens": int(n), "block_table": b} for n, b in zip(w.seq_lens, w.block_lists)], W.PAGE)
     k_src, v_src = w.k.transpose(0, 1).contiguous(), w.v.transpose(0, 1).contiguous()
@@ -80,7 +80,7 @@ def test_mapped_matches_oracle_prefill_shape(index_dtype):
 
 def test_paged_prefill_matches_mapped():
     """Device-side addressing == the call site's mapping loop (qwen3.py:296-318)."""
-    w = W.make("qwen3-4b-mixed-prefill")
+    w = W.make("qwen3-4b-prefill-8seq")
     blocks, slots = ok.build_block_slot_mappings(
         [{"num_tokens": int(n), "block_table": b} for n, b in zip(w.seq_lens, w.block_lists)], W.PAGE)
     kr, vr = w.k_cache.clone(), w.v_cache.clone()

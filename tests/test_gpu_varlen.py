@@ -6,7 +6,7 @@ Cases: the reference's self-test configuration (varlen_attention.py:257-307:
 fp16, seed 42, 4 sequences of U[32,256] tokens, 16/4 heads, D 64, causal and
 not), bf16/fp16/fp32, GQA groups, q_len != k_len, length-1 sequences, the
 call site's strided (T, H, D) views (qwen3.py:199-201), and the full
-Qwen3-8B-shaped 16-sequence prefill checked on sampled sequences and heads.
+Qwen3-8B-shaped 16-sequence prefill, every sequence and head.
 Tolerance: max-abs 2e-2, mean-abs 2e-3 for 16-bit dtypes (the reference's
 own fp16 check is max 5e-2, mean 1e-3); fp32 1e-4.
 """
@@ -148,21 +148,15 @@ def test_call_site_strided_views():
     assert_close(out, ref, what="strided views")
 
 
-def test_qwen3_8b_prefill_sampled():
+def test_qwen3_8b_prefill_full():
+    """The Qwen3-8B 16-sequence prefill, every sequence and every head."""
     w = W.make("qwen3-8b-prefill-16seq", device=DEV)
     out = flash_attn_varlen_func(w.q, w.k, w.v, w.cu_seqlens, w.cu_seqlens, w.max_seqlen, w.max_seqlen, True)
     torch.cuda.synchronize()
-    cu = w.cu_seqlens.tolist()
-    order = sorted(range(len(cu) - 1), key=lambda s: cu[s + 1] - cu[s])
-    for s in (order[0], order[-1]):
-        a, b = cu[s], cu[s + 1]
-        heads = [0, 13, 31]
-        sub_q = w.q[a:b, heads].cpu()
-        sub_k = w.k[a:b, [h // 4 for h in heads]].cpu()
-        sub_v = w.v[a:b, [h // 4 for h in heads]].cpu()
-        c1 = torch.tensor([0, b - a], dtype=torch.int32)
-        ref = ov.flash_attn_varlen_func(sub_q, sub_k, sub_v, c1, c1, b - a, b - a, True)
-        assert_close(out[a:b, heads], ref, what=f"seq {s} len {b - a}")
+    print(f"{w.name}: {w.q.shape[0]} tokens, oracle on the CPU", flush=True)
+    cu = w.cu_seqlens.cpu()
+    ref = ov.flash_attn_varlen_func(w.q.cpu(), w.k.cpu(), w.v.cpu(), cu, cu, w.max_seqlen, w.max_seqlen, True)
+    assert_close(out, ref, what="Qwen3-8B prefill, all 16 sequences x 32 heads")
 
 
 def test_long_sequence_sampled_rows():

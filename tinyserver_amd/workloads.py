@@ -8,8 +8,10 @@ Shapes follow Qwen3 attention (head_dim 128, page 16):
   qwen3-8b-decode-bs64      B=64,  32/8 heads, ctx U[512,4096], pool sum(pages)*1.1
   qwen3-8b-prefill-16seq    16 packed seqs, L U[128,2048], 32/8 heads
   qwen3-32b-decode-bs32     B=32,  64/8 heads, ctx 32768 each
-  qwen3-4b-mixed            120 decode seqs ctx U[256,8192] + 8 prefill seqs
-                            L U[256,1024], 32/8 heads, one shared pool
+  qwen3-4b-prefill-8seq     8 packed seqs, L U[256,1024], 32/8 heads
+  qwen3-4b-mixed            one continuous-batching step on one shared pool:
+                            8 new prefill seqs L U[256,1024], then 120 decode
+                            seqs ctx U[256,8192]; 32/8 heads
 
 A decode step stores one new token per sequence at position ctx-1 (pages for
 positions 0..ctx-2 hold N(0,1) K/V) and attends over ctx tokens. cos/sin are
@@ -207,17 +209,90 @@ WORKLOADS = {
                                                len_hi=2048)),
     "qwen3-32b-decode-bs32": ("decode", dict(seed=4, batch=32, num_heads=64, num_kv_heads=8, ctx_lo=32768,
                                              ctx_hi=32768, pool_slack=1.0)),
-    "qwen3-4b-mixed-decode": ("decode", dict(seed=5, batch=120, num_heads=32, num_kv_heads=8, ctx_lo=256,
-                                             ctx_hi=8192)),
-    "qwen3-4b-mixed-prefill": ("prefill", dict(seed=6, num_seqs=8, num_heads=32, num_kv_heads=8, len_lo=256,
-                                               len_hi=1024)),
+    # The mixed step's prefill shape on a pool of its own (a parity case for
+    # the stores and the norm, which do not need the 2 GB shared pool).
+    "qwen3-4b-prefill-8seq": ("prefill", dict(seed=6, num_seqs=8, num_heads=32, num_kv_heads=8, len_lo=256,
+                                              len_hi=1024)),
+    "qwen3-4b-mixed": ("mixed", dict(seed=5, decode_batch=120, ctx_lo=256, ctx_hi=8192, prefill_seqs=8,
+                                     len_lo=256, len_hi=1024, num_heads=32, num_kv_heads=8)),
 }
 
 
 def make(name: str, **overrides):
     kind, kw = WORKLOADS[name]
     kw = {**kw, **overrides}
-    return make_decode(name, **kw) if kind == "decode" else make_prefill(name, **kw)
+    maker = {"decode": make_decode, "prefill": make_prefill, "mixed": make_mixed}[kind]
+    return maker(name, **kw)
+
+
+@dataclass
+class MixedWorkload:
+    """One continuous-batching step over one shared KV pool, as the scheduler
+    issues it: a prefill batch of new sequences, then a decode batch of the
+    running ones (server/executor/scheduler.py:128-227; each batch is its own
+    forward, server/model/patches/qwen3.py:291-327 then :328-416). The two
+    halves own disjoint pages of the same k_cache/v_cache tensors and share
+    the layer's norm weights."""
+
+    name: str
+    seed: int
+    prefill: PrefillWorkload
+    decode: DecodeWorkload
+
+    @property
+    def k_cache(self):
+        return self.decode.k_cache
+
+    @property
+    def v_cache(self):
+        return self.decode.v_cache
+
+    def to(self, device) -> "MixedWorkload":
+        d = self.decode.to(device)
+        p = self.prefill.to(device)
+        p.k_cache, p.v_cache = d.k_cache, d.v_cache  # still one pool
+        return MixedWorkload(self.name, self.seed, p, d)
+
+
+def make_mixed(name, seed, decode_batch, ctx_lo, ctx_hi, prefill_seqs, len_lo, len_hi, num_heads, num_kv_heads,
+               pool_slack=1.1, dtype=torch.bfloat16, device="cpu", poison=False, head_dim=HEAD_DIM, page=PAGE):
+    """The shared-pool step. Draw order: decode context lengths, prefill
+    lengths, one page permutation of the pool (decode sequences take their
+    pages first, then the prefill sequences), cache contents, decode q/k/v,
+    prefill q/k/v, norm weights."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    ctx = torch.randint(ctx_lo, ctx_hi + 1, (decode_batch,), generator=gen, device=device).cpu()
+    lens = torch.randint(len_lo, len_hi + 1, (prefill_seqs,), generator=gen, device=device).cpu()
+    dpages = [math.ceil(int(n) / page) for n in ctx]
+    ppages = [math.ceil(int(n) / page) for n in lens]
+    nb = math.ceil((sum(dpages) + sum(ppages)) * pool_slack)
+    bt_all, lists = _assign_pages(gen, dpages + ppages, nb, device)
+    dlists, plists = lists[:decode_batch], lists[decode_batch:]
+    dbt = bt_all[:decode_batch, : max(max(dpages), 1)].contiguous()
+    pbt = bt_all[decode_batch:, : max(max(ppages), 1)].contiguous()
+    k_cache = _randn(gen, (nb, num_kv_heads, page, head_dim), dtype, device)
+    v_cache = _randn(gen, (nb, num_kv_heads, page, head_dim), dtype, device)
+    dq = _randn(gen, (decode_batch, num_heads, head_dim), dtype, device)
+    dk = _randn(gen, (decode_batch, num_kv_heads, head_dim), dtype, device)
+    dv = _randn(gen, (decode_batch, num_kv_heads, head_dim), dtype, device)
+    T = int(lens.sum())
+    pq = _randn(gen, (T, num_heads, head_dim), dtype, device)
+    pk = _randn(gen, (T, num_kv_heads, head_dim), dtype, device)
+    pv = _randn(gen, (T, num_kv_heads, head_dim), dtype, device)
+    qw = (1.0 + 0.1 * torch.randn(head_dim, generator=gen, device=device)).to(dtype)
+    kw = (1.0 + 0.1 * torch.randn(head_dim, generator=gen, device=device)).to(dtype)
+    if poison:  # everything but the decode sequences' stored prefixes
+        _poison_unused(k_cache, v_cache, dlists + plists, [int(n) - 1 for n in ctx] + [0] * len(plists))
+    dcos, dsin = rope_cos_sin(ctx - 1, head_dim, ROPE_THETA, dtype)
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0).to(torch.int32)
+    positions = torch.cat([torch.arange(int(n)) for n in lens])
+    pcos, psin = rope_cos_sin(positions, head_dim, ROPE_THETA, dtype)
+    dec = DecodeWorkload(name + ":decode", seed, ctx, dbt.to(device), dlists, k_cache, v_cache, dq, dk, dv, qw, kw,
+                         dcos.to(device), dsin.to(device))
+    pre = PrefillWorkload(name + ":prefill", seed, lens, cu.to(device), pbt.to(device), plists, k_cache, v_cache, pq,
+                          pk, pv, qw, kw, pcos.to(device), psin.to(device), positions.to(device))
+    return MixedWorkload(name, seed, pre, dec)
 
 
 def decode_bytes(ctx_lens, num_heads, num_kv_heads, head_dim=HEAD_DIM, page=PAGE, elem=2) -> int:
