@@ -4,23 +4,37 @@ Headline (the metric line): paged decode attention at the Qwen3-8B shape,
 batch 64, 32 q / 8 kv heads, head_dim 128, page 16, contexts U[512, 4096]
 (seed 2) -- microseconds per layer and achieved HBM bandwidth against the
 8 TB/s MI355X peak. A step is one decode-attention call over the batch (the
-stream-K kernel plus its cut-unit merge kernel, both on the caller's stream).
-Three copies of the KV pool are rotated so repeated steps cannot be served
-from the 256 MB MALL. The K timed steps are bracketed by one pair of HIP
-events recorded on the stream the kernels run on (and by synchronisations
-for the wall clock); a second pass times each call separately for the median
-and p10/p90.
+stream kernel plus its merge kernel, both on the caller's stream). Three
+copies of the KV pool are rotated so repeated steps cannot be served from
+the 256 MB MALL. The K timed steps are bracketed by one pair of HIP events
+recorded on the stream the kernels run on (and by synchronisations for the
+wall clock); a second pass times each call separately for the median and
+p10/p90.
 
-Also measured (in "secondary"): the whole decode block (fused QK
-norm+RoPE+store, then attention), the varlen prefill at the Qwen3-8B
-16-sequence shape (TFLOP/s against 2.5 PFLOP/s bf16 dense), the fused QK
-norm+RoPE+store at that shape (GB/s), the Qwen3-32B bs32 32k-context decode,
-the Qwen3-4B mixed batch (prefill+store then decode), the decode block as
-one fused launch, and batched sampling over 64 rows of the Qwen3 vocabulary
-(three filter settings). The CPU baseline
-runs the reference's CPU decode path (per-token gather loop +
-repeat_interleave + SDPA, restated in the oracle) on a bounded sample of the
-same batch on this host's cores.
+Also measured (in "secondary"), each with its roofline and a CPU baseline:
+  qwen3-0.6b-decode-bs4     the reference's CPU-runnable decode case
+  qwen3-32b-decode-bs32     32k-context decode
+  qwen3-8b-prefill-16seq    varlen prefill (TFLOP/s against 2.5 PFLOP/s bf16
+                            dense) and its fused norm/RoPE/store (GB/s)
+  qwen3-4b-mixed            the continuous-batching step on one shared pool,
+                            in scheduler order: the prefill batch's
+                            norm/RoPE/store and varlen attention, then the
+                            decode batch's norm/RoPE/store and paged
+                            attention; per-launch times and rooflines
+  qwen3-8b-decode-bs64-page256  the headline batch on the server's default
+                            256-token pages (decode and its fused store)
+  sampling-qwen3-vocab-bs64 batched sampling over 64 Qwen3-vocab rows
+The headline line also carries the decode block (norm/RoPE/store, then
+attention) as two launches and as the single fused launch.
+
+CPU baselines run on this host's cores, on the same seeded inputs, as two
+variants (server/model/patches/qwen3.py): "literal", the reference's own CPU
+branches (decode: per-token gather loop + repeat_interleave + SDPA, :359-385
+and :423-466; prefill: one SDPA with a block-diagonal causal mask over the
+packed tokens, :132-171), and "vectorized", the same math with index_select
+gathers and per-sequence causal SDPA. Each is bounded to a few seconds of
+CPU work: a batch that one pass does not fit is sampled sequence by
+sequence and scaled by context length, as its "sample" says.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --workload NAME  (one workload alone, e.g. for a
@@ -51,6 +65,7 @@ HEADLINE = "qwen3-8b-decode-bs64"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_traffic.json")
 
 
+# ------------------------------------------------------------------ timing --
 def time_region(fn, steps, warmup):
     """warmup untimed calls, then `steps` calls bracketed by synchronisations
     and one pair of events on the current stream. Returns (event ms per call,
@@ -86,15 +101,146 @@ def _spread(ev):
             "p90": ev[(9 * len(ev)) // 10] * 1e3}
 
 
-def bench_decode(name, steps, warmup, num_workgroups=0, copies=3, with_block=False):
+def norm_store_bytes(tokens, hq, hkv, d=128, elem=2):
+    """Algorithmic bytes of the fused norm/RoPE/store: read q, k, v, cos, sin
+    and the two weights; write the rotated q and k and the K/V cache rows."""
+    return (elem * tokens * d * (hq + 2 * hkv) + 2 * elem * tokens * d + 2 * elem * d
+            + elem * tokens * d * (hq + hkv) + 2 * elem * tokens * hkv * d)
+
+
+def _roof_hbm(nbytes, us):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": int(nbytes)}
+
+
+def _roof_mfma(flops, us):
+    tf = flops / (us * 1e-6) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops_per_launch": int(flops)}
+
+
+# ----------------------------------------------------------- CPU baselines --
+def _threads():
+    return {"cores": torch.get_num_threads(), "host_cpus": os.cpu_count()}
+
+
+def _timed_passes(run_item, n_items, weights, target_s):
+    """Time run_item(i) over items 0..n-1 in order, whole passes until about
+    target_s seconds of work (at least one item). Returns (seconds for one
+    whole pass, description of the sample)."""
+    passes, done_w, done_t, t_start = [], 0.0, 0.0, time.perf_counter()
+    total_w = float(sum(weights))
+    while True:
+        t_pass, i = 0.0, 0
+        while i < n_items:
+            t0 = time.perf_counter()
+            run_item(i)
+            dt = time.perf_counter() - t0
+            t_pass += dt
+            done_w += weights[i]
+            done_t += dt
+            i += 1
+            if time.perf_counter() - t_start > target_s and not passes:
+                break
+        if i == n_items:
+            passes.append(t_pass)
+        if time.perf_counter() - t_start > target_s or len(passes) >= 20:
+            break
+    if passes:
+        return statistics.median(passes), f"median of {len(passes)} whole passes ({done_t:.1f} s of CPU work)"
+    return done_t * total_w / done_w, (f"first {i} of {n_items} sequences ({done_w / total_w:.1%} of the batch's "
+                                       f"context), scaled to the whole batch by context length ({done_t:.1f} s)")
+
+
+def cpu_decode_baseline(w, literal, target_s):
+    """The reference's CPU decode attention (server/model/patches/qwen3.py:
+    359-385, restated in oracle.paged.decode_cpu_path) on w's batch: the
+    literal per-token gather loop (:444-466) or the index_select gather. The
+    new tokens are already in the pool: attention only."""
+    from oracle import paged as op
+    from tinyserver_amd import workloads as W
+
+    n = len(w.ctx_lens)
+    pages = sorted({p for lst in w.block_lists for p in lst})
+    remap = {p: i for i, p in enumerate(pages)}
+    idx = torch.tensor(pages, device=w.k_cache.device)
+    kc, vc = w.k_cache[idx].cpu(), w.v_cache[idx].cpu()
+    tables = [[remap[p] for p in lst] for lst in w.block_lists]
+    q = w.q.cpu().transpose(0, 1).unsqueeze(0).contiguous()  # (1, Hq, B, D)
+    positions = [int(x) - 1 for x in w.ctx_lens]
+
+    def one(i):
+        op.decode_cpu_path(q[:, :, i:i + 1], kc, vc, tables[i:i + 1], positions[i:i + 1], literal_gather=literal)
+
+    t, sample = _timed_passes(one, n, [int(x) for x in w.ctx_lens], target_s)
+    nbytes = W.decode_bytes(w.ctx_lens, w.num_heads, w.num_kv_heads, page=w.k_cache.shape[2])
+    return {"value": round(nbytes / t / 1e12, 6), "unit": "TB/s", **_threads(), "kind": "port",
+            "variant": "literal" if literal else "vectorized",
+            "path": ("per-token gather loop + repeat_interleave + SDPA (qwen3.py:359-385, 423-466)" if literal
+                     else "index_select page gather + repeat_interleave + SDPA per sequence"),
+            "sample": sample, "us_per_layer": round(t * 1e6, 1), "tokens_per_s": round(n / t, 2)}
+
+
+def cpu_prefill_baseline(p, literal, target_s):
+    """The reference's CPU prefill attention on p's packed batch: one SDPA
+    with a block-diagonal causal mask (qwen3.py:132-171, literal) or one
+    causal SDPA per sequence (vectorized). Attention only."""
+    from oracle import varlen as ov
+    from tinyserver_amd import workloads as W
+
+    q, k, v, cu = p.q.cpu(), p.k.cpu(), p.v.cpu(), p.cu_seqlens.cpu()
+    lens = [int(x) for x in p.seq_lens]
+    flops = W.prefill_flops(lens, q.shape[1])
+    if literal:
+        qh, kh, vh = (t.transpose(0, 1)[None].contiguous() for t in (q, k, v))
+
+        def one(_):
+            ov.prefill_sdpa_block_mask(qh, kh, vh, lens, q.shape[2])
+
+        t, sample = _timed_passes(one, 1, [1], target_s)
+        sample = "the whole packed batch, " + sample
+    else:
+        def one(i):
+            ov.prefill_sdpa_per_sequence(q[cu[i]:cu[i + 1]], k[cu[i]:cu[i + 1]], v[cu[i]:cu[i + 1]],
+                                         torch.tensor([0, lens[i]]))
+
+        t, sample = _timed_passes(one, len(lens), [n * n for n in lens], target_s)
+    return {"value": round(flops / t / 1e12, 6), "unit": "TFLOP/s", **_threads(), "kind": "port",
+            "variant": "literal" if literal else "vectorized",
+            "path": ("one SDPA with a block-diagonal causal mask over the packed tokens (qwen3.py:132-171)"
+                     if literal else "one causal SDPA per sequence"),
+            "sample": sample, "us_per_layer": round(t * 1e6, 1), "tokens_per_s": round(sum(lens) / t, 1)}
+
+
+def cpu_sampling_baseline(logits, temperature, top_k, top_p, uniforms, target_s):
+    """The reference's batched sampler (server/model/sampling.py:119-194, its
+    torch ops restated in oracle.sampling) on the CPU."""
+    from oracle import sampling as osm
+
+    args = [t.cpu() for t in (logits, temperature, top_k, top_p, uniforms)]
+    t, sample = _timed_passes(lambda _: osm.sample_tokens(*args), 1, [1], target_s)
+    nbytes = logits.numel() * logits.element_size()
+    return {"value": round(nbytes / t / 1e9, 4), "unit": "GB/s of logits", **_threads(), "kind": "port",
+            "variant": "literal", "path": "sort + softmax + cumsum + searchsorted, fp32", "sample": sample,
+            "us_per_call": round(t * 1e6, 1)}
+
+
+# ------------------------------------------------------------- GPU parts --
+def _decode_pools(w, copies):
+    return [(w.k_cache, w.v_cache)] + [(w.k_cache.clone(), w.v_cache.clone()) for _ in range(copies - 1)]
+
+
+def bench_decode(name, steps, warmup, num_workgroups=0, copies=3, with_block=False, **make_kw):
     from tinyserver_amd import workloads as W
     from tinyserver_amd.kernels import paged_attention_forward, paged_decode_step, qk_norm_rope_store
 
     dev = torch.device("cuda:0")
-    w = W.make(name, device=dev)
+    w = W.make(name, device=dev, **make_kw)
     B = len(w.ctx_lens)
+    page = w.k_cache.shape[2]
     seq_lens = w.ctx_lens.to(torch.int32).to(dev)
-    pools = [(w.k_cache, w.v_cache)] + [(w.k_cache.clone(), w.v_cache.clone()) for _ in range(copies - 1)]
+    pools = _decode_pools(w, copies)
     cu = torch.arange(B + 1, dtype=torch.int32, device=dev)
     pos = w.positions.to(dev)
     q_rot, _ = qk_norm_rope_store(w.q, w.k, w.v, w.q_weight, w.k_weight, w.cos, w.sin, w.eps, pools[0][0],
@@ -103,36 +249,41 @@ def bench_decode(name, steps, warmup, num_workgroups=0, copies=3, with_block=Fal
 
     def attn(i):
         kc, vc = pools[i % copies]
-        paged_attention_forward(q_rot, kc, vc, w.block_tables, W.PAGE, seq_lens, num_workgroups=num_workgroups,
+        paged_attention_forward(q_rot, kc, vc, w.block_tables, page, seq_lens, num_workgroups=num_workgroups,
                                 out=out)
 
     ev_ms, wall_ms = time_region(attn, steps, warmup)
     spread = _spread(time_each(attn, max(20, min(steps, 200)), warmup + steps))
-    nbytes = W.decode_bytes(w.ctx_lens, w.num_heads, w.num_kv_heads)
+    nbytes = W.decode_bytes(w.ctx_lens, w.num_heads, w.num_kv_heads, page=page)
+    us = ev_ms * 1e3
     res = {
-        "workload": name,
-        "batch": B,
-        "num_heads": w.num_heads,
-        "num_kv_heads": w.num_kv_heads,
-        "sum_ctx": int(w.ctx_lens.sum()),
-        "bytes_per_call": nbytes,
-        "us_per_call": ev_ms * 1e3,
-        "us_per_call_median": spread["median"],
-        "us_per_call_p10": spread["p10"],
-        "us_per_call_p90": spread["p90"],
-        "wall_ms_per_step": wall_ms,
+        "workload": name if page == W.PAGE else f"{name}-page{page}",
+        "batch": B, "num_heads": w.num_heads, "num_kv_heads": w.num_kv_heads, "page": page,
+        "sum_ctx": int(w.ctx_lens.sum()), "bytes_per_call": nbytes,
+        "us_per_call": us, "us_per_call_median": spread["median"], "us_per_call_p10": spread["p10"],
+        "us_per_call_p90": spread["p90"], "wall_ms_per_step": wall_ms,
+        "achieved_gbs": nbytes / (us * 1e-6) / 1e9, "tokens_per_s": B / (us * 1e-6),
+        "roofline": {**_roof_hbm(nbytes, us), "kernel": "paged_decode_stream + paged_decode_stream_merge"},
     }
-    res["achieved_gbs"] = nbytes / (res["us_per_call"] * 1e-6) / 1e9
     res["pct_peak_hbm"] = 100.0 * res["achieved_gbs"] / HBM_PEAK_GBS
-    res["tokens_per_s"] = B / (res["us_per_call"] * 1e-6)
     if with_block:
         qw, kw, cos, sin = w.q_weight, w.k_weight, w.cos, w.sin
+
+        def store(i):
+            kc, vc = pools[i % copies]
+            qk_norm_rope_store(w.q, w.k, w.v, qw, kw, cos, sin, w.eps, kc, vc, w.block_tables, cu, pos,
+                               return_k=False)
+
+        s_us = time_region(store, steps, warmup)[0] * 1e3
+        sb = norm_store_bytes(B, w.num_heads, w.num_kv_heads)
+        res["norm_rope_store_us"] = s_us
+        res["norm_rope_store_roofline"] = _roof_hbm(sb, s_us)
 
         def block(i):
             kc, vc = pools[i % copies]
             qr, _ = qk_norm_rope_store(w.q, w.k, w.v, qw, kw, cos, sin, w.eps, kc, vc, w.block_tables, cu, pos,
                                        return_k=False)
-            paged_attention_forward(qr, kc, vc, w.block_tables, W.PAGE, seq_lens, num_workgroups=num_workgroups,
+            paged_attention_forward(qr, kc, vc, w.block_tables, page, seq_lens, num_workgroups=num_workgroups,
                                     out=out)
 
         res["block_us_per_call"] = time_region(block, steps, warmup)[0] * 1e3
@@ -142,7 +293,12 @@ def bench_decode(name, steps, warmup, num_workgroups=0, copies=3, with_block=Fal
             paged_decode_step(w.q, w.k, w.v, qw, kw, cos, sin, w.eps, kc, vc, w.block_tables, seq_lens,
                               num_workgroups=num_workgroups, out=out)
 
-        res["block_fused_us_per_call"] = time_region(block_fused, steps, warmup)[0] * 1e3
+        try:
+            res["block_fused_us_per_call"] = time_region(block_fused, steps, warmup)[0] * 1e3
+        except NotImplementedError as e:  # outside the fused kernel's coverage
+            res["block_fused_us_per_call"] = None
+            res["block_fused_note"] = str(e)
+    del pools
     return res, w
 
 
@@ -153,7 +309,6 @@ def bench_prefill(name, steps, warmup):
     dev = torch.device("cuda:0")
     w = W.make(name, device=dev)
     T, hq, hkv = w.q.shape[0], w.q.shape[1], w.k.shape[1]
-    D = w.q.shape[2]
     q_rot, k_rot = qk_norm_rope_store(w.q, w.k, w.v, w.q_weight, w.k_weight, w.cos, w.sin, w.eps, w.k_cache,
                                       w.v_cache, w.block_tables, w.cu_seqlens)
     out = torch.empty_like(q_rot)
@@ -161,17 +316,15 @@ def bench_prefill(name, steps, warmup):
     def attn(i):
         flash_attn_varlen_func(q_rot, k_rot, w.v, w.cu_seqlens, w.cu_seqlens, w.max_seqlen, w.max_seqlen, True, out=out)
 
-    ev_ms, _ = time_region(attn, steps, warmup)
+    us = time_region(attn, steps, warmup)[0] * 1e3
     flops = W.prefill_flops(w.seq_lens, hq)
-    us = ev_ms * 1e3
 
     def norm_store(i):
         qk_norm_rope_store(w.q, w.k, w.v, w.q_weight, w.k_weight, w.cos, w.sin, w.eps, w.k_cache, w.v_cache,
                            w.block_tables, w.cu_seqlens)
 
     ns_us = time_region(norm_store, steps, warmup)[0] * 1e3
-    # read q, k, v, cos, sin, weights; write rotated q and k, and K/V into the cache
-    ns_bytes = 2 * T * D * (hq + 2 * hkv) + 2 * 2 * T * D + 2 * 2 * D + 2 * T * D * (hq + hkv) + 2 * 2 * T * hkv * D
+    ns_bytes = norm_store_bytes(T, hq, hkv)
 
     def block(i):
         qr, kr = qk_norm_rope_store(w.q, w.k, w.v, w.q_weight, w.k_weight, w.cos, w.sin, w.eps, w.k_cache,
@@ -180,23 +333,90 @@ def bench_prefill(name, steps, warmup):
 
     block_us = time_region(block, steps, warmup)[0] * 1e3
     return {
-        "workload": name,
-        "tokens": T,
-        "gflop": flops / 1e9,
-        "us_per_call": us,
-        "tflops": flops / (us * 1e-6) / 1e12,
+        "workload": name, "tokens": T, "gflop": flops / 1e9,
+        "us_per_call": us, "tflops": flops / (us * 1e-6) / 1e12,
         "pct_peak_mfma": 100.0 * flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
         "tokens_per_s": T / (us * 1e-6),
-        "norm_rope_store_us": ns_us,
-        "norm_rope_store_gbs": ns_bytes / (ns_us * 1e-6) / 1e9,
+        "roofline": {**_roof_mfma(flops, us), "kernel": "varlen_prefill_gqa"},
+        "norm_rope_store_us": ns_us, "norm_rope_store_gbs": ns_bytes / (ns_us * 1e-6) / 1e9,
+        "norm_rope_store_roofline": _roof_hbm(ns_bytes, ns_us),
         "block_us_per_call": block_us,
+    }, w
+
+
+def bench_mixed(name, steps, warmup, copies=3):
+    """The continuous-batching step on one shared pool, in scheduler order:
+    the prefill batch's fused norm/RoPE/store and varlen attention, then the
+    decode batch's norm/RoPE/store and paged attention, on one stream. Timed
+    as a whole step and launch by launch (each alone, on the same inputs)."""
+    from tinyserver_amd import workloads as W
+    from tinyserver_amd.kernels import flash_attn_varlen_func, paged_attention_forward, qk_norm_rope_store
+
+    dev = torch.device("cuda:0")
+    m = W.make(name, device=dev)
+    p, d = m.prefill, m.decode
+    pools = _decode_pools(d, copies)
+    B = len(d.ctx_lens)
+    cu_d = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    pos, seq_lens = d.positions.to(dev), d.ctx_lens.to(torch.int32).to(dev)
+    T, hq, hkv = p.q.shape[0], p.q.shape[1], p.k.shape[1]
+
+    def pre_store(i):
+        kc, vc = pools[i % copies]
+        return qk_norm_rope_store(p.q, p.k, p.v, p.q_weight, p.k_weight, p.cos, p.sin, p.eps, kc, vc,
+                                  p.block_tables, p.cu_seqlens)
+
+    def dec_store(i):
+        kc, vc = pools[i % copies]
+        return qk_norm_rope_store(d.q, d.k, d.v, d.q_weight, d.k_weight, d.cos, d.sin, d.eps, kc, vc,
+                                  d.block_tables, cu_d, pos, return_k=False)[0]
+
+    qp, kp = pre_store(0)
+    qd = dec_store(0)
+    out_p, out_d = torch.empty_like(qp), torch.empty_like(qd)
+
+    def pre_attn(i):
+        flash_attn_varlen_func(qp, kp, p.v, p.cu_seqlens, p.cu_seqlens, p.max_seqlen, p.max_seqlen, True, out=out_p)
+
+    def dec_attn(i):
+        kc, vc = pools[i % copies]
+        paged_attention_forward(qd, kc, vc, d.block_tables, W.PAGE, seq_lens, out=out_d)
+
+    def step(i):
+        kc, vc = pools[i % copies]
+        q1, k1 = pre_store(i)
+        flash_attn_varlen_func(q1, k1, p.v, p.cu_seqlens, p.cu_seqlens, p.max_seqlen, p.max_seqlen, True, out=out_p)
+        q2 = dec_store(i)
+        paged_attention_forward(q2, kc, vc, d.block_tables, W.PAGE, seq_lens, out=out_d)
+
+    step_us = time_region(step, steps, warmup)[0] * 1e3
+    t = {k: time_region(f, steps, warmup)[0] * 1e3
+         for k, f in (("prefill_norm_rope_store", pre_store), ("prefill_attention", pre_attn),
+                      ("decode_norm_rope_store", dec_store), ("decode_attention", dec_attn))}
+    flops = W.prefill_flops(p.seq_lens, hq)
+    dbytes = W.decode_bytes(d.ctx_lens, d.num_heads, d.num_kv_heads)
+    launches = {
+        "prefill_norm_rope_store": {"us": t["prefill_norm_rope_store"],
+                                    "roofline": _roof_hbm(norm_store_bytes(T, hq, hkv), t["prefill_norm_rope_store"])},
+        "prefill_attention": {"us": t["prefill_attention"], "roofline": _roof_mfma(flops, t["prefill_attention"])},
+        "decode_norm_rope_store": {"us": t["decode_norm_rope_store"],
+                                   "roofline": _roof_hbm(norm_store_bytes(B, hq, hkv), t["decode_norm_rope_store"])},
+        "decode_attention": {"us": t["decode_attention"], "roofline": _roof_hbm(dbytes, t["decode_attention"])},
     }
+    del pools
+    return {
+        "workload": name, "prefill_seqs": len(p.seq_lens), "prefill_tokens": T, "decode_batch": B,
+        "sum_ctx": int(d.ctx_lens.sum()), "pool_pages": int(m.k_cache.shape[0]),
+        "step_us": step_us, "sum_of_launches_us": sum(t.values()),
+        "tokens_per_s": (T + B) / (step_us * 1e-6), "launches": launches,
+        "order": "prefill norm/RoPE/store -> varlen attention -> decode norm/RoPE/store -> paged attention",
+    }, m
 
 
 def bench_sampling(steps, warmup, batch=64, vocab=151936):
     """sample_tokens over a Qwen3-vocab batch: bf16 logits (N(0, 2.5) plus a
-    few boosted tokens per row), temperature 0.8, top_k 50, top_p 0.9 (the
-    engine's usual settings), seeded uniforms. One launch per call."""
+    few boosted tokens per row), temperature 0.8, seeded uniforms; three
+    filter settings. One launch per call."""
     from tinyserver_amd.kernels import sample_tokens
 
     dev = torch.device("cuda:0")
@@ -210,53 +430,21 @@ def bench_sampling(steps, warmup, batch=64, vocab=151936):
     uniforms = torch.rand(batch, generator=g).to(dev)
     out = torch.empty(batch, dtype=torch.int64, device=dev)
     cases = {}
-    for label, k, p in (("topk50_topp0.9", 50, 0.9), ("topp0.9", 0, 0.9), ("full", 0, 1.0)):
+    nbytes = batch * vocab * 2
+    for label, k, pp in (("topk50_topp0.9", 50, 0.9), ("topp0.9", 0, 0.9), ("full", 0, 1.0)):
         top_k.fill_(k)
-        top_p.fill_(p)
+        top_p.fill_(pp)
 
         def call(i):
             sample_tokens(logits, temperature, top_k, top_p, uniforms, out=out)
 
         us = time_region(call, steps, warmup)[0] * 1e3
-        cases[label] = {"us_per_call": us, "logits_gbs": batch * vocab * 2 / (us * 1e-6) / 1e9}
-    return {"workload": f"sample_tokens bs{batch} vocab{vocab} bf16", "batch": batch, "vocab": vocab, **cases}
-
-
-def cpu_baseline(w, target_seconds=10.0, max_reps=50):
-    """The reference's CPU decode path (gather loop + repeat_interleave + SDPA) on
-    the whole batch, timed on this host: repeated for about `target_seconds` of
-    CPU work, the median run reported."""
-    from oracle import paged as op
-    from tinyserver_amd import workloads as W
-
-    n = len(w.ctx_lens)
-    pages = sorted({p for lst in w.block_lists[:n] for p in lst})
-    remap = {p: i for i, p in enumerate(pages)}
-    idx = torch.tensor(pages, device=w.k_cache.device)
-    kc, vc = w.k_cache[idx].cpu(), w.v_cache[idx].cpu()
-    tables = [[remap[p] for p in lst] for lst in w.block_lists[:n]]
-    q = w.q[:n].cpu().transpose(0, 1).unsqueeze(0).contiguous()  # (1, Hq, n, D)
-    positions = [int(x) - 1 for x in w.ctx_lens[:n]]
-    times = []
-    t_start = time.perf_counter()
-    while not times or (time.perf_counter() - t_start < target_seconds and len(times) < max_reps):
-        t0 = time.perf_counter()
-        op.decode_cpu_path(q, kc, vc, tables, positions, literal_gather=True)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    nbytes = W.decode_bytes(w.ctx_lens[:n], w.num_heads, w.num_kv_heads)
-    return {
-        "value": nbytes / t / 1e12,
-        "unit": "TB/s",
-        "cores": torch.get_num_threads(),
-        "host_cpus": os.cpu_count(),
-        "kind": "port",
-        "sample": f"reference CPU decode path (per-token gather loop + repeat_interleave + SDPA) on all {n} "
-                  f"sequences ({int(w.ctx_lens[:n].sum())} context tokens), median of {len(times)} runs "
-                  f"({sum(times):.1f} s of CPU work)",
-        "sample_seconds": t,
-        "us_per_layer": t * 1e6,
-    }
+        cases[label] = {"us_per_call": us, "logits_gbs": nbytes / (us * 1e-6) / 1e9,
+                        "roofline": {**_roof_hbm(nbytes, us), "kernel": "sample_tokens_kernel"}}
+    top_k.fill_(50)
+    top_p.fill_(0.9)
+    return {"workload": f"sample_tokens bs{batch} vocab{vocab} bf16", "batch": batch, "vocab": vocab, **cases}, \
+        (logits, temperature, top_k, top_p, uniforms)
 
 
 def copy_probe(nbytes=1 << 30, reps=5):
@@ -280,8 +468,69 @@ def measured_traffic():
 
 
 def _round(d):
-    return {k: (round(v, 3) if isinstance(v, float) else _round(v) if isinstance(v, dict) else v)
-            for k, v in d.items()}
+    if isinstance(d, dict):
+        return {k: _round(v) for k, v in d.items()}
+    if isinstance(d, float):
+        return round(d, 3)
+    return d
+
+
+def _free():
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def secondaries(steps, warmup, cpu, cpu_s):
+    """Every secondary workload, each with its CPU baselines (cpu=True)."""
+    sec = {}
+    # the reference's CPU-runnable decode case
+    s, w = bench_decode("qwen3-0.6b-decode-bs4", steps, warmup, with_block=True)
+    if cpu:
+        s["cpu_baseline"] = {"literal": cpu_decode_baseline(w, True, cpu_s),
+                             "vectorized": cpu_decode_baseline(w, False, cpu_s)}
+    sec["qwen3-0.6b-decode-bs4"] = _round(s)
+    del w
+    _free()
+    # 32k-context decode (one pool copy: 4.3 GB, far past the MALL)
+    s, w = bench_decode("qwen3-32b-decode-bs32", steps, min(warmup, 3), copies=1)
+    if cpu:
+        s["cpu_baseline"] = {"literal": cpu_decode_baseline(w, True, cpu_s),
+                             "vectorized": cpu_decode_baseline(w, False, cpu_s)}
+    sec["qwen3-32b-decode-bs32"] = _round(s)
+    del w
+    _free()
+    # varlen prefill
+    s, w = bench_prefill("qwen3-8b-prefill-16seq", steps, min(warmup, 3))
+    if cpu:
+        s["cpu_baseline"] = {
+            "literal": {"skipped": "the block-diagonal mask over 17,794 packed tokens is a dense 17,794^2 matrix "
+                                   "(606 MB in bf16) and its SDPA scores every pair: not a bounded sample"},
+            "vectorized": cpu_prefill_baseline(w, False, cpu_s)}
+    sec["qwen3-8b-prefill-16seq"] = _round(s)
+    del w
+    _free()
+    # the continuous-batching step on one shared pool
+    s, m = bench_mixed("qwen3-4b-mixed", steps, min(warmup, 3))
+    if cpu:
+        s["cpu_baseline"] = {
+            "prefill": {"literal": cpu_prefill_baseline(m.prefill, True, cpu_s),
+                        "vectorized": cpu_prefill_baseline(m.prefill, False, cpu_s)},
+            "decode": {"literal": cpu_decode_baseline(m.decode, True, cpu_s),
+                       "vectorized": cpu_decode_baseline(m.decode, False, cpu_s)}}
+    sec["qwen3-4b-mixed"] = _round(s)
+    del m
+    _free()
+    # the headline batch on the server's default 256-token pages
+    s, w = bench_decode(HEADLINE, steps, min(warmup, 3), with_block=True, page=256)
+    sec["qwen3-8b-decode-bs64-page256"] = _round(s)
+    del w
+    _free()
+    # batched sampling
+    s, args = bench_sampling(steps, min(warmup, 3))
+    if cpu:
+        s["cpu_baseline"] = cpu_sampling_baseline(*args, cpu_s)
+    sec["sampling-qwen3-vocab-bs64"] = _round(s)
+    return sec
 
 
 def main():
@@ -292,8 +541,10 @@ def main():
     ap.add_argument("--num-workgroups", type=int, default=0)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU work per secondary CPU baseline")
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--workload", default=None, help="run one workload of tinyserver_amd.workloads alone")
+    ap.add_argument("--page", type=int, default=None, help="page size for --workload (decode workloads)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -307,15 +558,20 @@ def main():
         copy_probe()
         return
     from tinyserver_amd import _lib
+    from tinyserver_amd import workloads as W
 
     _lib.load()
     if args.workload:
+        kind = W.WORKLOADS[args.workload][0] if args.workload in W.WORKLOADS else None
         if args.workload == "sampling-qwen3-vocab-bs64":
-            res = bench_sampling(args.steps, args.warmup)
-        elif "prefill" in args.workload:
-            res = bench_prefill(args.workload, args.steps, args.warmup)
+            res, _ = bench_sampling(args.steps, args.warmup)
+        elif kind == "prefill":
+            res, _ = bench_prefill(args.workload, args.steps, args.warmup)
+        elif kind == "mixed":
+            res, _ = bench_mixed(args.workload, args.steps, args.warmup)
         else:
-            res, _ = bench_decode(args.workload, args.steps, args.warmup, args.num_workgroups)
+            kw = {"page": args.page} if args.page else {}
+            res, _ = bench_decode(args.workload, args.steps, args.warmup, args.num_workgroups, with_block=True, **kw)
         print(json.dumps({"workload": args.workload, "steps": args.steps, "warmup": args.warmup, **_round(res)}),
               flush=True)
         return
@@ -350,6 +606,7 @@ def main():
         "us_per_layer_p10_p90": [round(head["us_per_call_p10"], 2), round(head["us_per_call_p90"], 2)],
         "pct_peak_hbm": round(head["pct_peak_hbm"], 2),
         "tokens_per_s": round(head["tokens_per_s"], 1),
+        "decode_norm_rope_store_us": round(head["norm_rope_store_us"], 2),
         "decode_block_us_per_layer": round(head["block_us_per_call"], 2),
         "decode_block_fused_us_per_layer": round(head["block_fused_us_per_call"], 2),
         "roofline": {
@@ -365,24 +622,12 @@ def main():
         },
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(w)
+        lit = cpu_decode_baseline(w, True, 10.0)
+        line["cpu_baseline"] = {**lit, "vectorized": cpu_decode_baseline(w, False, 5.0)}
     del w
-    torch.cuda.empty_cache()
+    _free()
     if not args.no_secondary:
-        sec = {}
-        n2 = max(10, args.steps // 5)
-        s, w2 = bench_decode("qwen3-32b-decode-bs32", n2, 3, copies=1)
-        del w2
-        torch.cuda.empty_cache()
-        sec["qwen3-32b-decode-bs32"] = _round(s)
-        s, w2 = bench_decode("qwen3-4b-mixed-decode", n2, 3)
-        del w2
-        torch.cuda.empty_cache()
-        sec["qwen3-4b-mixed-decode"] = _round(s)
-        for name in ("qwen3-8b-prefill-16seq", "qwen3-4b-mixed-prefill"):
-            sec[name] = _round(bench_prefill(name, n2, 3))
-        sec["sampling-qwen3-vocab-bs64"] = _round(bench_sampling(n2, 3))
-        line["secondary"] = sec
+        line["secondary"] = secondaries(max(10, args.steps // 5), 3, not args.no_cpu_baseline, args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
 

@@ -178,6 +178,9 @@ def test_varlen_block_mask_sdpa_agrees():
     sdpa = ov.prefill_sdpa_block_mask(q.transpose(0, 1)[None], k.transpose(0, 1)[None], v.transpose(0, 1)[None],
                                       lens, 128)
     assert (out.reshape(1, sum(lens), -1) - sdpa).abs().max() < 1e-5
+    per_seq = ov.prefill_sdpa_per_sequence(q, k, v, cu)  # the vectorised CPU baseline
+    assert (out - per_seq).abs().max() < 1e-5
+    assert torch.equal(per_seq.reshape(1, sum(lens), -1), sdpa) or (per_seq.reshape(1, sum(lens), -1) - sdpa).abs().max() < 1e-6
 
 
 def test_varlen_special_cases():
