@@ -34,8 +34,10 @@
 // * fp32 online softmax in the log2 domain (scale pre-multiplied by log2 e,
 //   v_exp_f32), the running max shared across the 4 lanes of a head by two
 //   cross-lane exchanges; the accumulator is rescaled only when a head's max
-//   grows, which a wave-uniform branch detects. P is rounded to the cache
-//   dtype to feed the MFMA (the reference's P.V is fp32); l sums the fp32 p.
+//   grows, which a wave-uniform branch detects. The reference's P.V is fp32
+//   (paged_attention.py:107-112): P goes to the MFMA as two cache-dtype
+//   halves, hi + lo, so the weights keep 16 (bf16) or 22 (f16) significant
+//   bits; l sums the fp32 p.
 // * Each wave keeps a ring of RING tiles in registers: the loads of the next
 //   RING-1 tiles are in flight while one is on the matrix cores. Loads are
 //   unconditional (past its last tile a wave reloads that tile, which hits
@@ -441,7 +443,14 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
       p[r] = m == kNegInf ? 0.f : fast_exp2(sv[r] - m);
       l += p[r];
     }
-    const u32x2 pop = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
+    // P.V with fp32-grade P, as the reference's fp32 p times V: p = hi + lo
+    // with hi = p rounded to the cache dtype and lo = (p - hi) rounded, two
+    // MFMAs per output block (hi + lo carries 16 significant bits for bf16,
+    // 22 for f16; V is exact in either). The matrix cores have the slack:
+    // this kernel streams memory.
+    const u32x2 phi = u32x2{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
+    const u32x2 plo = u32x2{pack2<T>(p[0] - lo_f<T>(phi[0]), p[1] - hi_f<T>(phi[0])),
+                            pack2<T>(p[2] - lo_f<T>(phi[1]), p[3] - hi_f<T>(phi[1]))};
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int wd = u >> 1;
@@ -453,7 +462,8 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
         bop[0] = pack_lo(vo[0][wd], vo[1][wd]);
         bop[1] = pack_lo(vo[2][wd], vo[3][wd]);
       }
-      acc[u] = mfma_k16<T>(pop, bop, acc[u]);  // acc[u][r] = O[head 4g + r][dim 8c + u]
+      acc[u] = mfma_k16<T>(phi, bop, acc[u]);  // acc[u][r] = O[head 4g + r][dim 8c + u]
+      acc[u] = mfma_k16<T>(plo, bop, acc[u]);
     }
   };
 
