@@ -5,7 +5,8 @@
  * point takes plain views of caller-owned device memory plus a HIP stream
  * (passed as void*, so no HIP header is needed to bind it) and returns an int
  * status. The library never allocates device memory: outputs and the decode
- * workspace are passed in by the caller. Launches are asynchronous on the
+ * workspace are passed in by the caller (tsa_paged_decode_noalloc uses a
+ * fixed array the library's code object holds instead). Launches are asynchronous on the
  * given stream; nothing synchronises.
  *
  * Status codes: TSA_OK (0); TSA_ERR_INVALID (-1) for an argument that the
@@ -26,6 +27,8 @@
  *   tsa_qk_norm_rope_store  the same, fused with tsa_store_kv_paged
  *   tsa_paged_decode        server/model/kernels/paged_attention.py:124-192
  *                           (paged_attention_forward)
+ *   tsa_paged_decode_noalloc  no counterpart: tsa_paged_decode with library-held
+ *                           scratch, for callers that cannot allocate
  *   tsa_paged_decode_step   the decode call site (qwen3.py:268-287, 335-409):
  *                           norm/RoPE, store and paged attention, fused
  *   tsa_varlen_prefill      server/model/kernels/varlen_attention.py:145-218
@@ -146,6 +149,20 @@ int tsa_paged_decode(const tsa_view* out, const tsa_view* query, const tsa_view*
                      const tsa_view* seq_lens, double softmax_scale, void* workspace,
                      size_t workspace_bytes, int32_t num_workgroups, void* stream);
 
+/* tsa_paged_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). It has no counterpart in the reference.
+ * Same arguments, kernels and results as tsa_paged_decode; the partials and
+ * tile prefix live in a 16 MiB array the library holds on each GPU it runs on
+ * until the process ends, so it allocates nothing. A call whose workspace
+ * (tsa_paged_decode_workspace_bytes) would exceed 16 MiB is rejected with
+ * TSA_ERR_INVALID before any device work. All calls on one GPU share that
+ * GPU's array: calls ordered on one stream are fine; calls that overlap on
+ * one GPU (concurrent streams, threads) race and must not be issued. */
+int tsa_paged_decode_noalloc(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache,
+                             const tsa_view* v_cache, const tsa_view* block_tables,
+                             const tsa_view* seq_lens, double softmax_scale, int32_t num_workgroups,
+                             void* stream);
 /* The decode step of the Qwen3 call site, fused (qwen3.py:268-287 norm and
  * RoPE of q and of the new k, :335-357 the store of the new token's k and v,
  * :359-409 paged_attention_forward), in the two launches of tsa_paged_decode:

@@ -108,6 +108,19 @@ def test_decode_validation():
     assert rc == _lib.TSA_ERR_INVALID and "2^31" in msg
 
 
+def test_noalloc_rejects_oversized_before_device_work():
+    """tsa_paged_decode_noalloc refuses a call whose partials exceed the 16 MiB
+    per-GPU scratch, from the shapes alone (no device is touched)."""
+    q = _v((8192, 64, 128))
+    kc = _v((4, 8, 16, 128))
+    bt = _v((8192, 1), torch.int32)
+    sl = _v((8192,), torch.int32)
+    rc, msg = _call("tsa_paged_decode_noalloc", R(q), R(q), R(kc), R(kc), R(bt), R(sl), 0.1, 0, None)
+    assert rc == _lib.TSA_ERR_INVALID and "bytes of scratch" in msg and "16777216" in msg
+    need = _lib.load().tsa_paged_decode_workspace_bytes(8192, 64, 8, 128, 1, 16, 0)
+    assert str(need) in msg
+
+
 def test_prefill_validation():
     q, k = _v((10, 6, 64)), _v((10, 4, 64))
     cu = _v((3,), torch.int32)

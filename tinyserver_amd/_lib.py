@@ -55,6 +55,7 @@ SIGNATURES = {
         c_int,
         [_V, _V, _V, _V, _V, _V, c_double, c_void_p, c_size_t, c_int32, c_void_p],
     ),
+    "tsa_paged_decode_noalloc": (c_int, [_V, _V, _V, _V, _V, _V, c_double, c_int32, c_void_p]),
     "tsa_paged_decode_step": (
         c_int,
         [_V] * 8 + [c_double] + [_V] * 4 + [c_double, c_void_p, c_size_t, c_int32, c_void_p],

@@ -55,7 +55,9 @@
 // A generic kernel (one wave per (sequence, q-head), fp32 VALU math) covers
 // what the MFMA path does not: fp32 caches, head_dim other than 64/128, GQA
 // groups over 16, non-unit innermost strides.
+#include <atomic>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 #include "tsa_common.h"
@@ -846,7 +848,8 @@ namespace tsa {
 // stream kernel serves the call).
 static int prepare_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache, const tsa_view* v_cache,
                           const tsa_view* block_tables, const tsa_view* seq_lens, double softmax_scale, void* workspace,
-                          size_t workspace_bytes, int32_t num_workgroups, DecodeArgs& a, bool& mfma) {
+                          size_t workspace_bytes, int32_t num_workgroups, DecodeArgs& a, bool& mfma,
+                          const char* workspace_name = "workspace") {
   TSA_REQUIRE(view_ok(query, 3), "query must be a 3D tensor (num_seqs, num_heads, head_dim)");
   TSA_REQUIRE(view_ok(out, 3), "out must be a 3D tensor shaped like query");
   TSA_REQUIRE(view_ok(k_cache, 4) && view_ok(v_cache, 4),
@@ -899,8 +902,8 @@ static int prepare_decode(const tsa_view* out, const tsa_view* query, const tsa_
     a.W = plan.W;
     a.NW = kWaves * plan.W;
     TSA_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total,
-                "workspace of %zu bytes is too small: %zu needed", workspace_bytes, plan.total);
-    TSA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "workspace must be 256-byte aligned");
+                "%s of %zu bytes is too small: %zu needed", workspace_name, workspace_bytes, plan.total);
+    TSA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "%s must be 256-byte aligned", workspace_name);
     char* ws = static_cast<char*>(workspace);
     a.part = reinterpret_cast<float*>(ws);
     a.pref_out = reinterpret_cast<int32_t*>(ws + plan.part_bytes);
@@ -972,4 +975,97 @@ extern "C" int tsa_paged_decode_step(const tsa_view* out, const tsa_view* query,
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dt == TSA_BF16) return launch_decode<bf16_t>(a, true, st, true);
   return launch_decode<f16_t>(a, true, st, true);
+}
+
+// ---------------------------------------------------------------------------
+// tsa_paged_decode_noalloc: tsa_paged_decode for callers that cannot allocate
+// (code under HIP graph capture, tight serving loops, harnesses that forbid
+// hipMalloc). The same kernels take their partials and tile prefix from a
+// file-scope device array instead of a caller workspace. Each GPU the
+// library runs on holds its own copy of the array until the process ends;
+// every call on a GPU shares it and leaves the last call's contents, which
+// is harmless here -- every partial slot a merge reads is written by the
+// stream launch of the same call, and the prefix too, so nothing needs
+// clearing. Two calls that overlap on one GPU (on different streams, say)
+// race on it; calls ordered on one stream do not.
+namespace tsa {
+
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;  // 16 MiB per GPU
+// In host code this name is a host-side stand-in: kernels get the address
+// from hipGetSymbolAddress (noalloc_scratch), never the name itself.
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// This GPU's scratch address: looked up once per device, on the first call
+// there, with that device current (each GPU holds its copy at its own
+// address), then read from the per-device cache.
+static int noalloc_scratch(hipStream_t stream, void** ptr) {
+  int dev = 0;
+  const hipError_t e0 = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e0 != hipSuccess) {
+    set_error("tsa_paged_decode_noalloc: cannot find the stream's device: %s", hipGetErrorString(e0));
+    return TSA_ERR_LAUNCH;
+  }
+  TSA_REQUIRE(dev >= 0 && dev < kMaxDevices, "tsa_paged_decode_noalloc: device %d beyond the %d supported", dev,
+              kMaxDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      int cur = -1;
+      hipError_t e = hipGetDevice(&cur);
+      if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+      if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (cur >= 0 && cur != dev) {
+        const hipError_t er = hipSetDevice(cur);
+        if (e == hipSuccess) e = er;
+      }
+      if (e != hipSuccess || p == nullptr) {
+        set_error("tsa_paged_decode_noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+        return TSA_ERR_LAUNCH;
+      }
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return TSA_OK;
+}
+
+}  // namespace tsa
+
+extern "C" int tsa_paged_decode_noalloc(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache,
+                                        const tsa_view* v_cache, const tsa_view* block_tables,
+                                        const tsa_view* seq_lens, double softmax_scale, int32_t num_workgroups,
+                                        void* stream) {
+  // The size limit first, before any device work: the scratch a call needs
+  // is the workspace tsa_paged_decode would take.
+  if (view_ok(query, 3) && view_ok(k_cache, 4) && k_cache->size[1] > 0 && query->size[1] % k_cache->size[1] == 0 &&
+      num_workgroups >= 0 && query->size[0] > 0 && query->size[1] > 0) {
+    const size_t need =
+        make_plan(query->size[0], query->size[1], k_cache->size[1], query->size[2], num_workgroups).total;
+    TSA_REQUIRE(need <= kNoAllocScratchBytes,
+                "tsa_paged_decode_noalloc: this call needs %zu bytes of scratch, beyond the %zu bytes the library "
+                "holds per GPU; use tsa_paged_decode with a caller workspace",
+                need, kNoAllocScratchBytes);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if (int rc = noalloc_scratch(st, &ws)) return rc;
+  DecodeArgs a;
+  bool mfma = false;
+  if (int rc = prepare_decode(out, query, k_cache, v_cache, block_tables, seq_lens, softmax_scale, ws,
+                              kNoAllocScratchBytes, num_workgroups, a, mfma, "the no-allocation scratch"))
+    return rc;
+  switch (query->dtype) {
+    case TSA_BF16: return launch_decode<bf16_t>(a, mfma, st);
+    case TSA_F16: return launch_decode<f16_t>(a, mfma, st);
+    case TSA_F32: return launch_decode<float>(a, false, st);
+  }
+  set_error("unsupported dtype");
+  return TSA_ERR_UNSUPPORTED;
 }
