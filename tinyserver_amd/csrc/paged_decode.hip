@@ -39,9 +39,11 @@
 //   halves, hi + lo, so the weights keep 16 (bf16) or 22 (f16) significant
 //   bits; l sums the fp32 p.
 // * Each wave keeps a ring of RING tiles in registers: the loads of the next
-//   RING-1 tiles are in flight while one is on the matrix cores. Loads are
-//   unconditional (past its last tile a wave reloads that tile, which hits
-//   the cache) so the compiler waits for exactly one tile.
+//   RING-1 tiles are in flight while one is on the matrix cores. K/V loads
+//   are unconditional (past its last tile a wave reloads that tile, which
+//   hits the cache) so the compiler waits for exactly one tile. A unit's Q
+//   operand is loaded once, with the unit's first tile (or the wave's first,
+//   when its run starts inside the unit), and kept in registers.
 // * A second kernel merges, per unit, the partials of the wave workers whose
 //   runs cover it with a log-sum-exp reduce. The kernel boundary orders the
 //   two, so no cache flushes or atomics are needed; no host sync, no memset.
@@ -178,13 +180,16 @@ constexpr int kStateOff = 1024 + RING * kUnitBytes;
 constexpr int kFusedWaveBytes = kStateOff + 128;
 static_assert(sizeof(FusedState) <= 128, "fused state exceeds its LDS slot");
 
-// K/V are read exactly once per call. Non-temporal loads (the streaming
-// hint) reach about 6.8 TB/s on this chip against about 6.0 for ordinary
-// ones, but a short run pays for them: a wave whose run has fewer than
-// kStreamNtMin tiles uses ordinary loads. Q, reread for every tile of a unit,
-// always uses ordinary loads.
+// K/V are read exactly once per call, with non-temporal loads (the
+// streaming hint). A gather of the same 4 KB pages with the same static
+// split and no arithmetic moves the Qwen3-8B batch-64 pool in about 97 us
+// with them and 111 us without. They pay only because Q is not in the
+// stream: loaded once per unit (not per tile, an ordinary-load L2 read of
+// half the K/V bytes again), the non-temporal K/V stream takes this kernel
+// from 127 to 114 us on the same box; with the per-tile Q reads it took 124.
+// A wave whose run has fewer than kStreamNtMin tiles uses ordinary loads.
 #ifndef TSA_DECODE_NT_MIN_TILES
-#define TSA_DECODE_NT_MIN_TILES 128
+#define TSA_DECODE_NT_MIN_TILES 0
 #endif
 constexpr int kStreamNtMin = TSA_DECODE_NT_MIN_TILES;
 template <bool NT, typename T>
@@ -258,9 +263,9 @@ struct TileCursor {
 
 // Wave worker v = 4 * workgroup + wave streams the contiguous tiles
 // [v * share, (v + 1) * share) of the global list, crossing unit boundaries
-// without stopping: its ring of RING tiles (K operand, V rows and the unit's
-// Q operand, all loaded together) keeps prefetching into the next unit while
-// the current one finishes. At the end of each of its units the wave writes
+// without stopping: its ring of RING tiles (K operand and V rows, plus the
+// unit's Q operand at a unit's first tile) keeps prefetching into the next
+// unit while the current one finishes. At the end of each of its units the wave writes
 // its partial (m, l, acc) to workspace slot unit + v (injective, since a
 // worker's units form a range that starts where the previous worker's ended)
 // and starts afresh; nothing waits for the other waves. The merge kernel
@@ -352,13 +357,18 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   // With 16-token pages the loads are unconditional (an invalid page id reads
   // page 0 and the tile is masked in compute), so nothing waits on the data
   // until it is consumed.
-  auto load_tile = [&](const TileCursor& tc, u32x4 (&qo)[KJ], u32x4 (&ko)[KJ], u32x4 (&vo)[4], auto nt) {
+  auto load_tile = [&](const TileCursor& tc, u32x4 (&qo)[KJ], u32x4 (&ko)[KJ], u32x4 (&vo)[4], auto nt, bool first) {
     constexpr bool NT = decltype(nt)::value;
     const int32_t* bt_row = a.bt + tc.s * a.bt_s0;
     if constexpr (!FUSED) {  // (fused: Q is made once per unit, from LDS)
-      const T* qrow = static_cast<const T*>(a.q) + tc.s * a.q_ss + (tc.kvh * G + cq) * a.q_sh + 8 * g;
+      // The unit's Q operand, once per unit: at its first tile, or at the
+      // wave's first tile when its run starts inside the unit. Issued ahead
+      // of the tile's K/V, so the wait for those covers it.
+      if (tc.t == 0 || first) {
+        const T* qrow = static_cast<const T*>(a.q) + tc.s * a.q_ss + (tc.kvh * G + cq) * a.q_sh + 8 * g;
 #pragma unroll
-      for (int j = 0; j < KJ; ++j) qo[j] = *reinterpret_cast<const u32x4*>(qrow + 32 * j);
+        for (int j = 0; j < KJ; ++j) qo[j] = *reinterpret_cast<const u32x4*>(qrow + 32 * j);
+      }
     }
     const T* kbase = static_cast<const T*>(a.kc) + tc.kvh * a.kc_h;
     const T* vbase = static_cast<const T*>(a.vc) + tc.kvh * a.vc_h;
@@ -507,7 +517,7 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
   // operand. new_token: in the unit's last tile, the new token's rotated K
   // and raw V replace the cache rows that do not hold them yet, and are
   // stored to the cache after the tile.
-  u32x4 qn[KJ];  // the current unit's Q operand (fused)
+  u32x4 qn[KJ];  // the current unit's Q operand
   auto unit_dma = [&](const TileCursor& tc, int ub) __attribute__((always_inline)) {
     const FusedState fs = *reinterpret_cast<const FusedState*>(fbuf + kStateOff);
     const uint32_t base = fbuf_lds + 1024 + ub * kUnitBytes;
@@ -582,7 +592,7 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
     if constexpr (FUSED) unit_dma(ld, 0);
 #pragma unroll
     for (int d = 0; d < RING; ++d) {
-      load_tile(ld, qbuf[d], kbuf[d], vbuf[d], nt);
+      load_tile(ld, qbuf[d], kbuf[d], vbuf[d], nt, d == 0);
       advance_load();
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -609,13 +619,17 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
               compute_tile(cur, qn, kbuf[d], vbuf[d]);
             }
           } else {
-            compute_tile(cur, qbuf[d], kbuf[d], vbuf[d]);
+            if (cur.t == 0 || i + d == 0) {  // a unit starts: its Q arrived with this tile
+#pragma unroll
+              for (int j = 0; j < KJ; ++j) qn[j] = qbuf[d][j];
+            }
+            compute_tile(cur, qn, kbuf[d], vbuf[d]);
           }
           if (cur.t + 1 == cur.n || i + d + 1 == n_tiles) flush(cur);
           cur.advance(pref, a.B, Hkv);
         }
         __builtin_amdgcn_sched_barrier(0);
-        load_tile(ld, qbuf[d], kbuf[d], vbuf[d], nt);
+        load_tile(ld, qbuf[d], kbuf[d], vbuf[d], nt, false);
         advance_load();
         __builtin_amdgcn_sched_barrier(0);
       }
