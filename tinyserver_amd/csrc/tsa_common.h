@@ -213,11 +213,32 @@ __device__ __forceinline__ void lds_barrier() {
 //
 // dma16: a per-lane 64-bit address. dma16_sv: a wave-uniform base plus a
 // 32-bit lane offset (half the address registers).
+//
+// Hazard: a VMEM instruction that reads an SGPR written by a VALU
+// instruction (v_readfirstlane_b32, v_readlane_b32, v_cmp ...) needs 5 wait
+// states in between. The compiler pads that for its own instructions, not
+// for the SGPR inputs of an asm statement. dma16_sv takes its base as the
+// compiler computed it, which must be SALU work in SGPRs (the kernels' bases
+// derive from kernel arguments and readfirstlane'd indices);
+// tests/test_dma_hazards.py checks every DMA site of the built kernels for
+// this. dma16_su is for a wave-uniform base the compiler may hold in VGPRs:
+// it moves it to SGPRs itself and waits the 5 states.
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma16_su(const void* ubase, uint32_t voff, uint32_t lds) {
+  // readfirstlane returns int: each half goes through uint32_t so that the
+  // low half is zero-extended, not sign-extended, into the 64-bit address.
+  const uint64_t p = reinterpret_cast<uint64_t>(ubase);
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(p >> 32))));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(p))));
+  const uint64_t su = (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo);
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(reinterpret_cast<const void*>(su)),
+               "{m0}"(lds)
+               : "memory");
 }
 
 // Wait until at most N of this wave's vector memory operations are in
