@@ -348,9 +348,11 @@ def bench_mixed(name, steps, warmup, copies=3):
     """The continuous-batching step on one shared pool, in scheduler order:
     the prefill batch's fused norm/RoPE/store and varlen attention, then the
     decode batch's norm/RoPE/store and paged attention, on one stream. Timed
-    as a whole step and launch by launch (each alone, on the same inputs)."""
+    as a whole step and launch by launch (each alone, on the same inputs);
+    and as the step with both attention calls in one launch (mixed_step)."""
     from tinyserver_amd import workloads as W
-    from tinyserver_amd.kernels import flash_attn_varlen_func, paged_attention_forward, qk_norm_rope_store
+    from tinyserver_amd.kernels import (flash_attn_varlen_func, mixed_step, paged_attention_forward, paged_decode_step,
+                                        qk_norm_rope_store)
 
     dev = torch.device("cuda:0")
     m = W.make(name, device=dev)
@@ -389,10 +391,32 @@ def bench_mixed(name, steps, warmup, copies=3):
         q2 = dec_store(i)
         paged_attention_forward(q2, kc, vc, d.block_tables, W.PAGE, seq_lens, out=out_d)
 
+    # The same step with the two attention calls in one launch: the prefill
+    # store, then mixed_step (prefill attention + the fused decode step in one
+    # kernel, + the decode merge).
+    def one_attn(i):
+        kc, vc = pools[i % copies]
+        mixed_step(qp, kp, p.v, p.cu_seqlens, p.max_seqlen, d.q, d.k, d.v, d.q_weight, d.k_weight, d.cos, d.sin,
+                   d.eps, kc, vc, d.block_tables, seq_lens, prefill_out=out_p, out=out_d)
+
+    def dec_step(i):
+        kc, vc = pools[i % copies]
+        paged_decode_step(d.q, d.k, d.v, d.q_weight, d.k_weight, d.cos, d.sin, d.eps, kc, vc, d.block_tables,
+                          seq_lens, out=out_d)
+
+    def step_one(i):
+        kc, vc = pools[i % copies]
+        q1, k1 = pre_store(i)
+        mixed_step(q1, k1, p.v, p.cu_seqlens, p.max_seqlen, d.q, d.k, d.v, d.q_weight, d.k_weight, d.cos, d.sin,
+                   d.eps, kc, vc, d.block_tables, seq_lens, prefill_out=out_p, out=out_d)
+
     step_us = time_region(step, steps, warmup)[0] * 1e3
+    step_one_us = time_region(step_one, steps, warmup)[0] * 1e3
     t = {k: time_region(f, steps, warmup)[0] * 1e3
          for k, f in (("prefill_norm_rope_store", pre_store), ("prefill_attention", pre_attn),
                       ("decode_norm_rope_store", dec_store), ("decode_attention", dec_attn))}
+    t_one = {k: time_region(f, steps, warmup)[0] * 1e3 for k, f in (("decode_step", dec_step),
+                                                                   ("mixed_attention", one_attn))}
     flops = W.prefill_flops(p.seq_lens, hq)
     dbytes = W.decode_bytes(d.ctx_lens, d.num_heads, d.num_kv_heads)
     launches = {
@@ -410,6 +434,16 @@ def bench_mixed(name, steps, warmup, copies=3):
         "step_us": step_us, "sum_of_launches_us": sum(t.values()),
         "tokens_per_s": (T + B) / (step_us * 1e-6), "launches": launches,
         "order": "prefill norm/RoPE/store -> varlen attention -> decode norm/RoPE/store -> paged attention",
+        "one_launch": {
+            "step_us": step_one_us, "tokens_per_s": (T + B) / (step_one_us * 1e-6),
+            "order": "prefill norm/RoPE/store -> mixed_step (varlen attention + fused decode step in one kernel, "
+                     "+ the decode merge)",
+            "mixed_attention_us": t_one["mixed_attention"],
+            "separate": {"prefill_attention_us": t["prefill_attention"], "decode_step_us": t_one["decode_step"],
+                         "sum_us": t["prefill_attention"] + t_one["decode_step"]},
+            "roofline": {"decode_hbm": _roof_hbm(dbytes, t_one["mixed_attention"]),
+                         "prefill_mfma": _roof_mfma(flops, t_one["mixed_attention"])},
+        },
     }, m
 
 

@@ -128,6 +128,34 @@ def test_prefill_validation():
     assert rc == _lib.TSA_ERR_INVALID and "divisible" in msg
 
 
+def test_mixed_step_validation():
+    """tsa_mixed_step checks both halves' arguments, as the two calls it
+    replaces do, before any device work."""
+    pq, pk = _v((10, 8, 128)), _v((10, 2, 128))
+    cu = _v((3,), torch.int32)
+    q, kn = _v((4, 8, 128)), _v((4, 2, 128))
+    w, cs = _v((128,)), _v((4, 128))
+    kc = _v((10, 2, 16, 128))
+    bt, sl = _v((4, 2), torch.int32), _v((4,), torch.int32)
+    lib = _lib.load()
+    ws_bytes = lib.tsa_paged_decode_workspace_bytes(4, 8, 2, 128, 2, 16, 0)
+    ws = 1 << 20  # a fake, 256-byte aligned address: never dereferenced
+
+    def call(p_k=pk, query=q, ws_ptr=ws, pwg=0):
+        return _call("tsa_mixed_step", R(pq), R(pq), R(p_k), R(p_k), R(cu), 9, 0.1, R(query), R(query), R(kn),
+                     R(kn), R(w), R(w), R(cs), R(cs), 1e-6, R(kc), R(kc), R(bt), R(sl), 0.1, ws_ptr, ws_bytes, 0, pwg,
+                     None)
+
+    rc, msg = call(p_k=_v((10, 3, 128)))
+    assert rc == _lib.TSA_ERR_INVALID and "divisible" in msg
+    rc, msg = call(query=_v((4, 7, 128)))
+    assert rc == _lib.TSA_ERR_INVALID and "multiple" in msg
+    rc, msg = call(ws_ptr=None)
+    assert rc == _lib.TSA_ERR_INVALID and "workspace" in msg
+    rc, msg = call(pwg=-1)
+    assert rc == _lib.TSA_ERR_INVALID and "prefill_workgroups" in msg
+
+
 def test_norm_rope_validation():
     q, k = _v((5, 4, 128)), _v((5, 2, 128))
     w, cs = _v((128,)), _v((5, 128))

@@ -18,6 +18,13 @@ Checked, for every sequence and every head:
   unused tails -- still holding the 1e4 poison;
 * all 8 prefill outputs and all 120 decode outputs against the oracle
   attention on the oracle's own rotated q/k (max-abs 2e-2, mean-abs 2e-3).
+
+The same step with the two attention calls in one launch (``mixed_step``:
+the prefill attention and the fused decode step in one kernel) gives every
+output and both caches bit-identical to the two launches it replaces
+(``flash_attn_varlen_func``, then ``paged_decode_step``), and so passes the
+oracle checks too; small cases cover the two-launch fallback (2 q-heads per
+kv head) and prefill workgroup counts below and above what is resident.
 """
 
 import pytest
@@ -29,7 +36,8 @@ from oracle import paged as op
 from oracle import varlen as ov
 from tests.helpers import assert_bitexact, assert_close
 from tinyserver_amd import workloads as W
-from tinyserver_amd.kernels import flash_attn_varlen_func, paged_attention_forward, qk_norm_rope_store
+from tinyserver_amd.kernels import (flash_attn_varlen_func, mixed_step, paged_attention_forward, paged_decode_step,
+                                    qk_norm_rope_store)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -58,8 +66,34 @@ def _store_all(kc, vc, pre, dec, kp, kd):
         ok.store_kv_cache(int(dec.positions[i]), torch.tensor(lst), kd[i][:, None], dec.v[i][:, None], kc, vc)
 
 
+_REFS = {}
+
+
+def _workload():
+    if "w" not in _REFS:
+        _REFS["w"] = W.make("qwen3-4b-mixed", poison=True)
+    return _REFS["w"]
+
+
+def _oracle_outputs(cpu):
+    """The oracle's prefill and decode attention on its own rotated q/k and
+    the oracle store of both halves (computed once per module)."""
+    if "out" not in _REFS:
+        pre, dec = cpu.prefill, cpu.decode
+        qp_ref, kp_ref = _rotated(pre)
+        qd_ref, kd_ref = _rotated(dec)
+        kc_ref, vc_ref = cpu.k_cache.clone(), cpu.v_cache.clone()
+        _store_all(kc_ref, vc_ref, pre, dec, kp_ref, kd_ref)
+        ref_p = ov.flash_attn_varlen_func(qp_ref, kp_ref, pre.v, pre.cu_seqlens, pre.cu_seqlens, pre.max_seqlen,
+                                          pre.max_seqlen, True)
+        ref_d = op.paged_attention_forward(qd_ref, kc_ref, vc_ref, dec.block_tables, W.PAGE,
+                                           dec.ctx_lens.to(torch.int32))
+        _REFS["out"] = (ref_p, ref_d)
+    return _REFS["out"]
+
+
 def test_qwen3_4b_mixed_step_shared_pool():
-    cpu = W.make("qwen3-4b-mixed", poison=True)
+    cpu = _workload()
     pre, dec = cpu.prefill, cpu.decode
     print(f"mixed step: {len(pre.seq_lens)} prefill seqs ({pre.q.shape[0]} tokens), {len(dec.ctx_lens)} decode seqs "
           f"(ctx {int(dec.ctx_lens.min())}..{int(dec.ctx_lens.max())}), pool {cpu.k_cache.shape[0]} pages",
@@ -97,11 +131,57 @@ def test_qwen3_4b_mixed_step_shared_pool():
     del kc_exp, vc_exp, kc_gpu, vc_gpu
 
     # ---- attention outputs, every sequence and head, on the oracle's own q/k
-    kc_ref, vc_ref = cpu.k_cache.clone(), cpu.v_cache.clone()
-    _store_all(kc_ref, vc_ref, pre, dec, kp_ref, kd_ref)
-    ref_p = ov.flash_attn_varlen_func(qp_ref, kp_ref, pre.v, pre.cu_seqlens, pre.cu_seqlens, pre.max_seqlen,
-                                      pre.max_seqlen, True)
+    ref_p, ref_d = _oracle_outputs(cpu)
     assert_close(out_p, ref_p, what="prefill attention, all 8 sequences")
-    ref_d = op.paged_attention_forward(qd_ref, kc_ref, vc_ref, dec.block_tables, W.PAGE,
-                                       dec.ctx_lens.to(torch.int32))
     assert_close(out_d, ref_d, what=f"decode attention, all {B} sequences")
+
+
+def _two_vs_one(cpu, **kw):
+    """The step after the prefill store, as two launches and as one; returns
+    both runs' (prefill out, decode out, k_cache, v_cache) on the CPU."""
+    runs = {}
+    for mode in ("two", "one"):
+        g = cpu.to(DEV)
+        gp, gd = g.prefill, g.decode
+        kc, vc = g.k_cache, g.v_cache
+        qp, kp = qk_norm_rope_store(gp.q, gp.k, gp.v, gp.q_weight, gp.k_weight, gp.cos, gp.sin, gp.eps, kc, vc,
+                                    gp.block_tables, gp.cu_seqlens)
+        sl = gd.ctx_lens.to(torch.int32)
+        if mode == "two":
+            out_p = flash_attn_varlen_func(qp, kp, gp.v, gp.cu_seqlens, gp.cu_seqlens, gp.max_seqlen, gp.max_seqlen,
+                                           True)
+            out_d = paged_decode_step(gd.q, gd.k, gd.v, gd.q_weight, gd.k_weight, gd.cos, gd.sin, gd.eps, kc, vc,
+                                      gd.block_tables, sl)
+        else:
+            out_p, out_d = mixed_step(qp, kp, gp.v, gp.cu_seqlens, gp.max_seqlen, gd.q, gd.k, gd.v, gd.q_weight,
+                                      gd.k_weight, gd.cos, gd.sin, gd.eps, kc, vc, gd.block_tables, sl, **kw)
+        torch.cuda.synchronize()
+        runs[mode] = [t.cpu() for t in (out_p, out_d, kc, vc)]
+        del g, gp, gd, kc, vc, qp, kp, out_p, out_d
+        torch.cuda.empty_cache()
+    for name, a, b in zip(("prefill output", "decode output", "k_cache", "v_cache"), runs["two"], runs["one"]):
+        assert_bitexact(b, a, f"one launch vs two: {name}")
+    return runs["one"]
+
+
+def test_qwen3_4b_mixed_step_one_launch():
+    cpu = _workload()
+    print(f"mixed step, one launch: {len(cpu.prefill.seq_lens)} prefill + {len(cpu.decode.ctx_lens)} decode seqs",
+          flush=True)
+    out_p, out_d, _, _ = _two_vs_one(cpu)
+    ref_p, ref_d = _oracle_outputs(cpu)
+    assert_close(out_p, ref_p, what="one launch: prefill attention, all 8 sequences")
+    assert_close(out_d, ref_d, what=f"one launch: decode attention, all {len(cpu.decode.ctx_lens)} sequences")
+
+
+@pytest.mark.parametrize("num_heads,num_kv_heads,prefill_workgroups",
+                         [(8, 2, 0), (8, 2, 3), (8, 2, 1000), (8, 4, 0)])
+def test_small_mixed_step_one_launch(num_heads, num_kv_heads, prefill_workgroups):
+    """5 decode sequences (ctx 1..300) and 3 prefill sequences (1..150
+    tokens) on one pool: 4 q-heads per kv head take the one kernel (with 3
+    prefill workgroups, the default one per CU, and 1000, more than fit
+    beside the decode ones); 2 take the two-launch fallback."""
+    cpu = W.make_mixed("mixed-small", 21, decode_batch=5, ctx_lo=1, ctx_hi=300, prefill_seqs=3, len_lo=1, len_hi=150,
+                       num_heads=num_heads, num_kv_heads=num_kv_heads, poison=True)
+    print(f"small mixed step: heads {num_heads}/{num_kv_heads}, prefill_workgroups {prefill_workgroups}", flush=True)
+    _two_vs_one(cpu, prefill_workgroups=prefill_workgroups)

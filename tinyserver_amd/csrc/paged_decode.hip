@@ -64,6 +64,7 @@
 
 #include "tsa_common.h"
 #include "norm_rope_row.h"
+#include "varlen_prefill_gqa.h"
 
 namespace tsa {
 
@@ -188,10 +189,17 @@ static_assert(sizeof(FusedState) <= 128, "fused state exceeds its LDS slot");
 // half the K/V bytes again), the non-temporal K/V stream takes this kernel
 // from 127 to 114 us on the same box; with the per-tile Q reads it took 124.
 // A wave whose run has fewer than kStreamNtMin tiles uses ordinary loads.
+// The fused step keeps ordinary loads for runs below kFusedNtMin tiles: with
+// non-temporal loads there, its Qwen3-8B batch-64 step measured 138 us
+// against 130.
 #ifndef TSA_DECODE_NT_MIN_TILES
 #define TSA_DECODE_NT_MIN_TILES 0
 #endif
 constexpr int kStreamNtMin = TSA_DECODE_NT_MIN_TILES;
+#ifndef TSA_FUSED_NT_MIN_TILES
+#define TSA_FUSED_NT_MIN_TILES 128
+#endif
+constexpr int kFusedNtMin = TSA_FUSED_NT_MIN_TILES;
 template <bool NT, typename T>
 __device__ __forceinline__ u32x4 load_stream(const T* p) {
   if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
@@ -274,15 +282,17 @@ struct TileCursor {
 // __restrict__ parameters: with the partial stores inside the loop, that is
 // what lets the compiler read block-table entries and lengths with scalar
 // loads.
+// decode_stream_body runs workgroup blockIdx.x of that grid (the first
+// workgroups of the launch); lds_i is the workgroup's LDS: kWaves tile prefixes of B + 1 ints, then (fused step)
+// kWaves areas of kFusedWaveBytes at the next 16-byte boundary.
 template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TSA_DECODE_WAVES_PER_EU)))
-void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ sl,
-                         float* __restrict__ part) {
+__device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* __restrict__ bt,
+                                                   const int32_t* __restrict__ sl, float* __restrict__ part,
+                                                   int* lds_i) {
   constexpr int KJ = D / 32;  // k-steps of the score MFMA
   a.bt = bt;
   a.seq_lens = sl;
   a.part = part;
-  extern __shared__ int lds_i[];
   const int G = a.G, Hkv = a.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
   // Wave-uniform (scalar) so tile indices, block-table reads and page bases
@@ -635,8 +645,16 @@ void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int
       }
     }
   };
-  if (n_tiles >= kStreamNtMin) stream(std::true_type{});
+  if (n_tiles >= (FUSED ? kFusedNtMin : kStreamNtMin)) stream(std::true_type{});
   else stream(std::false_type{});
+}
+
+template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TSA_DECODE_WAVES_PER_EU)))
+void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ sl,
+                         float* __restrict__ part) {
+  extern __shared__ int lds_i[];
+  decode_stream_body<T, D, PAGE16, CONTIG, FUSED>(a, bt, sl, part, lds_i);
 }
 
 // out[s, kvh * G + hd] = sum_v 2^(m_v - M) acc_v / sum_v 2^(m_v - M) l_v over
@@ -805,6 +823,25 @@ static DecodePlan make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int32
   return p;
 }
 
+// The merge of the stream kernel's partials (after it, on the same stream).
+template <typename T>
+static int launch_merge(const DecodeArgs& a, hipStream_t stream) {
+  const dim3 mgrid(a.B * a.Hkv);
+  const int outs = (a.G * a.D + 255) / 256;
+  if (outs <= 1) paged_decode_stream_merge<T, 1><<<mgrid, dim3(256), 0, stream>>>(a);
+  else if (outs <= 2) paged_decode_stream_merge<T, 2><<<mgrid, dim3(256), 0, stream>>>(a);
+  else if (outs <= 4) paged_decode_stream_merge<T, 4><<<mgrid, dim3(256), 0, stream>>>(a);
+  else paged_decode_stream_merge<T, 8><<<mgrid, dim3(256), 0, stream>>>(a);
+  return check_launch("tsa_paged_decode");
+}
+
+// LDS bytes of the fused stream kernel: kWaves tile prefixes, then the
+// per-wave fused areas at the next 16-byte boundary.
+static size_t fused_lds_bytes(int64_t B) {
+  return ((static_cast<size_t>(kWaves) * (B + 1) * 4 + 15) & ~size_t(15)) +
+         static_cast<size_t>(kWaves) * kFusedWaveBytes;
+}
+
 template <typename T>
 static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream, bool fused = false) {
   if (a.B == 0 || a.Hq == 0) return TSA_OK;
@@ -820,7 +857,7 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream, bool fuse
 #define TSA_DECODE_LAUNCH(DD, P16, CT) \
   paged_decode_stream<T, DD, P16, CT, false><<<grid, dim3(kThreads), lds, stream>>>(a, a.bt, a.seq_lens, a.part)
     if (fused) {  // checked by the caller: head_dim 128, 16-token pages, contiguous rows
-      const size_t lds_f = ((lds + 15) & ~size_t(15)) + static_cast<size_t>(kWaves) * kFusedWaveBytes;
+      const size_t lds_f = fused_lds_bytes(a.B);
       paged_decode_stream<T, 128, true, true, true><<<grid, dim3(kThreads), lds_f, stream>>>(a, a.bt, a.seq_lens,
                                                                                            a.part);
     } else if (a.D == 128) {
@@ -834,12 +871,7 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream, bool fuse
     }
 #undef TSA_DECODE_LAUNCH
     if (int rc = check_launch("tsa_paged_decode")) return rc;
-    const dim3 mgrid(a.B * a.Hkv);
-    const int outs = (a.G * a.D + 255) / 256;
-    if (outs <= 1) paged_decode_stream_merge<T, 1><<<mgrid, dim3(256), 0, stream>>>(a);
-    else if (outs <= 2) paged_decode_stream_merge<T, 2><<<mgrid, dim3(256), 0, stream>>>(a);
-    else if (outs <= 4) paged_decode_stream_merge<T, 4><<<mgrid, dim3(256), 0, stream>>>(a);
-    else paged_decode_stream_merge<T, 8><<<mgrid, dim3(256), 0, stream>>>(a);
+    return launch_merge<T>(a, stream);
   }
   return check_launch("tsa_paged_decode");
 }
@@ -946,13 +978,17 @@ extern "C" int tsa_paged_decode(const tsa_view* out, const tsa_view* query, cons
   return TSA_ERR_UNSUPPORTED;
 }
 
-extern "C" int tsa_paged_decode_step(const tsa_view* out, const tsa_view* query, const tsa_view* k_new,
-                                     const tsa_view* v_new, const tsa_view* q_weight, const tsa_view* k_weight,
-                                     const tsa_view* cos, const tsa_view* sin, double eps, const tsa_view* k_cache,
-                                     const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
-                                     double softmax_scale, void* workspace, size_t workspace_bytes,
-                                     int32_t num_workgroups, void* stream) {
-  DecodeArgs a;
+namespace tsa {
+// Checks of the fused decode step: prepare_decode's, then the new token's
+// rows, the norm weights and the cos/sin rows, and the shapes the fused
+// kernel covers (else TSA_ERR_UNSUPPORTED: such calls go through
+// tsa_qk_norm_rope_store + tsa_paged_decode).
+static int prepare_decode_step(const tsa_view* out, const tsa_view* query, const tsa_view* k_new,
+                               const tsa_view* v_new, const tsa_view* q_weight, const tsa_view* k_weight,
+                               const tsa_view* cos, const tsa_view* sin, double eps, const tsa_view* k_cache,
+                               const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
+                               double softmax_scale, void* workspace, size_t workspace_bytes, int32_t num_workgroups,
+                               DecodeArgs& a) {
   bool mfma = false;
   if (int rc = prepare_decode(out, query, k_cache, v_cache, block_tables, seq_lens, softmax_scale, workspace,
                               workspace_bytes, num_workgroups, a, mfma))
@@ -970,13 +1006,9 @@ extern "C" int tsa_paged_decode_step(const tsa_view* out, const tsa_view* query,
   TSA_REQUIRE(view_ok(cos, 2) && view_ok(sin, 2) && cos->size[0] == B && cos->size[1] == D && sin->size[0] == B &&
                   sin->size[1] == D && cos->dtype == dt && sin->dtype == dt,
               "cos and sin must be (num_seqs, head_dim) of query's dtype");
-  // The fused kernel covers the Qwen3 decode shape; other calls go through
-  // tsa_qk_norm_rope_store + tsa_paged_decode.
-  const size_t lds = ((static_cast<size_t>(kWaves) * (B + 1) * 4 + 15) & ~size_t(15)) +
-                     static_cast<size_t>(kWaves) * kFusedWaveBytes;
   TSA_UNSUPPORTED(mfma && D == 128 && a.BS % 16 == 0 && a.kc_s == D && a.vc_s == D && a.G <= 8 &&
                       rows_vec16(k_new) && rows_vec16(v_new) && rows_vec16(q_weight) && rows_vec16(k_weight) &&
-                      rows_vec16(cos) && rows_vec16(sin) && lds <= 64 * 1024,
+                      rows_vec16(cos) && rows_vec16(sin) && fused_lds_bytes(B) <= 64 * 1024,
                   "the fused decode step needs a 16-bit dtype, head_dim 128, 16-token-multiple pages, contiguous "
                   "cache rows, at most 8 q-heads per kv head and unit-stride 16-byte-aligned rows");
   a.kn = k_new->data; a.vn = v_new->data; a.qw = q_weight->data; a.kw = k_weight->data;
@@ -986,9 +1018,109 @@ extern "C" int tsa_paged_decode_step(const tsa_view* out, const tsa_view* query,
   a.cs_ss = cos->stride[0]; a.sn_ss = sin->stride[0];
   a.eps = static_cast<float>(eps);
   a.kc_out = k_cache->data; a.vc_out = v_cache->data;
+  return TSA_OK;
+}
+}  // namespace tsa
+
+extern "C" int tsa_paged_decode_step(const tsa_view* out, const tsa_view* query, const tsa_view* k_new,
+                                     const tsa_view* v_new, const tsa_view* q_weight, const tsa_view* k_weight,
+                                     const tsa_view* cos, const tsa_view* sin, double eps, const tsa_view* k_cache,
+                                     const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
+                                     double softmax_scale, void* workspace, size_t workspace_bytes,
+                                     int32_t num_workgroups, void* stream) {
+  DecodeArgs a;
+  if (int rc = prepare_decode_step(out, query, k_new, v_new, q_weight, k_weight, cos, sin, eps, k_cache, v_cache,
+                                   block_tables, seq_lens, softmax_scale, workspace, workspace_bytes, num_workgroups,
+                                   a))
+    return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dt == TSA_BF16) return launch_decode<bf16_t>(a, true, st, true);
+  if (query->dtype == TSA_BF16) return launch_decode<bf16_t>(a, true, st, true);
   return launch_decode<f16_t>(a, true, st, true);
+}
+
+// ---------------------------------------------------------------------------
+// tsa_mixed_step: a continuous-batching step's prefill attention and decode
+// step in one launch (plus the decode merge). The first W workgroups run the
+// fused decode step's stream (decode_stream_body: norm/RoPE + store of each
+// decode sequence's new token, then its paged attention); the others run the
+// LDS-staged GQA prefill (prefill_gqa_body) over the prefill batch. Both take
+// 4-wave workgroups with at most 256 registers per lane, and the kernel's
+// 78 KB of LDS lets two workgroups share a CU, so with the default split (W =
+// one decode workgroup per CU, one prefill workgroup per CU) every workgroup
+// is resident at once and each CU runs one of each: the MFMA-bound prefill
+// waves and the HBM-bound decode waves share its SIMDs. The two halves touch
+// disjoint pages (a page belongs to one sequence), and the prefill attends
+// over its own q/k/v, written to the pool beforehand by its norm/RoPE/store
+// launch, so they need no ordering between them; every output is
+// bit-identical to tsa_varlen_prefill followed by tsa_paged_decode_step.
+namespace tsa {
+
+constexpr int kMixedLds = gqa_smem_bytes<128, 4>();
+static_assert(kMixedLds >= 64 * 1024, "the mixed kernel's LDS also holds the fused decode step's (at most 64 KB)");
+static_assert(kThreads == 64 * 4 && TSA_DECODE_WAVES_PER_EU == 2,
+              "the decode and prefill roles share a 4-wave workgroup compiled for two waves per SIMD");
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void mixed_step_kernel(
+    DecodeArgs d, const int32_t* __restrict__ bt, const int32_t* __restrict__ sl, float* __restrict__ part,
+    PrefillArgs p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
+  __shared__ __align__(16) char lds_m[kMixedLds];
+  if (static_cast<int>(blockIdx.x) < d.W)
+    decode_stream_body<T, 128, true, true, true>(d, bt, sl, part, reinterpret_cast<int*>(lds_m));
+  else
+    prefill_gqa_body<T, 128, 4>(p, cu_q, cu_k, lds_m, d.W);
+}
+
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess || cus <= 0)
+    cus = 256;
+  return cus;
+}
+
+}  // namespace tsa
+
+extern "C" int tsa_mixed_step(const tsa_view* prefill_out, const tsa_view* prefill_q, const tsa_view* prefill_k,
+                              const tsa_view* prefill_v, const tsa_view* cu_seqlens, int64_t max_seqlen,
+                              double prefill_scale, const tsa_view* out, const tsa_view* query, const tsa_view* k_new,
+                              const tsa_view* v_new, const tsa_view* q_weight, const tsa_view* k_weight,
+                              const tsa_view* cos, const tsa_view* sin, double eps, const tsa_view* k_cache,
+                              const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
+                              double softmax_scale, void* workspace, size_t workspace_bytes, int32_t num_workgroups,
+                              int32_t prefill_workgroups, void* stream) {
+  PrefillArgs pa;
+  bool pmfma = false;
+  if (int rc = prefill_prepare(prefill_out, prefill_q, prefill_k, prefill_v, cu_seqlens, cu_seqlens, max_seqlen,
+                               max_seqlen, 1, prefill_scale, pa, pmfma))
+    return rc;
+  DecodeArgs a;
+  if (int rc = prepare_decode_step(out, query, k_new, v_new, q_weight, k_weight, cos, sin, eps, k_cache, v_cache,
+                                   block_tables, seq_lens, softmax_scale, workspace, workspace_bytes, num_workgroups,
+                                   a))
+    return rc;
+  TSA_REQUIRE(prefill_workgroups >= 0, "prefill_workgroups must be non-negative");
+  const int dt = query->dtype;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // One launch when the prefill takes varlen_prefill_gqa<T, 128, 4> in the
+  // decode step's dtype and both halves have work; else the two launches.
+  const bool one = pa.nseq > 0 && pa.Hq > 0 && pa.total_q > 0 && a.B > 0 && prefill_q->dtype == dt &&
+                   prefill_takes_gqa4(pa, pmfma);
+  if (!one) {
+    if (int rc = prefill_launch(pa, pmfma, prefill_q->dtype, max_seqlen, st)) return rc;
+    if (a.B == 0) return TSA_OK;
+    return dt == TSA_BF16 ? launch_decode<bf16_t>(a, true, st, true) : launch_decode<f16_t>(a, true, st, true);
+  }
+  const int P = prefill_workgroups > 0 ? prefill_workgroups : device_cus();
+  const dim3 grid(a.W + P);
+  if (dt == TSA_BF16) {
+    mixed_step_kernel<bf16_t><<<grid, dim3(kThreads), 0, st>>>(a, a.bt, a.seq_lens, a.part, pa, pa.cu_q, pa.cu_k);
+    if (int rc = check_launch("tsa_mixed_step")) return rc;
+    return launch_merge<bf16_t>(a, st);
+  }
+  mixed_step_kernel<f16_t><<<grid, dim3(kThreads), 0, st>>>(a, a.bt, a.seq_lens, a.part, pa, pa.cu_q, pa.cu_k);
+  if (int rc = check_launch("tsa_mixed_step")) return rc;
+  return launch_merge<f16_t>(a, st);
 }
 
 // ---------------------------------------------------------------------------
