@@ -20,7 +20,11 @@ Also measured (in "secondary"), each with its roofline and a CPU baseline:
                             in scheduler order: the prefill batch's
                             norm/RoPE/store and varlen attention, then the
                             decode batch's norm/RoPE/store and paged
-                            attention; per-launch times and rooflines
+                            attention; per-launch times and rooflines; and
+                            as one norm/RoPE/store of both batches plus
+                            mixed_attention (both attentions in one call)
+  qwen3-4b-mixed-chunk      the same decode batch beside two short prefill
+                            chunks, where mixed_attention runs one kernel
   qwen3-8b-decode-bs64-page256  the headline batch on the server's default
                             256-token pages (decode and its fused store)
   sampling-qwen3-vocab-bs64 batched sampling over 64 Qwen3-vocab rows
@@ -349,9 +353,10 @@ def bench_mixed(name, steps, warmup, copies=3):
     the prefill batch's fused norm/RoPE/store and varlen attention, then the
     decode batch's norm/RoPE/store and paged attention, on one stream. Timed
     as a whole step and launch by launch (each alone, on the same inputs);
-    and as the step with both attention calls in one launch (mixed_step)."""
+    and as one norm/RoPE/store of both batches plus one attention launch
+    (mixed_attention)."""
     from tinyserver_amd import workloads as W
-    from tinyserver_amd.kernels import (flash_attn_varlen_func, mixed_step, paged_attention_forward, paged_decode_step,
+    from tinyserver_amd.kernels import (flash_attn_varlen_func, mixed_attention, paged_attention_forward,
                                         qk_norm_rope_store)
 
     dev = torch.device("cuda:0")
@@ -391,32 +396,50 @@ def bench_mixed(name, steps, warmup, copies=3):
         q2 = dec_store(i)
         paged_attention_forward(q2, kc, vc, d.block_tables, W.PAGE, seq_lens, out=out_d)
 
-    # The same step with the two attention calls in one launch: the prefill
-    # store, then mixed_step (prefill attention + the fused decode step in one
-    # kernel, + the decode merge).
-    def one_attn(i):
-        kc, vc = pools[i % copies]
-        mixed_step(qp, kp, p.v, p.cu_seqlens, p.max_seqlen, d.q, d.k, d.v, d.q_weight, d.k_weight, d.cos, d.sin,
-                   d.eps, kc, vc, d.block_tables, seq_lens, prefill_out=out_p, out=out_d)
+    # The same step as an engine batching both would issue it: one
+    # norm/RoPE/store over the tokens of both batches (packed outside the
+    # timed region, as the engine's metadata step would), then both attention
+    # calls in one launch (mixed_attention, + the decode merge).
+    width = max(p.block_tables.shape[1], d.block_tables.shape[1])
 
-    def dec_step(i):
+    def pad(t):
+        return torch.nn.functional.pad(t, (0, width - t.shape[1]))
+
+    ppos = torch.cat([torch.arange(int(n)) for n in p.seq_lens.cpu()]).to(dev)
+    pk = dict(q=torch.cat([p.q, d.q]), k=torch.cat([p.k, d.k]), v=torch.cat([p.v, d.v]),
+              cos=torch.cat([p.cos, d.cos]), sin=torch.cat([p.sin, d.sin]),
+              bt=torch.cat([pad(p.block_tables), pad(d.block_tables)]),
+              cu=torch.cat([p.cu_seqlens, T + torch.arange(1, B + 1, dtype=torch.int32, device=dev)]),
+              pos=torch.cat([ppos, pos]).to(torch.int64))
+    q_all = torch.empty_like(pk["q"])
+    k_all = torch.empty_like(pk["k"])
+
+    def packed_store(i):
         kc, vc = pools[i % copies]
-        paged_decode_step(d.q, d.k, d.v, d.q_weight, d.k_weight, d.cos, d.sin, d.eps, kc, vc, d.block_tables,
-                          seq_lens, out=out_d)
+        qk_norm_rope_store(pk["q"], pk["k"], pk["v"], p.q_weight, p.k_weight, pk["cos"], pk["sin"], p.eps, kc, vc,
+                           pk["bt"], pk["cu"], pk["pos"], q_out=q_all, k_out=k_all)
+
+    packed_store(0)
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+
+    def one_attn(i, prefill_workgroups=0):
+        kc, vc = pools[i % copies]
+        mixed_attention(q_all[:T], k_all[:T], p.v, p.cu_seqlens, p.max_seqlen, q_all[T:], kc, vc, d.block_tables,
+                        seq_lens, prefill_workgroups=prefill_workgroups, prefill_out=out_p, out=out_d)
 
     def step_one(i):
-        kc, vc = pools[i % copies]
-        q1, k1 = pre_store(i)
-        mixed_step(q1, k1, p.v, p.cu_seqlens, p.max_seqlen, d.q, d.k, d.v, d.q_weight, d.k_weight, d.cos, d.sin,
-                   d.eps, kc, vc, d.block_tables, seq_lens, prefill_out=out_p, out=out_d)
+        packed_store(i)
+        one_attn(i)
 
     step_us = time_region(step, steps, warmup)[0] * 1e3
     step_one_us = time_region(step_one, steps, warmup)[0] * 1e3
     t = {k: time_region(f, steps, warmup)[0] * 1e3
          for k, f in (("prefill_norm_rope_store", pre_store), ("prefill_attention", pre_attn),
                       ("decode_norm_rope_store", dec_store), ("decode_attention", dec_attn))}
-    t_one = {k: time_region(f, steps, warmup)[0] * 1e3 for k, f in (("decode_step", dec_step),
-                                                                   ("mixed_attention", one_attn))}
+    t_one = {k: time_region(f, steps, warmup)[0] * 1e3
+             for k, f in (("norm_rope_store", packed_store), ("mixed_attention", one_attn),
+                          ("one_kernel", lambda i: one_attn(i, cus)))}
     flops = W.prefill_flops(p.seq_lens, hq)
     dbytes = W.decode_bytes(d.ctx_lens, d.num_heads, d.num_kv_heads)
     launches = {
@@ -436,13 +459,16 @@ def bench_mixed(name, steps, warmup, copies=3):
         "order": "prefill norm/RoPE/store -> varlen attention -> decode norm/RoPE/store -> paged attention",
         "one_launch": {
             "step_us": step_one_us, "tokens_per_s": (T + B) / (step_one_us * 1e-6),
-            "order": "prefill norm/RoPE/store -> mixed_step (varlen attention + fused decode step in one kernel, "
-                     "+ the decode merge)",
+            "order": "norm/RoPE/store of both batches' tokens -> mixed_attention (varlen attention + paged "
+                     "attention in one kernel, + the decode merge)",
+            "norm_rope_store_us": t_one["norm_rope_store"],
             "mixed_attention_us": t_one["mixed_attention"],
-            "separate": {"prefill_attention_us": t["prefill_attention"], "decode_step_us": t_one["decode_step"],
-                         "sum_us": t["prefill_attention"] + t_one["decode_step"]},
-            "roofline": {"decode_hbm": _roof_hbm(dbytes, t_one["mixed_attention"]),
-                         "prefill_mfma": _roof_mfma(flops, t_one["mixed_attention"])},
+            "mixed_attention_path": "one kernel" if T <= 512 else "two launches (prefill batch over 512 tokens)",
+            "one_kernel_us": t_one["one_kernel"],
+            "separate_attention_sum_us": t["prefill_attention"] + t["decode_attention"],
+            "roofline": {"decode_hbm": _roof_hbm(dbytes, t_one["one_kernel"]),
+                         "prefill_mfma": _roof_mfma(flops, t_one["one_kernel"]),
+                         "note": "the one kernel: decode bytes and prefill FLOPs each over its whole time"},
         },
     }, m
 
@@ -552,6 +578,10 @@ def secondaries(steps, warmup, cpu, cpu_s):
             "decode": {"literal": cpu_decode_baseline(m.decode, True, cpu_s),
                        "vectorized": cpu_decode_baseline(m.decode, False, cpu_s)}}
     sec["qwen3-4b-mixed"] = _round(s)
+    del m
+    _free()
+    s, m = bench_mixed("qwen3-4b-mixed-chunk", steps, min(warmup, 3))
+    sec["qwen3-4b-mixed-chunk"] = _round(s)
     del m
     _free()
     # the headline batch on the server's default 256-token pages

@@ -33,9 +33,10 @@
  *                           norm/RoPE, store and paged attention, fused
  *   tsa_varlen_prefill      server/model/kernels/varlen_attention.py:145-218
  *                           (flash_attn_varlen_func)
- *   tsa_mixed_step          no single counterpart: a prefill batch's attention
- *                           (qwen3.py:291-327) and a decode batch's step
- *                           (qwen3.py:328-416) in one launch, for an engine
+ *   tsa_mixed_attention     no single counterpart: a prefill batch's attention
+ *                           (flash_attn_varlen_func, qwen3.py:173-214) and a
+ *                           decode batch's (paged_attention_forward,
+ *                           qwen3.py:387-409) in one launch, for an engine
  *                           that batches them together (the reference's
  *                           scheduler issues them apart, scheduler.py:128-227)
  *   tsa_sample_tokens       server/model/sampling.py:119-194 (sample_tokens)
@@ -197,25 +198,27 @@ int tsa_varlen_prefill(const tsa_view* out, const tsa_view* q, const tsa_view* k
                        int32_t causal, double softmax_scale, void* stream);
 
 /* A continuous-batching step's two attention calls in one launch (+ the
- * decode merge): the causal varlen prefill of a prefill batch -- prefill_out,
- * prefill_q/k/v and cu_seqlens as tsa_varlen_prefill's out, q, k, v and
- * cu_seqlens_q = cu_seqlens_k, causal, scale prefill_scale -- and the fused
- * decode step of a decode batch, with tsa_paged_decode_step's arguments and
- * rules. Same outputs, bit for bit, as tsa_varlen_prefill then
- * tsa_paged_decode_step on one stream. One kernel runs both when the prefill
- * takes the 4-head-group, head_dim-128 LDS-staged kernel in the decode
- * step's dtype: num_workgroups decode workgroups (0: one per CU) beside
- * prefill_workgroups prefill workgroups (0: one per CU), so that each CU
- * runs one of each. Otherwise it issues those two calls. The two batches
- * must use disjoint pages, as distinct sequences do. */
-int tsa_mixed_step(const tsa_view* prefill_out, const tsa_view* prefill_q, const tsa_view* prefill_k,
-                   const tsa_view* prefill_v, const tsa_view* cu_seqlens, int64_t max_seqlen,
-                   double prefill_scale, const tsa_view* out, const tsa_view* query, const tsa_view* k_new,
-                   const tsa_view* v_new, const tsa_view* q_weight, const tsa_view* k_weight,
-                   const tsa_view* cos, const tsa_view* sin, double eps, const tsa_view* k_cache,
-                   const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
-                   double softmax_scale, void* workspace, size_t workspace_bytes, int32_t num_workgroups,
-                   int32_t prefill_workgroups, void* stream);
+ * decode merge): the causal varlen prefill of a prefill batch --
+ * prefill_out, prefill_q/k/v and cu_seqlens as tsa_varlen_prefill's out, q,
+ * k, v and cu_seqlens_q = cu_seqlens_k, causal, scale prefill_scale -- and
+ * the paged decode attention of a decode batch, with tsa_paged_decode's
+ * arguments and rules (its K/V already stored). Same outputs, bit for bit,
+ * as tsa_varlen_prefill then tsa_paged_decode on one stream. One kernel can
+ * run both when the decode has head_dim 128, 16-token-multiple pages and
+ * contiguous cache rows and the prefill takes the 4-head-group,
+ * head_dim-128 LDS-staged kernel in the decode's dtype: num_workgroups
+ * decode workgroups (0: one per CU) beside the prefill workgroups, so that
+ * each CU runs one of each. prefill_workgroups > 0 asks for that kernel with
+ * that many prefill workgroups; 0 takes it for prefill batches of at most 512
+ * tokens (the two roles slow each other down on a shared CU, so it pays for
+ * short prefill chunks only) and issues the two calls otherwise. */
+int tsa_mixed_attention(const tsa_view* prefill_out, const tsa_view* prefill_q, const tsa_view* prefill_k,
+                        const tsa_view* prefill_v, const tsa_view* cu_seqlens, int64_t max_seqlen,
+                        double prefill_scale, const tsa_view* out, const tsa_view* query,
+                        const tsa_view* k_cache, const tsa_view* v_cache, const tsa_view* block_tables,
+                        const tsa_view* seq_lens, double softmax_scale, void* workspace,
+                        size_t workspace_bytes, int32_t num_workgroups, int32_t prefill_workgroups,
+                        void* stream);
 
 /* sample_tokens (server/model/sampling.py:119-194): one token per row of
  * logits (B, V) (bf16, f16 or f32): x = logits / max(temperature, 1e-5), in

@@ -128,13 +128,12 @@ def test_prefill_validation():
     assert rc == _lib.TSA_ERR_INVALID and "divisible" in msg
 
 
-def test_mixed_step_validation():
-    """tsa_mixed_step checks both halves' arguments, as the two calls it
+def test_mixed_attention_validation():
+    """tsa_mixed_attention checks both halves' arguments, as the two calls it
     replaces do, before any device work."""
     pq, pk = _v((10, 8, 128)), _v((10, 2, 128))
     cu = _v((3,), torch.int32)
-    q, kn = _v((4, 8, 128)), _v((4, 2, 128))
-    w, cs = _v((128,)), _v((4, 128))
+    q = _v((4, 8, 128))
     kc = _v((10, 2, 16, 128))
     bt, sl = _v((4, 2), torch.int32), _v((4,), torch.int32)
     lib = _lib.load()
@@ -142,9 +141,8 @@ def test_mixed_step_validation():
     ws = 1 << 20  # a fake, 256-byte aligned address: never dereferenced
 
     def call(p_k=pk, query=q, ws_ptr=ws, pwg=0):
-        return _call("tsa_mixed_step", R(pq), R(pq), R(p_k), R(p_k), R(cu), 9, 0.1, R(query), R(query), R(kn),
-                     R(kn), R(w), R(w), R(cs), R(cs), 1e-6, R(kc), R(kc), R(bt), R(sl), 0.1, ws_ptr, ws_bytes, 0, pwg,
-                     None)
+        return _call("tsa_mixed_attention", R(pq), R(pq), R(p_k), R(p_k), R(cu), 9, 0.1, R(query), R(query), R(kc),
+                     R(kc), R(bt), R(sl), 0.1, ws_ptr, ws_bytes, 0, pwg, None)
 
     rc, msg = call(p_k=_v((10, 3, 128)))
     assert rc == _lib.TSA_ERR_INVALID and "divisible" in msg

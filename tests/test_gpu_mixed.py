@@ -19,12 +19,12 @@ Checked, for every sequence and every head:
 * all 8 prefill outputs and all 120 decode outputs against the oracle
   attention on the oracle's own rotated q/k (max-abs 2e-2, mean-abs 2e-3).
 
-The same step with the two attention calls in one launch (``mixed_step``:
-the prefill attention and the fused decode step in one kernel) gives every
-output and both caches bit-identical to the two launches it replaces
-(``flash_attn_varlen_func``, then ``paged_decode_step``), and so passes the
-oracle checks too; small cases cover the two-launch fallback (2 q-heads per
-kv head) and prefill workgroup counts below and above what is resident.
+The same step as an engine batching both would issue it -- one norm/RoPE/
+store over the tokens of both batches, then both attentions in one launch
+(``mixed_attention``) -- gives every output, the rotated q/k and both caches
+bit-identical to the scheduler-order step above, and so passes the oracle
+checks too; small cases cover the two-launch fallback (2 q-heads per kv
+head) and prefill workgroup counts below and above what is resident.
 """
 
 import pytest
@@ -36,8 +36,7 @@ from oracle import paged as op
 from oracle import varlen as ov
 from tests.helpers import assert_bitexact, assert_close
 from tinyserver_amd import workloads as W
-from tinyserver_amd.kernels import (flash_attn_varlen_func, mixed_step, paged_attention_forward, paged_decode_step,
-                                    qk_norm_rope_store)
+from tinyserver_amd.kernels import flash_attn_varlen_func, mixed_attention, paged_attention_forward, qk_norm_rope_store
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -136,39 +135,69 @@ def test_qwen3_4b_mixed_step_shared_pool():
     assert_close(out_d, ref_d, what=f"decode attention, all {B} sequences")
 
 
+def _packed(gp, gd):
+    """The tokens of both batches as one norm/RoPE/store call: prefill
+    tokens first (positions 0..L-1 per sequence), then one token per decode
+    sequence (position ctx-1); block tables padded to one width."""
+    dev = gp.q.device
+    T, B = gp.q.shape[0], gd.q.shape[0]
+    width = max(gp.block_tables.shape[1], gd.block_tables.shape[1])
+
+    def pad(t):
+        return torch.nn.functional.pad(t, (0, width - t.shape[1]))
+
+    ppos = torch.cat([torch.arange(int(n)) for n in gp.seq_lens.cpu()]).to(dev)
+    return dict(
+        q=torch.cat([gp.q, gd.q]), k=torch.cat([gp.k, gd.k]), v=torch.cat([gp.v, gd.v]),
+        cos=torch.cat([gp.cos, gd.cos]), sin=torch.cat([gp.sin, gd.sin]),
+        block_tables=torch.cat([pad(gp.block_tables), pad(gd.block_tables)]),
+        cu_seqlens=torch.cat([gp.cu_seqlens, T + torch.arange(1, B + 1, dtype=torch.int32, device=dev)]),
+        positions=torch.cat([ppos, gd.positions.to(dev)]).to(torch.int64),
+    )
+
+
 def _two_vs_one(cpu, **kw):
-    """The step after the prefill store, as two launches and as one; returns
-    both runs' (prefill out, decode out, k_cache, v_cache) on the CPU."""
+    """The step in scheduler order (two stores, two attention launches) and
+    as one store + one attention launch; every output, the rotated q/k and
+    both caches must match bit for bit. Returns the one-launch outputs."""
     runs = {}
     for mode in ("two", "one"):
         g = cpu.to(DEV)
         gp, gd = g.prefill, g.decode
         kc, vc = g.k_cache, g.v_cache
-        qp, kp = qk_norm_rope_store(gp.q, gp.k, gp.v, gp.q_weight, gp.k_weight, gp.cos, gp.sin, gp.eps, kc, vc,
-                                    gp.block_tables, gp.cu_seqlens)
+        T, B = gp.q.shape[0], gd.q.shape[0]
         sl = gd.ctx_lens.to(torch.int32)
         if mode == "two":
+            qp, kp = qk_norm_rope_store(gp.q, gp.k, gp.v, gp.q_weight, gp.k_weight, gp.cos, gp.sin, gp.eps, kc, vc,
+                                        gp.block_tables, gp.cu_seqlens)
             out_p = flash_attn_varlen_func(qp, kp, gp.v, gp.cu_seqlens, gp.cu_seqlens, gp.max_seqlen, gp.max_seqlen,
                                            True)
-            out_d = paged_decode_step(gd.q, gd.k, gd.v, gd.q_weight, gd.k_weight, gd.cos, gd.sin, gd.eps, kc, vc,
-                                      gd.block_tables, sl)
+            qd, kd = qk_norm_rope_store(gd.q, gd.k, gd.v, gd.q_weight, gd.k_weight, gd.cos, gd.sin, gd.eps, kc, vc,
+                                        gd.block_tables, torch.arange(B + 1, dtype=torch.int32, device=DEV),
+                                        gd.positions)
+            out_d = paged_attention_forward(qd, kc, vc, gd.block_tables, W.PAGE, sl)
+            qr, kr = torch.cat([qp, qd]), torch.cat([kp, kd])
         else:
-            out_p, out_d = mixed_step(qp, kp, gp.v, gp.cu_seqlens, gp.max_seqlen, gd.q, gd.k, gd.v, gd.q_weight,
-                                      gd.k_weight, gd.cos, gd.sin, gd.eps, kc, vc, gd.block_tables, sl, **kw)
+            pk = _packed(gp, gd)
+            qr, kr = qk_norm_rope_store(pk["q"], pk["k"], pk["v"], gp.q_weight, gp.k_weight, pk["cos"], pk["sin"],
+                                        gp.eps, kc, vc, pk["block_tables"], pk["cu_seqlens"], pk["positions"])
+            out_p, out_d = mixed_attention(qr[:T], kr[:T], gp.v, gp.cu_seqlens, gp.max_seqlen, qr[T:], kc, vc,
+                                           gd.block_tables, sl, **kw)
         torch.cuda.synchronize()
-        runs[mode] = [t.cpu() for t in (out_p, out_d, kc, vc)]
-        del g, gp, gd, kc, vc, qp, kp, out_p, out_d
+        runs[mode] = [t.cpu() for t in (out_p, out_d, qr, kr, kc, vc)]
+        del g, gp, gd, kc, vc, qr, kr, out_p, out_d
         torch.cuda.empty_cache()
-    for name, a, b in zip(("prefill output", "decode output", "k_cache", "v_cache"), runs["two"], runs["one"]):
-        assert_bitexact(b, a, f"one launch vs two: {name}")
+    names = ("prefill output", "decode output", "rotated q", "rotated k", "k_cache", "v_cache")
+    for name, a, b in zip(names, runs["two"], runs["one"]):
+        assert_bitexact(b, a, f"one store + one attention launch vs scheduler order: {name}")
     return runs["one"]
 
 
 def test_qwen3_4b_mixed_step_one_launch():
     cpu = _workload()
-    print(f"mixed step, one launch: {len(cpu.prefill.seq_lens)} prefill + {len(cpu.decode.ctx_lens)} decode seqs",
-          flush=True)
-    out_p, out_d, _, _ = _two_vs_one(cpu)
+    print(f"mixed step, one attention launch: {len(cpu.prefill.seq_lens)} prefill + {len(cpu.decode.ctx_lens)} "
+          f"decode seqs", flush=True)
+    out_p, out_d = _two_vs_one(cpu, prefill_workgroups=256)[:2]  # one kernel (automatic would take two launches)
     ref_p, ref_d = _oracle_outputs(cpu)
     assert_close(out_p, ref_p, what="one launch: prefill attention, all 8 sequences")
     assert_close(out_d, ref_d, what=f"one launch: decode attention, all {len(cpu.decode.ctx_lens)} sequences")
@@ -178,9 +207,10 @@ def test_qwen3_4b_mixed_step_one_launch():
                          [(8, 2, 0), (8, 2, 3), (8, 2, 1000), (8, 4, 0)])
 def test_small_mixed_step_one_launch(num_heads, num_kv_heads, prefill_workgroups):
     """5 decode sequences (ctx 1..300) and 3 prefill sequences (1..150
-    tokens) on one pool: 4 q-heads per kv head take the one kernel (with 3
-    prefill workgroups, the default one per CU, and 1000, more than fit
-    beside the decode ones); 2 take the two-launch fallback."""
+    tokens, a short chunk) on one pool: 4 q-heads per kv head take the one
+    kernel (automatically with one prefill workgroup per CU, and asked for
+    with 3 and 1000, more than fit beside the decode ones); 2 take the
+    two-launch fallback."""
     cpu = W.make_mixed("mixed-small", 21, decode_batch=5, ctx_lo=1, ctx_hi=300, prefill_seqs=3, len_lo=1, len_hi=150,
                        num_heads=num_heads, num_kv_heads=num_kv_heads, poison=True)
     print(f"small mixed step: heads {num_heads}/{num_kv_heads}, prefill_workgroups {prefill_workgroups}", flush=True)

@@ -61,10 +61,9 @@ SIGNATURES = {
         [_V] * 8 + [c_double] + [_V] * 4 + [c_double, c_void_p, c_size_t, c_int32, c_void_p],
     ),
     "tsa_varlen_prefill": (c_int, [_V, _V, _V, _V, _V, _V, c_int64, c_int64, c_int32, c_double, c_void_p]),
-    "tsa_mixed_step": (
+    "tsa_mixed_attention": (
         c_int,
-        [_V] * 5 + [c_int64, c_double] + [_V] * 8 + [c_double] + [_V] * 4
-        + [c_double, c_void_p, c_size_t, c_int32, c_int32, c_void_p],
+        [_V] * 5 + [c_int64, c_double] + [_V] * 6 + [c_double, c_void_p, c_size_t, c_int32, c_int32, c_void_p],
     ),
     "tsa_sample_tokens": (c_int, [_V, _V, _V, _V, _V, _V, c_void_p]),
 }

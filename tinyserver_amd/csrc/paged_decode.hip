@@ -1039,34 +1039,43 @@ extern "C" int tsa_paged_decode_step(const tsa_view* out, const tsa_view* query,
 }
 
 // ---------------------------------------------------------------------------
-// tsa_mixed_step: a continuous-batching step's prefill attention and decode
-// step in one launch (plus the decode merge). The first W workgroups run the
-// fused decode step's stream (decode_stream_body: norm/RoPE + store of each
-// decode sequence's new token, then its paged attention); the others run the
-// LDS-staged GQA prefill (prefill_gqa_body) over the prefill batch. Both take
-// 4-wave workgroups with at most 256 registers per lane, and the kernel's
-// 78 KB of LDS lets two workgroups share a CU, so with the default split (W =
-// one decode workgroup per CU, one prefill workgroup per CU) every workgroup
-// is resident at once and each CU runs one of each: the MFMA-bound prefill
-// waves and the HBM-bound decode waves share its SIMDs. The two halves touch
-// disjoint pages (a page belongs to one sequence), and the prefill attends
-// over its own q/k/v, written to the pool beforehand by its norm/RoPE/store
-// launch, so they need no ordering between them; every output is
-// bit-identical to tsa_varlen_prefill followed by tsa_paged_decode_step.
+// tsa_mixed_attention: a continuous-batching step's two attention calls in
+// one launch (plus the decode merge). The first W workgroups run the decode
+// stream (decode_stream_body: paged attention of each decode sequence over
+// its pages); the others run the LDS-staged GQA prefill (prefill_gqa_body)
+// over the prefill batch. Both take 4-wave workgroups with at most 256
+// registers per lane, and the kernel's 78 KB of LDS lets two workgroups share
+// a CU, so with the default split (W = one decode workgroup per CU, one
+// prefill workgroup per CU) every workgroup is resident at once and each CU
+// runs one of each (a per-workgroup trace of CU ids and start/end times
+// showed exactly that). Both read only (the caches and q/k/v); each writes
+// its own output and the decode its workspace, so they need no ordering;
+// every output is bit-identical to tsa_varlen_prefill followed by
+// tsa_paged_decode.
 namespace tsa {
 
 constexpr int kMixedLds = gqa_smem_bytes<128, 4>();
-static_assert(kMixedLds >= 64 * 1024, "the mixed kernel's LDS also holds the fused decode step's (at most 64 KB)");
+// Automatic choice (prefill_workgroups == 0): one kernel only for prefill
+// batches of at most this many tokens. Sharing a CU, the two roles slow each
+// other down -- the LDS-staged prefill's loads wait behind the decode's HBM
+// stream -- so one launch pays only when the prefill is a short chunk beside
+// the decode. Measured on Qwen3-4B heads (one launch vs two):
+//   4 decode (ctx 128-512) + 322 prefill tokens       29.0 vs 37.8 us
+//   120 decode (ctx 256-8192) + 402 prefill tokens    343-346 vs 354.7 us
+//   8 decode (ctx 256-2048) + 2583 prefill tokens     66.9 vs 63.1 us
+//   120 decode (ctx 256-8192) + 5760 prefill tokens   419.4 vs 396.1 us
+constexpr int64_t kMixedAutoMaxTokens = 512;
+static_assert(kMixedLds >= 64 * 1024, "the mixed kernel's LDS also holds the decode tile prefixes (at most 64 KB)");
 static_assert(kThreads == 64 * 4 && TSA_DECODE_WAVES_PER_EU == 2,
               "the decode and prefill roles share a 4-wave workgroup compiled for two waves per SIMD");
 
 template <typename T>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void mixed_step_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void mixed_attention_kernel(
     DecodeArgs d, const int32_t* __restrict__ bt, const int32_t* __restrict__ sl, float* __restrict__ part,
     PrefillArgs p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
   __shared__ __align__(16) char lds_m[kMixedLds];
   if (static_cast<int>(blockIdx.x) < d.W)
-    decode_stream_body<T, 128, true, true, true>(d, bt, sl, part, reinterpret_cast<int*>(lds_m));
+    decode_stream_body<T, 128, true, true, false>(d, bt, sl, part, reinterpret_cast<int*>(lds_m));
   else
     prefill_gqa_body<T, 128, 4>(p, cu_q, cu_k, lds_m, d.W);
 }
@@ -1081,45 +1090,54 @@ static int device_cus() {
 
 }  // namespace tsa
 
-extern "C" int tsa_mixed_step(const tsa_view* prefill_out, const tsa_view* prefill_q, const tsa_view* prefill_k,
-                              const tsa_view* prefill_v, const tsa_view* cu_seqlens, int64_t max_seqlen,
-                              double prefill_scale, const tsa_view* out, const tsa_view* query, const tsa_view* k_new,
-                              const tsa_view* v_new, const tsa_view* q_weight, const tsa_view* k_weight,
-                              const tsa_view* cos, const tsa_view* sin, double eps, const tsa_view* k_cache,
-                              const tsa_view* v_cache, const tsa_view* block_tables, const tsa_view* seq_lens,
-                              double softmax_scale, void* workspace, size_t workspace_bytes, int32_t num_workgroups,
-                              int32_t prefill_workgroups, void* stream) {
+extern "C" int tsa_mixed_attention(const tsa_view* prefill_out, const tsa_view* prefill_q, const tsa_view* prefill_k,
+                                   const tsa_view* prefill_v, const tsa_view* cu_seqlens, int64_t max_seqlen,
+                                   double prefill_scale, const tsa_view* out, const tsa_view* query,
+                                   const tsa_view* k_cache, const tsa_view* v_cache, const tsa_view* block_tables,
+                                   const tsa_view* seq_lens, double softmax_scale, void* workspace,
+                                   size_t workspace_bytes, int32_t num_workgroups, int32_t prefill_workgroups,
+                                   void* stream) {
   PrefillArgs pa;
   bool pmfma = false;
   if (int rc = prefill_prepare(prefill_out, prefill_q, prefill_k, prefill_v, cu_seqlens, cu_seqlens, max_seqlen,
                                max_seqlen, 1, prefill_scale, pa, pmfma))
     return rc;
   DecodeArgs a;
-  if (int rc = prepare_decode_step(out, query, k_new, v_new, q_weight, k_weight, cos, sin, eps, k_cache, v_cache,
-                                   block_tables, seq_lens, softmax_scale, workspace, workspace_bytes, num_workgroups,
-                                   a))
+  bool dmfma = false;
+  if (int rc = prepare_decode(out, query, k_cache, v_cache, block_tables, seq_lens, softmax_scale, workspace,
+                              workspace_bytes, num_workgroups, a, dmfma))
     return rc;
   TSA_REQUIRE(prefill_workgroups >= 0, "prefill_workgroups must be non-negative");
   const int dt = query->dtype;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // One launch when the prefill takes varlen_prefill_gqa<T, 128, 4> in the
-  // decode step's dtype and both halves have work; else the two launches.
-  const bool one = pa.nseq > 0 && pa.Hq > 0 && pa.total_q > 0 && a.B > 0 && prefill_q->dtype == dt &&
-                   prefill_takes_gqa4(pa, pmfma);
+  // One launch when the decode takes the head_dim-128, 16-token-page,
+  // contiguous-row stream kernel, the prefill varlen_prefill_gqa<T, 128, 4>
+  // in the same dtype, both halves have work, and the caller asks for it
+  // (prefill_workgroups > 0) or the prefill is a short chunk; else the two
+  // launches.
+  const bool one = dmfma && a.D == 128 && a.BS % 16 == 0 && a.kc_s == a.D && a.vc_s == a.D && a.B > 0 &&
+                   pa.nseq > 0 && pa.Hq > 0 && pa.total_q > 0 && prefill_q->dtype == dt &&
+                   prefill_takes_gqa4(pa, pmfma) && (prefill_workgroups > 0 || pa.total_q <= kMixedAutoMaxTokens);
   if (!one) {
     if (int rc = prefill_launch(pa, pmfma, prefill_q->dtype, max_seqlen, st)) return rc;
-    if (a.B == 0) return TSA_OK;
-    return dt == TSA_BF16 ? launch_decode<bf16_t>(a, true, st, true) : launch_decode<f16_t>(a, true, st, true);
+    switch (dt) {
+      case TSA_BF16: return launch_decode<bf16_t>(a, dmfma, st);
+      case TSA_F16: return launch_decode<f16_t>(a, dmfma, st);
+      case TSA_F32: return launch_decode<float>(a, false, st);
+    }
+    set_error("unsupported dtype");
+    return TSA_ERR_UNSUPPORTED;
   }
   const int P = prefill_workgroups > 0 ? prefill_workgroups : device_cus();
   const dim3 grid(a.W + P);
   if (dt == TSA_BF16) {
-    mixed_step_kernel<bf16_t><<<grid, dim3(kThreads), 0, st>>>(a, a.bt, a.seq_lens, a.part, pa, pa.cu_q, pa.cu_k);
-    if (int rc = check_launch("tsa_mixed_step")) return rc;
+    mixed_attention_kernel<bf16_t><<<grid, dim3(kThreads), 0, st>>>(a, a.bt, a.seq_lens, a.part, pa, pa.cu_q,
+                                                                     pa.cu_k);
+    if (int rc = check_launch("tsa_mixed_attention")) return rc;
     return launch_merge<bf16_t>(a, st);
   }
-  mixed_step_kernel<f16_t><<<grid, dim3(kThreads), 0, st>>>(a, a.bt, a.seq_lens, a.part, pa, pa.cu_q, pa.cu_k);
-  if (int rc = check_launch("tsa_mixed_step")) return rc;
+  mixed_attention_kernel<f16_t><<<grid, dim3(kThreads), 0, st>>>(a, a.bt, a.seq_lens, a.part, pa, pa.cu_q, pa.cu_k);
+  if (int rc = check_launch("tsa_mixed_attention")) return rc;
   return launch_merge<f16_t>(a, st);
 }
 

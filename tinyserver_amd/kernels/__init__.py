@@ -8,7 +8,7 @@ continuous-batching step's prefill and decode attention in one launch.
 """
 
 from .kv_cache import store_kv_cache, store_kv_cache_batched, store_kv_cache_paged
-from .mixed_step import mixed_step
+from .mixed_attention import mixed_attention
 from .paged_attention import paged_attention_forward, paged_decode_step
 from .qk_norm_rope import qk_norm_rope, qk_norm_rope_store
 from .sampling import sample_tokens
@@ -24,5 +24,5 @@ __all__ = [
     "qk_norm_rope",
     "qk_norm_rope_store",
     "sample_tokens",
-    "mixed_step",
+    "mixed_attention",
 ]

@@ -12,6 +12,8 @@ Shapes follow Qwen3 attention (head_dim 128, page 16):
   qwen3-4b-mixed            one continuous-batching step on one shared pool:
                             8 new prefill seqs L U[256,1024], then 120 decode
                             seqs ctx U[256,8192]; 32/8 heads
+  qwen3-4b-mixed-chunk      the same decode batch beside 2 short prefill
+                            chunks, L U[128,512] (a chunked-prefill step)
 
 A decode step stores one new token per sequence at position ctx-1 (pages for
 positions 0..ctx-2 hold N(0,1) K/V) and attends over ctx tokens. cos/sin are
@@ -215,6 +217,8 @@ WORKLOADS = {
                                               len_hi=1024)),
     "qwen3-4b-mixed": ("mixed", dict(seed=5, decode_batch=120, ctx_lo=256, ctx_hi=8192, prefill_seqs=8,
                                      len_lo=256, len_hi=1024, num_heads=32, num_kv_heads=8)),
+    "qwen3-4b-mixed-chunk": ("mixed", dict(seed=7, decode_batch=120, ctx_lo=256, ctx_hi=8192, prefill_seqs=2,
+                                           len_lo=128, len_hi=512, num_heads=32, num_kv_heads=8)),
 }
 
 
