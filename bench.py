@@ -70,13 +70,27 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_traffic.json")
 
 
 # ------------------------------------------------------------------ timing --
+# Untimed calls before each timed region also run for at least this long
+# (the secondary lines set it): the shader clock ramps under sustained load,
+# and a few warmup calls of a short launch leave it mid-ramp.
+_MIN_WARM_MS = 0.0
+
+
 def time_region(fn, steps, warmup):
-    """warmup untimed calls, then `steps` calls bracketed by synchronisations
-    and one pair of events on the current stream. Returns (event ms per call,
-    wall ms per call)."""
+    """warmup untimed calls (and more, to _MIN_WARM_MS of wall time), then
+    `steps` calls bracketed by synchronisations and one pair of events on the
+    current stream. Returns (event ms per call, wall ms per call)."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    if _MIN_WARM_MS > 0:
+        t_end = time.perf_counter() + _MIN_WARM_MS / 1e3
+        i = warmup
+        while time.perf_counter() < t_end:
+            for _ in range(8):
+                fn(i)
+                i += 1
+            torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
@@ -540,8 +554,14 @@ def _free():
     torch.cuda.empty_cache()
 
 
+def _progress(name):
+    print(f"bench: {name} done", file=sys.stderr, flush=True)
+
+
 def secondaries(steps, warmup, cpu, cpu_s):
     """Every secondary workload, each with its CPU baselines (cpu=True)."""
+    global _MIN_WARM_MS
+    _MIN_WARM_MS = 200.0
     sec = {}
     # the reference's CPU-runnable decode case
     s, w = bench_decode("qwen3-0.6b-decode-bs4", steps, warmup, with_block=True)
@@ -549,6 +569,7 @@ def secondaries(steps, warmup, cpu, cpu_s):
         s["cpu_baseline"] = {"literal": cpu_decode_baseline(w, True, cpu_s),
                              "vectorized": cpu_decode_baseline(w, False, cpu_s)}
     sec["qwen3-0.6b-decode-bs4"] = _round(s)
+    _progress("qwen3-0.6b-decode-bs4")
     del w
     _free()
     # 32k-context decode (one pool copy: 4.3 GB, far past the MALL)
@@ -557,6 +578,7 @@ def secondaries(steps, warmup, cpu, cpu_s):
         s["cpu_baseline"] = {"literal": cpu_decode_baseline(w, True, cpu_s),
                              "vectorized": cpu_decode_baseline(w, False, cpu_s)}
     sec["qwen3-32b-decode-bs32"] = _round(s)
+    _progress("qwen3-32b-decode-bs32")
     del w
     _free()
     # varlen prefill
@@ -567,6 +589,7 @@ def secondaries(steps, warmup, cpu, cpu_s):
                                    "(606 MB in bf16) and its SDPA scores every pair: not a bounded sample"},
             "vectorized": cpu_prefill_baseline(w, False, cpu_s)}
     sec["qwen3-8b-prefill-16seq"] = _round(s)
+    _progress("qwen3-8b-prefill-16seq")
     del w
     _free()
     # the continuous-batching step on one shared pool
@@ -578,15 +601,18 @@ def secondaries(steps, warmup, cpu, cpu_s):
             "decode": {"literal": cpu_decode_baseline(m.decode, True, cpu_s),
                        "vectorized": cpu_decode_baseline(m.decode, False, cpu_s)}}
     sec["qwen3-4b-mixed"] = _round(s)
+    _progress("qwen3-4b-mixed")
     del m
     _free()
     s, m = bench_mixed("qwen3-4b-mixed-chunk", steps, min(warmup, 3))
     sec["qwen3-4b-mixed-chunk"] = _round(s)
+    _progress("qwen3-4b-mixed-chunk")
     del m
     _free()
     # the headline batch on the server's default 256-token pages
     s, w = bench_decode(HEADLINE, steps, min(warmup, 3), with_block=True, page=256)
     sec["qwen3-8b-decode-bs64-page256"] = _round(s)
+    _progress("qwen3-8b-decode-bs64-page256")
     del w
     _free()
     # batched sampling
@@ -594,6 +620,7 @@ def secondaries(steps, warmup, cpu, cpu_s):
     if cpu:
         s["cpu_baseline"] = cpu_sampling_baseline(*args, cpu_s)
     sec["sampling-qwen3-vocab-bs64"] = _round(s)
+    _progress("sampling-qwen3-vocab-bs64")
     return sec
 
 
@@ -626,6 +653,8 @@ def main():
 
     _lib.load()
     if args.workload:
+        global _MIN_WARM_MS
+        _MIN_WARM_MS = 200.0
         kind = W.WORKLOADS[args.workload][0] if args.workload in W.WORKLOADS else None
         if args.workload == "sampling-qwen3-vocab-bs64":
             res, _ = bench_sampling(args.steps, args.warmup)
