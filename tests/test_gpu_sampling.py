@@ -11,13 +11,23 @@ row. Cases: the reference's known answers and allowed-set rule
 with mixed temperatures, top-k, top-p and greedy rows in bf16, f16 and f32;
 all-equal and few-valued rows (ties resolved in index order, buckets split
 again); rows half masked to -inf; strided logits; repeat calls; a row alone
-vs inside a batch.
+vs inside a batch. Top-k and greedy rows of 16-bit logits take the candidate
+pass (the row read once into registers, a sample bounding its k-th largest
+value, the few elements above it ranked and decided on); it is checked
+against the oracle in the cases above and against the histogram paths
+(TSA_SAMPLE_CANDIDATES=0) on the same rows token for token, and its edge rows
+(too many candidates, -0 beside +0, the largest top_k it takes and the next,
+flat rows with many candidates, short and odd-sized rows) against the
+oracle.
 """
+
+import os
 
 import pytest
 import torch
 
 from oracle import sampling as osm
+from tinyserver_amd import _lib
 from tinyserver_amd.kernels import sample_tokens
 
 pytestmark = pytest.mark.gpu
@@ -210,3 +220,97 @@ def test_nonfinite_rows_match_reference(dtype):
     assert greedy[5] == 10 and greedy[6] == 0 and greedy[7] == 20 and greedy[9] == v - 3
     sampled = _gpu(rows, [1.0] * n, [0] * n, [1.0] * n, [0.3] * n, dtype=dtype).tolist()
     assert sampled[3] == v - 1 and sampled[6] == v - 1
+
+
+def _single_kernel(logits, temperature, top_k, top_p, uniforms):
+    """sample_tokens with the candidate pass switched off: every row on the
+    histogram paths."""
+    os.environ["TSA_SAMPLE_CANDIDATES"] = "0"
+    try:
+        out = sample_tokens(logits, temperature, top_k, top_p, uniforms)
+        torch.cuda.synchronize()
+    finally:
+        del os.environ["TSA_SAMPLE_CANDIDATES"]
+    return out.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_candidate_path_matches_single_kernel(dtype):
+    """The same 64 Qwen3-vocab rows through both paths: the same tokens,
+    except where the oracle's decision margin puts a row within fp32
+    rounding of a threshold."""
+    logits, temperature, top_k, top_p, uniforms = _qwen3_batch(17)
+    t = lambda v, dt: torch.tensor(v, dtype=dt, device=DEV)
+    args = (logits.to(DEV, dtype), t(temperature, torch.float32), t(top_k, torch.int64), t(top_p, torch.float32),
+            t(uniforms, torch.float32))
+    fast = sample_tokens(*args).cpu()
+    full = _single_kernel(*args)
+    lf = logits.to(dtype).float()
+    diff = (fast != full).nonzero().flatten().tolist()
+    for i in diff:
+        m = osm.decision_margin(lf[i], temperature[i], top_k[i], top_p[i], uniforms[i])
+        assert m < MARGIN, f"row {i}: candidate path {fast[i].item()} vs single kernel {full[i].item()}, margin {m:.3e}"
+    print(f"candidate vs single-kernel path, {dtype}: {len(diff)} of 64 rows differ", flush=True)
+    assert len(diff) <= 2
+
+
+def test_candidate_path_edge_rows():
+    """bf16 rows at the edges of the candidate path, against the oracle:
+    all-equal and two-valued rows (too many candidates: the histogram paths
+    take them); -0 and +0 ties; top_k 512 (the largest the pass takes) and
+    513; greedy rows with the tied maximum at both ends of the row."""
+    v = 151936
+    g = torch.Generator().manual_seed(18)
+    base = torch.randn(4, v, generator=g) * 2.5
+    equal = torch.zeros(2, v)
+    two = (torch.rand(2, v, generator=g) < 0.5).float()
+    zeros = torch.randn(2, v, generator=g)
+    zeros[:, ::5] = 0.0
+    zeros[:, 1::5] = -0.0
+    zeros[:, 2::7] = -3.0
+    tied = torch.randn(2, v, generator=g)
+    tied[:, [v - 1, 40000, 7]] = 9.0  # the same maximum at three places
+    rows = torch.cat([base, equal, two, zeros, tied])
+    temperature = [0.8, 1.0, 0.7, 1.2, 1.0, 1.0, 1.0, 0.9, 1.0, 0.5, 0.0, 1.0]
+    top_k = [512, 513, 1, 50, 10, 1, 20, 500, 3, 5, 0, 2]
+    top_p = [0.9, 0.9, 1.0, 0.5, 1.0, 1.0, 0.7, 1.0, 1.0, 0.6, 1.0, 1.0]
+    uniforms = [0.5, 0.2, 0.9, 0.99, 0.3, 0.0, 0.45, 0.8, 0.1, 0.7, 0.5, 0.75]
+    got, _ = _compare(rows, temperature, top_k, top_p, uniforms, dtype=torch.bfloat16, what="candidate edges")
+    assert got[10].item() == 7  # greedy: the first index of the tied maximum
+    ref_exact = osm.sample_tokens(rows.to(torch.bfloat16), torch.tensor(temperature), torch.tensor(top_k),
+                                  torch.tensor(top_p), torch.tensor(uniforms), dtype=torch.float64)
+    assert got[4:6].tolist() == ref_exact[4:6].tolist()  # all-equal rows: exact in fp64
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_candidate_path_large_k(dtype):
+    """top_k from 127 up to the pass's largest, 512, on Qwen3-vocab rows with
+    a few hot tokens and on flat rows (many near-ties, so far more than k
+    candidates): the oracle, and the histogram paths token for token."""
+    v = 151936
+    g = torch.Generator().manual_seed(23)
+    hot, _, _, _, _ = _qwen3_batch(24, b=8)
+    flat = torch.randn(8, v, generator=g) * 0.05
+    rows = torch.cat([hot, flat])
+    ks = [127, 128, 129, 200, 300, 400, 511, 512] * 2
+    temperature = [1.0, 0.8, 1.2, 0.7, 1.0, 0.9, 1.1, 1.0] * 2
+    top_p = [1.0, 0.95, 0.9, 1.0, 0.8, 1.0, 0.99, 0.5] * 2
+    uniforms = torch.rand(16, generator=g).tolist()
+    got, _ = _compare(rows, temperature, ks, top_p, uniforms, dtype=dtype, what=f"large k {dtype}")
+    t = lambda x, dt: torch.tensor(x, dtype=dt, device=DEV)
+    full = _single_kernel(rows.to(DEV, dtype), t(temperature, torch.float32), t(ks, torch.int64),
+                          t(top_p, torch.float32), t(uniforms, torch.float32))
+    assert torch.equal(got, full), (got.tolist(), full.tolist())
+
+
+@pytest.mark.parametrize("v", [8, 200, 1001, 4096 + 8, 155648, 155656])
+def test_candidate_path_short_and_odd_rows(v):
+    """Short rows (most threads hold no chunk), a row whose length is not a
+    multiple of 8, the longest row the pass holds in registers (155,648
+    logits) and the next multiple of 8 (the histogram paths), against the
+    oracle."""
+    g = torch.Generator().manual_seed(19 + v)
+    rows = torch.randn(6, v, generator=g) * 2
+    k = min(5, v - 1)
+    _compare(rows, [1.0, 0.0, 0.7, 1.0, 1.3, 0.9], [k, 0, 1, k, 3 if v > 3 else 1, 2], [0.9, 1.0, 1.0, 0.5, 1.0, 0.8],
+             [0.1, 0.5, 0.6, 0.99, 0.3, 0.0], dtype=torch.bfloat16, what=f"v={v}")

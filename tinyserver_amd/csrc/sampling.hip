@@ -30,7 +30,15 @@
 // per-decision path above.
 // Greedy rows (temperature <= 0) take the first index of the row's maximum,
 // which is the stable sort's rank 0, as the reference does.
+//
+// Top-k rows (top_k <= 512) and greedy rows of a 16-bit row of at most
+// 155,648 logits first take a candidate pass: the row is read once into
+// registers, a sample of it bounds its k-th largest value from below, and
+// only the few elements above that bound are gathered, ranked and decided
+// on. A row it cannot finish (too many candidates, NaN or inf) continues down
+// the paths above.
 #include <cmath>
+#include <cstdlib>
 
 #include "tsa_common.h"
 
@@ -53,6 +61,7 @@ struct SampleArgs {
   const float* topp; int64_t topp_s;
   const float* unif; int64_t unif_s;
   int64_t* out; int64_t out_s;
+  int cand;  // 1: top-k and greedy rows may take the register-resident candidate pass
 };
 
 __device__ __forceinline__ int64_t load_int(const void* p, int dt, int64_t i) {
@@ -72,6 +81,61 @@ __device__ __forceinline__ float key_of_rank(uint64_t rk) {
   const uint32_t o = ~static_cast<uint32_t>(rk >> 32);
   return __builtin_bit_cast(float, (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
+
+// 2^40 exp2((kv - kmax) * kc) on v_exp_f32, truncated to an integer in two
+// 32-bit halves (exact: the value has at most 24 significant bits). Both
+// paths weigh keys with this one function, so their sums agree bit for bit.
+__device__ __forceinline__ uint64_t mass_of(float kv, float kmax, float kc) {
+  const float v = fast_exp2((kv - kmax) * kc) * kMassOne;
+  const uint32_t hi = static_cast<uint32_t>(v * 2.3283064365386963e-10f);  // v / 2^32
+  const uint32_t lo = static_cast<uint32_t>(v - static_cast<float>(hi) * 4294967296.0f);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// ---- The candidate pass (top-k and greedy rows of 16-bit logits).
+constexpr int kRegChunks = 19;  // 8-logit chunks per thread: the row stays in registers
+constexpr int64_t kRegMaxV = int64_t{kSampThreads} * kRegChunks * 8;  // 155,648 logits
+constexpr int64_t kFastK = 512;                                        // the largest top_k it takes
+constexpr int kGatherCap = kCap / 2;  // candidates it may gather: keys[kGatherCap, kCap)
+constexpr int kStageCap = 256;        // chunks holding a candidate it may stage
+constexpr int kSelBins = 4096;        // 12-bit key prefixes
+
+// The rows the candidate pass takes: greedy rows (rank 0) and rows whose
+// top-k cut falls inside the row, with top_k <= kFastK.
+__device__ __forceinline__ bool candidate_row(const SampleArgs& a, float temp, int64_t k) {
+  return temp <= 0.f || (k > 0 && k <= kFastK && k < a.V);
+}
+
+// Two 16-bit floats (one word) -> two order-preserving 16-bit keys, larger
+// keys for larger values (v_pk_ashrrev_i16 + v_bitop3_b32). -0 (0x7FFF) sits
+// just below +0 (0x8000); a positive NaN lies above +inf, a negative NaN below
+// -inf.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_key(uint32_t w) {
+  const s16x2 m = __builtin_bit_cast(s16x2, w) >> (s16x2){15, 15};
+  return w ^ (__builtin_bit_cast(uint32_t, m) | 0x80008000u);
+}
+__device__ __forceinline__ uint32_t pk_max(uint32_t x, uint32_t y) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_max(__builtin_bit_cast(u16x2, x), __builtin_bit_cast(u16x2, y)));
+}
+__device__ __forceinline__ uint32_t pk_min(uint32_t x, uint32_t y) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_min(__builtin_bit_cast(u16x2, x), __builtin_bit_cast(u16x2, y)));
+}
+__device__ __forceinline__ uint32_t hmax(uint32_t w) { return max(w & 0xFFFFu, w >> 16); }
+// A key's 16-bit float bits.
+__device__ __forceinline__ uint32_t key_bits(uint32_t key) {
+  return (key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu);
+}
+template <typename T> struct Inf16;
+template <> struct Inf16<bf16_t> {
+  static constexpr uint32_t kPosKey = 0xFF80u, kNegKey = 0x007Fu, kNegBits = 0xFF80u;
+};
+template <> struct Inf16<f16_t> {
+  static constexpr uint32_t kPosKey = 0xFC00u, kNegKey = 0x03FFu, kNegBits = 0xFC00u;
+};
 
 struct SampleLds {
   uint32_t cnt[kBuckets];
@@ -98,20 +162,20 @@ struct RowSampler {
   float xmax;  // row maximum of x
   int tid, lane, wave;
 
-  __device__ float logit(int64_t i) const { return to_float(UNIT ? row[static_cast<int>(i)] : row[i * a.ls1]); }
-  __device__ float x_at(int64_t i) const { return __fdiv_rn(logit(i), t); }
+  __device__ __forceinline__ float logit(int64_t i) const { return to_float(UNIT ? row[static_cast<int>(i)] : row[i * a.ls1]); }
+  __device__ __forceinline__ float x_at(int64_t i) const { return __fdiv_rn(logit(i), t); }
   // The value the single-histogram path orders by. For 16-bit logits it is
   // the logit itself: distinct 16-bit values differ by at least 2^-8
   // relatively, so dividing them by one t keeps them distinct and in order,
   // and ties in x are exactly ties in the logit. fp32 logits order by x.
   static constexpr bool kByLogit = sizeof(T) == 2;
-  __device__ float key_at(int64_t i) const { return kByLogit ? logit(i) : x_at(i); }
+  __device__ __forceinline__ float key_at(int64_t i) const { return kByLogit ? logit(i) : x_at(i); }
   // f(i, key_at(i)) for every element of the row, each thread taking its
   // elements in an order of its own (every use is order-free). A 16-bit row
   // that is 16-byte aligned with a multiple of 8 elements is read 8 logits
   // per lane per load, so each load moves 1 KB per wave and several are in
   // flight; other rows one element at a time.
-  __device__ bool chunked() const {
+  __device__ __forceinline__ bool chunked() const {
     return UNIT && sizeof(T) == 2 && (reinterpret_cast<uintptr_t>(row) & 15) == 0 && (a.V & 7) == 0;
   }
   // f(i, key) for the elements whose key may lie in [lo, hi]: in a chunked
@@ -119,7 +183,7 @@ struct RowSampler {
   // comparison (the callers' ranges carry a margin, and f still tests each
   // element exactly); otherwise every element.
   template <typename F>
-  __device__ void each_key_in(float lo, float hi, F f) const {
+  __device__ __forceinline__ void each_key_in(float lo, float hi, F f) const {
     if constexpr (UNIT && sizeof(T) == 2) {
       if (chunked()) {
         const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
@@ -151,7 +215,7 @@ struct RowSampler {
   // The key range that holds buckets [b0, b1] of the shared histogram, with
   // a bucket's width of margin on each side; unbounded where that cannot be
   // said (no spread, or the last bucket, which also takes -inf and NaN).
-  __device__ void bucket_range(int b0, int b1, float scale, float& lo, float& hi) const {
+  __device__ __forceinline__ void bucket_range(int b0, int b1, float scale, float& lo, float& hi) const {
     lo = -INFINITY;
     hi = INFINITY;
     if (!(scale > 0.f) || b1 >= kBuckets - 1) return;
@@ -164,7 +228,7 @@ struct RowSampler {
   }
 
   template <typename F>
-  __device__ void each_key(F f) const {
+  __device__ __forceinline__ void each_key(F f) const {
     if constexpr (UNIT && sizeof(T) == 2) {
       if (chunked()) {
         const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
@@ -183,25 +247,18 @@ struct RowSampler {
     }
     for (int i = tid; i < static_cast<int>(a.V); i += kSampThreads) f(i, key_at(i));
   }
-  __device__ float key_to_x(float k) const { return kByLogit ? __fdiv_rn(k, t) : k; }
+  __device__ __forceinline__ float key_to_x(float k) const { return kByLogit ? __fdiv_rn(k, t) : k; }
   float kmax;  // row maximum of key_at
   float kc;    // log2(e) / t for 16-bit logits, log2(e) for fp32 (keys are x)
-  // 2^40 exp(x - xmax) from a key, as exp2((key - kmax) * kc) on v_exp_f32,
-  // truncated to an integer in two 32-bit halves (exact: the value has at
-  // most 24 significant bits). The single-histogram path's mass; the row
-  // maximum weighs exactly 2^40.
-  __device__ uint64_t mass_key(float kv) const {
-    const float v = fast_exp2((kv - kmax) * kc) * kMassOne;
-    const uint32_t hi = static_cast<uint32_t>(v * 2.3283064365386963e-10f);  // v / 2^32
-    const uint32_t lo = static_cast<uint32_t>(v - static_cast<float>(hi) * 4294967296.0f);
-    return (static_cast<uint64_t>(hi) << 32) | lo;
-  }
-  __device__ uint64_t mass(float x) const {
+  // 2^40 exp(x - xmax) from a key (mass_of): the single-histogram path's
+  // mass; the row maximum weighs exactly 2^40.
+  __device__ __forceinline__ uint64_t mass_key(float kv) const { return mass_of(kv, kmax, kc); }
+  __device__ __forceinline__ uint64_t mass(float x) const {
     return static_cast<uint64_t>(rintf(expf(x - xmax) * kMassOne));
   }
 
   // Wave then block sum of a 64-bit value; every thread gets the total.
-  __device__ uint64_t block_sum(uint64_t v) {
+  __device__ __forceinline__ uint64_t block_sum(uint64_t v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     __syncthreads();
     if (lane == 0) s.wave_u64[wave] = v;
@@ -213,7 +270,7 @@ struct RowSampler {
 
   // Exclusive prefix of s.wsum over the buckets in place (two per thread),
   // in bucket order.
-  __device__ void scan_buckets() {
+  __device__ __forceinline__ void scan_buckets() {
     const uint64_t w0 = s.wsum[2 * tid], w1 = s.wsum[2 * tid + 1];
     uint64_t incl = w0 + w1;
     for (int o = 1; o < 64; o <<= 1) {
@@ -232,7 +289,7 @@ struct RowSampler {
   }
 
   // Bitonic sort of s.keys[0, n) ascending, padded to a power of two.
-  __device__ void sort_keys(int n) {
+  __device__ __forceinline__ void sort_keys(int n) {
     int p = 1;
     while (p < n) p <<= 1;
     for (int i = n + tid; i < p; i += kSampThreads) s.keys[i] = ~uint64_t{0};
@@ -253,7 +310,7 @@ struct RowSampler {
       }
   }
 
-  __device__ static int bucket0(float x, float h, float sc) {
+  __device__ __forceinline__ static int bucket0(float x, float h, float sc) {
     if (x == -INFINITY) return kBuckets - 1;
     const float f = (h - x) * sc;
     if (!(f < static_cast<float>(kBuckets - 1))) return kBuckets - 1;  // also NaN: never an index from it
@@ -262,7 +319,7 @@ struct RowSampler {
 
   // Exclusive prefix over the buckets (two per thread) of in[] into out[].
   template <typename U>
-  __device__ void scan2(const U* in, U* out) {
+  __device__ __forceinline__ void scan2(const U* in, U* out) {
     const U w0 = in[2 * tid], w1 = in[2 * tid + 1];
     uint64_t incl = static_cast<uint64_t>(w0) + w1;
     for (int o = 1; o < 64; o <<= 1) {
@@ -282,7 +339,7 @@ struct RowSampler {
 
   // The smallest non-empty bucket b <= last whose running mass through b
   // (the full bucket, or last_incl for bucket `last`) reaches the target.
-  __device__ int first_bucket(int last, uint64_t last_incl, bool ge, double target) {
+  __device__ __forceinline__ int first_bucket(int last, uint64_t last_incl, bool ge, double target) {
     if (tid == 0) s.found_bucket = kBuckets;
     __syncthreads();
     for (int b = tid; b < kBuckets; b += kSampThreads) {
@@ -297,7 +354,7 @@ struct RowSampler {
   }
 
   // Gathers bucket b of the shared histogram into s.keys in rank order.
-  __device__ bool gather_sorted(int b, float scale, int& cached) {
+  __device__ __forceinline__ bool gather_sorted(int b, float scale, int& cached) {
     if (cached == b) return true;
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
@@ -317,7 +374,7 @@ struct RowSampler {
 
   // Gathers every bucket up to nb (the top ranks of the row) into s.keys in
   // rank order: position e of the sorted list is rank e of the row.
-  __device__ bool gather_prefix(int nb, float scale) {
+  __device__ __forceinline__ bool gather_prefix(int nb, float scale) {
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
     float lo, hi;
@@ -338,7 +395,7 @@ struct RowSampler {
   // lim_k, top-p the ranks through the first whose running mass exceeds
   // p * Z (z: the kept mass when known from the histogram, else summed
   // here), the pick is the first kept rank reaching u * (kept mass).
-  __device__ int64_t decide_on_prefix(int n, int lim_k, bool z_known, uint64_t z, double p, double u) {
+  __device__ __forceinline__ int64_t decide_on_prefix(int n, int lim_k, bool z_known, uint64_t z, double p, double u) {
     uint64_t cum, tot;
     const int lk = lim_k >= 0 ? lim_k : n;
     if (!z_known) {
@@ -362,7 +419,7 @@ struct RowSampler {
   // Over the first `limit` sorted elements, with `base` before them: the
   // position of the one element that reaches the target (see select), its
   // running mass through it, and the mass of all `limit` elements.
-  __device__ int scan_sorted(int limit, uint64_t base, bool ge, double target, uint64_t& cum_at, uint64_t& total) {
+  __device__ __forceinline__ int scan_sorted(int limit, uint64_t base, bool ge, double target, uint64_t& cum_at, uint64_t& total) {
     const int per = (limit + kSampThreads - 1) / kSampThreads;
     const int e0 = min(limit, tid * per), e1 = min(limit, e0 + per);
     uint64_t mine = 0;
@@ -399,12 +456,351 @@ struct RowSampler {
     return pos;
   }
 
+  // The candidate pass for a top-k or greedy row of a 16-bit row of at most
+  // kRegMaxV logits (chunked). load_row reads the row into registers (issued
+  // before the row's parameters arrive); candidates then:
+  //   1. keys every logit; each half-lane's largest key is a sample (2048
+  //      distinct elements), and the row's largest and smallest keys flag a
+  //      NaN, a +inf or a row of -inf (those go on to the histogram paths);
+  //   2. K = the k-th largest sample (12-bit prefix histogram, then the low 4
+  //      bits of the samples in that prefix), so at least k elements have key
+  //      >= K; +0's key is lowered to take -0 too;
+  //   3. finds the chunks holding a key >= K from each chunk's maximum (kept
+  //      in LDS by step 1), skipping with a scalar test every chunk no lane
+  //      of the wave holds one in, and stages those chunks in LDS (one atomic
+  //      per wave and chunk);
+  //   4. wave 0 turns the staged chunks' keys >= K into candidates -- a
+  //      prefix of the row in rank order that holds its first k ranks -- and,
+  //      for at most 64, ranks them (a count: keys are distinct), moves each
+  //      to its rank's lane (ds_permute) and decides there (decide_lanes);
+  //   5. more candidates are ranked by the block, and decide_wave decides;
+  //      a greedy row takes rank 0.
+  // The token, or -1 to send the row on (more than kStageCap chunks or
+  // kGatherCap candidates, a non-finite row, or a pick past the candidates).
+  __device__ __forceinline__ void load_row(u32x4 (&ch)[kRegChunks]) const {
+    const int n8 = static_cast<int>(a.V >> 3);  // in [1, kSampThreads * kRegChunks]
+    const char* base = reinterpret_cast<const char*>(row);  // (uniform; 32-bit byte offsets below)
+#pragma unroll
+    for (int j = 0; j < kRegChunks; ++j) {
+      const uint32_t c = min(static_cast<uint32_t>(tid + j * kSampThreads), static_cast<uint32_t>(n8 - 1));
+      ch[j] = *reinterpret_cast<const u32x4*>(base + (c << 4));
+    }
+  }
+
+  __device__ __forceinline__ int64_t candidates(u32x4 (&ch)[kRegChunks], float temp, int64_t k, double p,
+                                                double u) {
+    constexpr uint32_t kNegKeys = Inf16<T>::kNegKey * 0x10001u;  // two -inf keys
+    constexpr int kMaxWords = (kRegChunks + 1) / 2;                // chunk maxima words per thread
+    const int n8 = static_cast<int>(a.V >> 3);
+    const uint32_t k_eff = temp <= 0.f ? 1u : static_cast<uint32_t>(k);  // in [1, kFastK]
+    // LDS: red = s.cnt ([0, 16) wave maxima, [16, 32) minima, [32, 48) bin
+    // sums, [48] samples above the bin, [49] candidates, [64, 80) the
+    // low-bits histogram); hist = s.wsum as kSelBins counts; cmx = each
+    // thread's chunk maxima (two 16-bit keys a word, word w of thread t at
+    // w * kSampThreads + t) from s.pcnt on; staged chunks after them; the
+    // candidates in s.keys[kGatherCap, kCap); ranked keys in s.keys[0, k)
+    // once cmx is no longer read.
+    static_assert(offsetof(SampleLds, pcnt) + sizeof(uint32_t) * kMaxWords * kSampThreads +
+                          (sizeof(u32x4) + sizeof(uint32_t)) * kStageCap <=
+                      offsetof(SampleLds, keys) + sizeof(uint64_t) * kGatherCap,
+                  "chunk maxima and staged chunks end before the candidates");
+    uint32_t* red = s.cnt;
+    uint32_t* hist = reinterpret_cast<uint32_t*>(s.wsum);
+    uint32_t* cmx = s.pcnt;
+    u32x4* stage = reinterpret_cast<u32x4*>(cmx + kMaxWords * kSampThreads);
+    uint32_t* sid = reinterpret_cast<uint32_t*>(stage + kStageCap);
+    uint64_t* cand = s.keys + kGatherCap;
+#pragma unroll
+    for (int b = tid; b < kSelBins; b += kSampThreads) hist[b] = 0;
+    if (tid < 16) red[64 + tid] = 0;
+    if (tid == 0) s.n_gather = 0;
+    __syncthreads();
+    // 1. keys, samples, chunk maxima, the row's largest and smallest key
+    // A chunk past the row's end (its load was clamped onto the row's last
+    // chunk) counts as -inf in the maxima, so it is never sampled and never
+    // gathered; its duplicate keys cannot lower the minimum below a real one.
+    uint32_t t0 = 0, mn = 0xFFFFFFFFu, pend = 0;  // packed: each half-lane's largest and smallest key
+#pragma unroll
+    for (int j = 0; j < kRegChunks; ++j) {
+      const u32x4 w = ch[j];
+      const uint32_t x0 = pk_key(w[0]), x1 = pk_key(w[1]), x2 = pk_key(w[2]), x3 = pk_key(w[3]);
+      ch[j] = u32x4{x0, x1, x2, x3};
+      uint32_t mj = pk_max(pk_max(x0, x1), pk_max(x2, x3));
+      if (tid + j * kSampThreads >= n8) mj = kNegKeys;
+      t0 = pk_max(t0, mj);
+      mn = pk_min(mn, pk_min(pk_min(x0, x1), pk_min(x2, x3)));
+      if (j & 1) cmx[(j >> 1) * kSampThreads + tid] = pend | (hmax(mj) << 16);
+      else pend = hmax(mj);
+    }
+    if (kRegChunks & 1) cmx[(kMaxWords - 1) * kSampThreads + tid] = pend;
+    uint32_t wmx = hmax(t0), wmn = min(mn & 0xFFFFu, mn >> 16);
+    for (int o = 32; o > 0; o >>= 1) {
+      wmx = max(wmx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wmx), o, 64)));
+      wmn = min(wmn, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wmn), o, 64)));
+    }
+    if (lane == 0) {
+      red[wave] = wmx;
+      red[16 + wave] = wmn;
+    }
+    const uint32_t s0 = t0 & 0xFFFFu, s1 = t0 >> 16;  // this thread's two samples
+    atomicAdd(&hist[s0 >> 4], 1u);
+    atomicAdd(&hist[s1 >> 4], 1u);
+    __syncthreads();
+    uint32_t kmx = 0, kmn = 0xFFFFu;
+#pragma unroll
+    for (int w = 0; w < kSampWaves; ++w) {
+      kmx = max(kmx, red[w]);
+      kmn = min(kmn, red[16 + w]);
+    }
+    if (kmx >= Inf16<T>::kPosKey || kmn < Inf16<T>::kNegKey || kmx <= Inf16<T>::kNegKey) return -1;  // (uniform)
+    // 2. thread t holds bins 4095 - 4t down to 4092 - 4t: a scan in descending order
+    const int b0 = kSelBins - 1 - 4 * tid;
+    const uint32_t h0 = hist[b0], h1 = hist[b0 - 1], h2 = hist[b0 - 2], h3 = hist[b0 - 3];
+    const uint32_t mine = h0 + h1 + h2 + h3;
+    uint32_t incl = mine;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t up = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += up;
+    }
+    if (lane == 63) red[32 + wave] = incl;
+    __syncthreads();
+    uint32_t excl = incl - mine;
+    for (int w = 0; w < wave; ++w) excl += red[32 + w];
+    if (excl < k_eff && excl + mine >= k_eff) {  // the one thread whose bins reach k_eff
+      const uint32_t c0 = excl + h0, c1 = c0 + h1, c2 = c1 + h2;
+      s.found_bucket = c0 >= k_eff ? b0 : c1 >= k_eff ? b0 - 1 : c2 >= k_eff ? b0 - 2 : b0 - 3;
+      red[48] = c0 >= k_eff ? excl : c1 >= k_eff ? c0 : c2 >= k_eff ? c1 : c2;  // samples above that bin
+    }
+    __syncthreads();
+    const uint32_t bin = static_cast<uint32_t>(s.found_bucket), need = k_eff - red[48];
+    if ((s0 >> 4) == bin) atomicAdd(&red[64 + (s0 & 15u)], 1u);
+    if ((s1 >> 4) == bin) atomicAdd(&red[64 + (s1 & 15u)], 1u);
+    __syncthreads();
+    uint32_t low = 0, c = 0;
+#pragma unroll
+    for (int b = 15; b >= 0; --b) {  // the low bits where the count from the top reaches `need`
+      const uint32_t c2 = c + red[64 + b];
+      if (c < need && c2 >= need) low = static_cast<uint32_t>(b);
+      c = c2;
+    }
+    uint32_t K = (bin << 4) | low;  // >= the -inf key: the row holds no NaN
+    if (K == 0x8000u) K = 0x7FFFu;   // +0: -0 has the same value
+    // 3. the chunks holding a key >= K (from the chunk maxima), staged in LDS
+    uint32_t mask = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < kMaxWords; ++w2) {
+      const uint32_t v = cmx[w2 * kSampThreads + tid];
+      mask |= ((v & 0xFFFFu) >= K ? 1u : 0u) << (2 * w2);
+      if (2 * w2 + 1 < kRegChunks) mask |= ((v >> 16) >= K ? 1u : 0u) << (2 * w2 + 1);
+    }
+    const int nv = n8 > tid ? (n8 - tid + kSampThreads - 1) / kSampThreads : 0;  // this lane's chunks in the row
+    mask &= (1u << nv) - 1u;                                                      // (nv <= kRegChunks < 32)
+    uint32_t wmask = mask;
+    for (int o = 1; o < 64; o <<= 1) wmask |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(wmask), o, 64));
+    wmask = __builtin_amdgcn_readfirstlane(wmask);  // (uniform: the wave's hot chunks)
+#pragma unroll
+    for (int j = 0; j < kRegChunks; ++j) {
+      if (!(wmask & (1u << j))) continue;  // (uniform)
+      const bool hot = (mask >> j) & 1u;
+      const uint64_t b = __ballot(hot);
+      uint32_t base0 = 0;
+      if (lane == 0) base0 = atomicAdd(&s.n_gather, static_cast<uint32_t>(__popcll(b)));
+      const uint32_t base = __builtin_amdgcn_readfirstlane(base0);
+      if (hot) {
+        const uint32_t at = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(b >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b), 0u));
+        if (at < static_cast<uint32_t>(kStageCap)) {
+          stage[at] = ch[j];
+          sid[at] = static_cast<uint32_t>(tid + j * kSampThreads);
+        }
+      }
+    }
+    __syncthreads();
+    const uint32_t nst = s.n_gather;
+    if (nst > static_cast<uint32_t>(kStageCap)) return -1;  // (uniform)
+    const float kc0 = 1.4426950408889634f / t;  // (16-bit rows order by the logit)
+    // 4. wave 0: the staged chunks' keys >= K become candidates; for at most
+    // 64 it ranks and decides at once
+    if (wave == 0) {
+      uint32_t nc = 0;  // (uniform) candidates written
+      for (uint32_t i0 = 0; i0 < nst; i0 += 64) {
+        const uint32_t i = i0 + lane;
+        const u32x4 w = i < nst ? stage[i] : u32x4{0, 0, 0, 0};
+        const uint32_t id = i < nst ? sid[i] : 0u;
+        uint32_t take = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t key = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu);
+          take |= (key >= K ? 1u : 0u) << e;
+        }
+        const uint32_t cnt = __popc(take);
+        uint32_t pre = 0, tot = 0;  // exclusive prefix of cnt (<= 8) over the wave, by bit planes
+#pragma unroll
+        for (int bp = 0; bp < 4; ++bp) {
+          const uint64_t bb = __ballot((cnt >> bp) & 1u);
+          pre += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bb >> 32),
+                                           __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bb), 0u))
+                 << bp;
+          tot += static_cast<uint32_t>(__popcll(bb)) << bp;
+        }
+        uint32_t at = nc + pre;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if ((take >> e) & 1u) {
+            const uint32_t key = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu);
+            if (at < static_cast<uint32_t>(kGatherCap)) cand[at] = rank_key(lo_f<T>(key_bits(key)), 8 * int64_t{id} + e);
+            ++at;
+          }
+        }
+        nc += tot;
+      }
+      const uint32_t nc8 = (nc + 7) & ~7u;  // padded with keys that rank below every candidate
+      if (nc + lane < min(nc8, static_cast<uint32_t>(kGatherCap))) cand[nc + lane] = ~uint64_t{0};
+      int64_t token = -2;  // (more than 64 candidates: the block ranks them below)
+      if (nc <= 64) {
+        const int lk = static_cast<int>(min(k_eff, nc));  // (nc >= k_eff: at least k_eff samples are >= K)
+        const uint64_t kv = lane < static_cast<int>(nc) ? cand[lane] : ~uint64_t{0};
+        int rank = 0;
+        for (uint32_t q = 0; q < nc8; q += 8) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) rank += cand[q + i] < kv ? 1 : 0;
+        }
+        if (lane >= static_cast<int>(nc)) rank = lane;  // (distinct from the ranks below nc)
+        const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_ds_permute(rank * 4, static_cast<int>(kv)));
+        const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_ds_permute(rank * 4, static_cast<int>(kv >> 32)));
+        const uint64_t sorted = (static_cast<uint64_t>(hi) << 32) | lo;  // lane e: rank e
+        const uint64_t top = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(hi))))
+                              << 32) |
+                             static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lo)));
+        token = temp <= 0.f ? static_cast<int64_t>(static_cast<uint32_t>(top))  // greedy: rank 0
+                            : decide_lanes(sorted, lk, key_of_rank(top), kc0, p, u);
+      }
+      if (lane == 0) {
+        s.found_index = token;
+        red[49] = nc;
+      }
+    }
+    __syncthreads();
+    if (s.found_index != -2) return s.found_index;  // (uniform)
+    // 5. more than 64 candidates: every thread ranks, wave 0 decides
+    const uint32_t n = red[49];
+    if (n > static_cast<uint32_t>(kGatherCap)) return -1;
+    const int lk = static_cast<int>(min(k_eff, n));
+    for (int i = tid; i < static_cast<int>(n); i += kSampThreads) {  // each candidate's rank among them
+      const uint64_t kv = cand[i];
+      int rank = 0, q = 0;
+      for (; q + 4 <= static_cast<int>(n); q += 4)
+        rank += (cand[q] < kv ? 1 : 0) + (cand[q + 1] < kv ? 1 : 0) + (cand[q + 2] < kv ? 1 : 0) +
+                (cand[q + 3] < kv ? 1 : 0);
+      for (; q < static_cast<int>(n); ++q) rank += cand[q] < kv ? 1 : 0;
+      if (rank < lk) s.keys[rank] = kv;
+    }
+    __syncthreads();
+    if (temp <= 0.f) return static_cast<uint32_t>(s.keys[0]);  // greedy: the first index of the maximum
+    kmax = key_of_rank(s.keys[0]);
+    kc = kc0;
+    if (wave == 0) {
+      const int64_t token = decide_wave(lk, p, u);
+      if (lane == 0) s.found_index = token;
+    }
+    __syncthreads();
+    return s.found_index;
+  }
+
+  // decide_on_prefix(lk, lk, ...) on ranks held one per lane (lane e: rank e,
+  // lk <= 64), with the row's maximum km: the same masses and comparisons.
+  __device__ __forceinline__ int64_t decide_lanes(uint64_t sorted, int lk, float km, float kcv, double p,
+                                                  double u) const {
+    const uint64_t m = lane < lk ? mass_of(key_of_rank(sorted), km, kcv) : 0;
+    uint64_t incl = m;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t up = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += up;
+    }
+    const uint64_t excl = incl - m;
+    const uint64_t z = __shfl(incl, 63, 64);
+    const double tp = p * static_cast<double>(z);
+    const uint64_t hp = __ballot(lane < lk && static_cast<double>(incl) > tp &&
+                                 (lane == 0 || !(static_cast<double>(excl) > tp)));
+    int lim = lk;
+    uint64_t kept = z;
+    if (hp != 0) {
+      const int src = __builtin_ctzll(hp);
+      lim = src + 1;
+      kept = __shfl(incl, src, 64);
+    }
+    const double tu = u * static_cast<double>(kept);
+    const uint64_t hu = __ballot(lane < lim && static_cast<double>(incl) >= tu &&
+                                 (lane == 0 || !(static_cast<double>(excl) >= tu)));
+    if (hu == 0) return -1;
+    return static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(sorted)), __builtin_ctzll(hu), 64));
+  }
+
+  // decide_on_prefix(lk, lk, ...) in one wave, on s.keys[0, lk) (lk <= 512):
+  // lane L holds ranks [8L, 8L + 8); the masses are exact integers, so the
+  // running sums, and every comparison with the targets, are the same.
+  __device__ __forceinline__ int64_t decide_wave(int lk, double p, double u) const {
+    uint64_t m[8];
+    uint64_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = 8 * lane + i;
+      m[i] = e < lk ? mass_key(key_of_rank(s.keys[e])) : 0;
+      mine += m[i];
+    }
+    uint64_t incl = mine;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t up = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += up;
+    }
+    const uint64_t z = __shfl(incl, 63, 64);
+    // top-p: the first rank whose running mass exceeds p * z (exactly one lane holds it)
+    const double tp = p * static_cast<double>(z);
+    uint64_t cum = incl - mine;
+    int pos_p = -1;
+    uint64_t cum_p = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = 8 * lane + i;
+      const uint64_t c2 = cum + m[i];
+      if (e < lk && pos_p < 0 && static_cast<double>(c2) > tp && (e == 0 || !(static_cast<double>(cum) > tp))) {
+        pos_p = e;
+        cum_p = c2;
+      }
+      cum = c2;
+    }
+    const uint64_t hp = __ballot(pos_p >= 0);
+    int lim = lk;
+    uint64_t kept = z;
+    if (hp != 0) {
+      const int src = __builtin_ctzll(hp);
+      lim = __shfl(pos_p, src, 64) + 1;
+      kept = __shfl(cum_p, src, 64);
+    }
+    // the pick: the first kept rank whose running mass reaches u * kept
+    const double tu = u * static_cast<double>(kept);
+    cum = incl - mine;
+    int pos = -1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = 8 * lane + i;
+      const uint64_t c2 = cum + m[i];
+      if (e < lim && pos < 0 && static_cast<double>(c2) >= tu && (e == 0 || !(static_cast<double>(cum) >= tu)))
+        pos = e;
+      cum = c2;
+    }
+    const uint64_t hu = __ballot(pos >= 0);
+    if (hu == 0) return -1;
+    const int at = __shfl(pos, __builtin_ctzll(hu), 64);
+    return static_cast<int64_t>(static_cast<uint32_t>(s.keys[at]));
+  }
+
   // All three decisions from one histogram of every element (count and
   // mass): each decision's kept set is a prefix in rank order -- full buckets,
   // then a known prefix of one sorted bucket -- so only the buckets where a
   // cut or the pick falls are gathered. False if such a bucket is larger
   // than LDS holds (the caller then runs the per-decision path).
-  __device__ bool fast(float lo, int64_t k, bool cut_k, double p, double u, int64_t& token) {
+  __device__ __forceinline__ bool fast(float lo, int64_t k, bool cut_k, double p, double u, int64_t& token) {
     // lo: the smallest finite key
     const float scale = kmax > lo ? static_cast<float>(kBuckets - 1) / (kmax - lo) : 0.f;
     for (int b = tid; b < kBuckets; b += kSampThreads) {
@@ -481,10 +877,10 @@ struct RowSampler {
   // The target is target_abs, or frac * (total candidate weight) when
   // use_frac. Returns false when no candidate reaches it.
   template <typename Keep>
-  __device__ bool select(Keep keep, bool by_mass, bool ge, bool use_frac, double frac, double target_abs,
+  __device__ __forceinline__ bool select(Keep keep, bool by_mass, bool ge, bool use_frac, double frac, double target_abs,
                          float lo, float hi, float& rx, int64_t& ri, uint64_t& rcum) {
-    float lv_hi[kMaxLevels], lv_scale[kMaxLevels];
-    int lv_b[kMaxLevels];
+    float lv_hi[kMaxLevels] = {}, lv_scale[kMaxLevels] = {};
+    int lv_b[kMaxLevels] = {};
     int levels = 0;
     uint64_t base = 0;
     double target = target_abs;
@@ -496,10 +892,14 @@ struct RowSampler {
       if (!(f < static_cast<float>(kBuckets - 1))) return kBuckets - 1;
       return f > 0.f ? static_cast<int>(f) : 0;
     };
+    // (the level arrays are only ever indexed by unrolled constants, so they
+    // stay in registers)
     auto in_levels = [&](float x) {
-      for (int l = 0; l < levels; ++l)
-        if (bucket_of(x, lv_hi[l], lv_scale[l]) != lv_b[l]) return false;
-      return true;
+      bool in = true;
+#pragma unroll
+      for (int l = 0; l < kMaxLevels; ++l)
+        if (l < levels && bucket_of(x, lv_hi[l], lv_scale[l]) != lv_b[l]) in = false;
+      return in;
     };
     auto reached = [&](uint64_t cum) {
       const double c = static_cast<double>(cum);
@@ -658,9 +1058,14 @@ struct RowSampler {
         return ri >= 0;
       }
       if (levels == kMaxLevels) return false;  // distinct values closer than 4 splits resolve: not expected
-      lv_hi[levels] = hi;
-      lv_scale[levels] = scale;
-      lv_b[levels] = fb;
+#pragma unroll
+      for (int l = 0; l < kMaxLevels; ++l) {
+        if (l == levels) {
+          lv_hi[l] = hi;
+          lv_scale[l] = scale;
+          lv_b[l] = fb;
+        }
+      }
       ++levels;
       lo = bmin;
       hi = bmax;
@@ -673,9 +1078,27 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   SampleLds& s = *reinterpret_cast<SampleLds*>(lds_raw);
   const int64_t r = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (uniform: an SGPR)
   const float temp = a.temp[r * a.temp_s];
   RowSampler<T, UNIT> rs{a, s, static_cast<const T*>(a.logits) + r * a.ls0, fmaxf(temp, 1e-5f), 0.f, tid, lane, wave, 0.f, 0.f};
+
+  // Top-k and greedy rows of a 16-bit row that fits the registers: the
+  // candidate pass decides from one read of the row, or sends it on.
+  if constexpr (UNIT && sizeof(T) == 2) {
+    if (a.cand && rs.chunked() && a.V <= kRegMaxV) {
+      u32x4 ch[kRegChunks];
+      rs.load_row(ch);  // (in flight while the row's parameters arrive)
+      const int64_t k = load_int(a.topk, a.topk_dt, r * a.topk_s);
+      if (candidate_row(a, temp, k)) {
+        const int64_t token = rs.candidates(ch, temp, k, a.topp[r * a.topp_s], a.unif[r * a.unif_s]);
+        if (token >= 0) {
+          if (tid == 0) a.out[r * a.out_s] = token;
+          return;
+        }
+      }
+    }
+  }
 
   // Row maximum and its first index (rank 0), the finite minimum, the last
   // index of the minimum (the last rank), and the first NaN.
@@ -847,6 +1270,15 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
 
 using namespace tsa;
 
+namespace {
+// TSA_SAMPLE_CANDIDATES=0 turns the candidate pass off (every row then takes
+// the histogram paths; the tokens are the same).
+bool candidates_enabled() {
+  const char* e = getenv("TSA_SAMPLE_CANDIDATES");
+  return !(e && e[0] == '0');
+}
+}  // namespace
+
 extern "C" int tsa_sample_tokens(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature,
                                  const tsa_view* top_k, const tsa_view* top_p, const tsa_view* uniforms,
                                  void* stream) {
@@ -873,6 +1305,7 @@ extern "C" int tsa_sample_tokens(const tsa_view* out, const tsa_view* logits, co
   a.unif = static_cast<const float*>(uniforms->data); a.unif_s = uniforms->stride[0];
   a.out = static_cast<int64_t*>(out->data); a.out_s = out->stride[0];
   hipStream_t st = static_cast<hipStream_t>(stream);
+  a.cand = candidates_enabled() ? 1 : 0;
   const size_t lds = sizeof(SampleLds);
   switch (logits->dtype) {
     case TSA_BF16:
