@@ -490,7 +490,8 @@ def bench_mixed(name, steps, warmup, copies=3):
 def bench_sampling(steps, warmup, batch=64, vocab=151936):
     """sample_tokens over a Qwen3-vocab batch: bf16 logits (N(0, 2.5) plus a
     few boosted tokens per row), temperature 0.8, seeded uniforms; three
-    filter settings. One launch per call."""
+    filter settings. One launch per call, timed eagerly and replayed from a
+    captured graph."""
     from tinyserver_amd.kernels import sample_tokens
 
     dev = torch.device("cuda:0")
@@ -513,12 +514,35 @@ def bench_sampling(steps, warmup, batch=64, vocab=151936):
             sample_tokens(logits, temperature, top_k, top_p, uniforms, out=out)
 
         us = time_region(call, steps, warmup)[0] * 1e3
-        cases[label] = {"us_per_call": us, "logits_gbs": nbytes / (us * 1e-6) / 1e9,
-                        "roofline": {**_roof_hbm(nbytes, us), "kernel": "sample_tokens_kernel"}}
+        gus = _graph_us_per_call(lambda: sample_tokens(logits, temperature, top_k, top_p, uniforms, out=out),
+                                 steps, warmup)
+        cases[label] = {"us_per_call": us, "graph_us_per_call": gus, "logits_gbs": nbytes / (gus * 1e-6) / 1e9,
+                        "roofline": {**_roof_hbm(nbytes, gus), "kernel": "sample_tokens_kernel",
+                                     "note": "per call in a captured graph of 20 calls (the eager "
+                                             "us_per_call also holds the Python enqueue)"}}
     top_k.fill_(50)
     top_p.fill_(0.9)
     return {"workload": f"sample_tokens bs{batch} vocab{vocab} bf16", "batch": batch, "vocab": vocab, **cases}, \
         (logits, temperature, top_k, top_p, uniforms)
+
+
+def _graph_us_per_call(fn, steps, warmup, calls=20):
+    """fn() x `calls` captured in one HIP graph, replayed: the GPU time per
+    call without the host's enqueue cost."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    reps = max(2, steps // calls)
+    ms = time_region(lambda i: graph.replay(), reps, max(1, warmup // calls))[0]
+    del graph
+    return ms * 1e3 / calls
 
 
 def copy_probe(nbytes=1 << 30, reps=5):

@@ -314,3 +314,30 @@ def test_candidate_path_short_and_odd_rows(v):
     k = min(5, v - 1)
     _compare(rows, [1.0, 0.0, 0.7, 1.0, 1.3, 0.9], [k, 0, 1, k, 3 if v > 3 else 1, 2], [0.9, 1.0, 1.0, 0.5, 1.0, 0.8],
              [0.1, 0.5, 0.6, 0.99, 0.3, 0.0], dtype=torch.bfloat16, what=f"v={v}")
+
+
+def test_graph_replays_match_eager():
+    """sample_tokens captured in a HIP graph (a serving step's usual form):
+    three replays, with eager work and a synchronisation between them, each
+    equal to the eager call, for candidate-pass and histogram-path rows."""
+    logits, temperature, top_k, top_p, uniforms = _qwen3_batch(26, b=16)
+    t = lambda x, dt: torch.tensor(x, dtype=dt, device=DEV)
+    args = (logits.to(DEV, torch.bfloat16), t(temperature, torch.float32), t(top_k, torch.int64),
+            t(top_p, torch.float32), t(uniforms, torch.float32))
+    eager = sample_tokens(*args).cpu()
+    out = torch.full((16,), -1, dtype=torch.int64, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        sample_tokens(*args, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sample_tokens(*args, out=out)
+    for rep in range(3):
+        out.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), eager), (rep, out.tolist(), eager.tolist())
+        sample_tokens(*args)  # eager work between replays
+        torch.cuda.synchronize()

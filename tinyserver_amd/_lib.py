@@ -8,6 +8,7 @@ tensor's device. There is no CPU fallback: a missing library raises.
 from __future__ import annotations
 
 import ctypes
+import struct
 from ctypes import POINTER, c_double, c_int, c_int32, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
@@ -92,22 +93,23 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+# One struct.pack per view (the layout of tsa_view; unused entries stay zero)
+# instead of ctypes field sets, which cost microseconds per call.
+_PACK = [struct.Struct("<Q" + "q" * nd + "x" * (8 * (4 - nd)) + "q" * nd + "x" * (8 * (4 - nd)) + "ii")
+         for nd in range(5)]
+
+
 def view(t: torch.Tensor | None) -> TsaView | None:
     """Describe a tensor for the C ABI (None stays None -> NULL)."""
     if t is None:
         return None
-    if t.dim() > 4:
-        raise ValueError(f"tensors of rank > 4 are not supported (got {t.dim()})")
-    if t.dtype not in _DTYPES:
+    nd = t.dim()
+    if nd > 4:
+        raise ValueError(f"tensors of rank > 4 are not supported (got {nd})")
+    dt = _DTYPES.get(t.dtype)
+    if dt is None:
         raise ValueError(f"unsupported dtype {t.dtype}")
-    v = TsaView()
-    v.data = t.data_ptr() if t.numel() else None
-    for i, (n, s) in enumerate(zip(t.shape, t.stride())):
-        v.size[i] = n
-        v.stride[i] = s
-    v.ndim = t.dim()
-    v.dtype = _DTYPES[t.dtype]
-    return v
+    return TsaView.from_buffer_copy(_PACK[nd].pack(t.data_ptr() if t.numel() else 0, *t.shape, *t.stride(), nd, dt))
 
 
 def ref(v: TsaView | None):
@@ -141,4 +143,5 @@ def require_device(*tensors: torch.Tensor) -> torch.device:
 
 
 def stream_of(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw handle of the device's current stream (no Stream object made)."""
+    return torch._C._cuda_getCurrentRawStream(device.index if device.index is not None else torch.cuda.current_device())

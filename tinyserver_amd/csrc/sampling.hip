@@ -96,8 +96,9 @@ __device__ __forceinline__ uint64_t mass_of(float kv, float kmax, float kc) {
 constexpr int kRegChunks = 19;  // 8-logit chunks per thread: the row stays in registers
 constexpr int64_t kRegMaxV = int64_t{kSampThreads} * kRegChunks * 8;  // 155,648 logits
 constexpr int64_t kFastK = 512;                                        // the largest top_k it takes
-constexpr int kGatherCap = kCap / 2;  // candidates it may gather: keys[kGatherCap, kCap)
-constexpr int kStageCap = 256;        // chunks holding a candidate it may stage
+constexpr int kWaveStage = 64;    // chunks holding a candidate one wave may stage
+constexpr int kCandOff = 4608;    // the candidates: keys[kCandOff, kCap)
+constexpr int kGatherCap = kCap - kCandOff;
 constexpr int kSelBins = 4096;        // 12-bit key prefixes
 
 // The rows the candidate pass takes: greedy rows (rank 0) and rows whose
@@ -123,6 +124,10 @@ __device__ __forceinline__ uint32_t pk_max(uint32_t x, uint32_t y) {
 __device__ __forceinline__ uint32_t pk_min(uint32_t x, uint32_t y) {
   return __builtin_bit_cast(uint32_t,
                             __builtin_elementwise_min(__builtin_bit_cast(u16x2, x), __builtin_bit_cast(u16x2, y)));
+}
+__device__ __forceinline__ uint32_t pk_smax(uint32_t x, uint32_t y) {  // signed 16-bit halves
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_max(__builtin_bit_cast(s16x2, x), __builtin_bit_cast(s16x2, y)));
 }
 __device__ __forceinline__ uint32_t hmax(uint32_t w) { return max(w & 0xFFFFu, w >> 16); }
 // A key's 16-bit float bits.
@@ -459,12 +464,14 @@ struct RowSampler {
   // The candidate pass for a top-k or greedy row of a 16-bit row of at most
   // kRegMaxV logits (chunked). load_row reads the row into registers (issued
   // before the row's parameters arrive); candidates then:
-  //   1. keys every logit; each half-lane's largest key is a sample (2048
-  //      distinct elements), and the row's largest and smallest keys flag a
-  //      NaN, a +inf or a row of -inf (those go on to the histogram paths);
+  //   1. takes each half-lane's largest logit as a sample (2048 distinct
+  //      elements) and each chunk's largest key into LDS, from packed signed
+  //      maxima of the raw patterns, and flags a NaN, a +inf or no sign of a
+  //      value above -inf (those rows go on to the histogram paths);
   //   2. K = the k-th largest sample (12-bit prefix histogram, then the low 4
   //      bits of the samples in that prefix), so at least k elements have key
-  //      >= K; +0's key is lowered to take -0 too;
+  //      >= K; +0's key is lowered to take -0 too; a cut at or below zero
+  //      recomputes the chunk maxima from every key;
   //   3. finds the chunks holding a key >= K from each chunk's maximum (kept
   //      in LDS by step 1), skipping with a scalar test every chunk no lane
   //      of the wave holds one in, and stages those chunks in LDS (one atomic
@@ -475,84 +482,99 @@ struct RowSampler {
   //      to its rank's lane (ds_permute) and decides there (decide_lanes);
   //   5. more candidates are ranked by the block, and decide_wave decides;
   //      a greedy row takes rank 0.
-  // The token, or -1 to send the row on (more than kStageCap chunks or
-  // kGatherCap candidates, a non-finite row, or a pick past the candidates).
+  // The token, or -1 to send the row on (more than kWaveStage chunks in a
+  // wave or kGatherCap candidates, a non-finite row, or a pick past the
+  // candidates).
   __device__ __forceinline__ void load_row(u32x4 (&ch)[kRegChunks]) const {
+    // Chunk min(j * kSampThreads + tid, n8 - 1) of the row: a uniform base
+    // (the first chunk of the block's j-th span, or the row's last chunk)
+    // plus a clamped 32-bit lane offset.
     const int n8 = static_cast<int>(a.V >> 3);  // in [1, kSampThreads * kRegChunks]
-    const char* base = reinterpret_cast<const char*>(row);  // (uniform; 32-bit byte offsets below)
+    const char* base = reinterpret_cast<const char*>(row);
+    const uint32_t toff = static_cast<uint32_t>(tid) << 4;
 #pragma unroll
     for (int j = 0; j < kRegChunks; ++j) {
-      const uint32_t c = min(static_cast<uint32_t>(tid + j * kSampThreads), static_cast<uint32_t>(n8 - 1));
-      ch[j] = *reinterpret_cast<const u32x4*>(base + (c << 4));
+      const int cj = min(j * kSampThreads, n8 - 1);                      // (uniform)
+      const uint32_t lim = static_cast<uint32_t>(n8 - 1 - cj) << 4;      // (uniform)
+      ch[j] = *reinterpret_cast<const u32x4*>(base + (static_cast<int64_t>(cj) << 4) + min(toff, lim));
     }
   }
 
   __device__ __forceinline__ int64_t candidates(u32x4 (&ch)[kRegChunks], float temp, int64_t k, double p,
                                                 double u) {
-    constexpr uint32_t kNegKeys = Inf16<T>::kNegKey * 0x10001u;  // two -inf keys
+    constexpr uint32_t kNegKeys = Inf16<T>::kNegKey * 0x10001u;   // two -inf keys
+    constexpr uint32_t kNegPair = Inf16<T>::kNegBits * 0x10001u;  // two -inf patterns
     constexpr int kMaxWords = (kRegChunks + 1) / 2;                // chunk maxima words per thread
     const int n8 = static_cast<int>(a.V >> 3);
     const uint32_t k_eff = temp <= 0.f ? 1u : static_cast<uint32_t>(k);  // in [1, kFastK]
     // LDS: red = s.cnt ([0, 16) wave maxima, [16, 32) minima, [32, 48) bin
     // sums, [48] samples above the bin, [49] candidates, [64, 80) the
-    // low-bits histogram); hist = s.wsum as kSelBins counts; cmx = each
+    // low-bits histogram, [80, 96) chunks staged per wave); hist = s.wsum as kSelBins counts; cmx = each
     // thread's chunk maxima (two 16-bit keys a word, word w of thread t at
     // w * kSampThreads + t) from s.pcnt on; staged chunks after them; the
-    // candidates in s.keys[kGatherCap, kCap); ranked keys in s.keys[0, k)
+    // candidates in s.keys[kCandOff, kCap); ranked keys in s.keys[0, k)
     // once cmx is no longer read.
     static_assert(offsetof(SampleLds, pcnt) + sizeof(uint32_t) * kMaxWords * kSampThreads +
-                          (sizeof(u32x4) + sizeof(uint32_t)) * kStageCap <=
-                      offsetof(SampleLds, keys) + sizeof(uint64_t) * kGatherCap,
+                          (sizeof(u32x4) + sizeof(uint32_t)) * kWaveStage * kSampWaves <=
+                      offsetof(SampleLds, keys) + sizeof(uint64_t) * kCandOff,
                   "chunk maxima and staged chunks end before the candidates");
     uint32_t* red = s.cnt;
     uint32_t* hist = reinterpret_cast<uint32_t*>(s.wsum);
     uint32_t* cmx = s.pcnt;
     u32x4* stage = reinterpret_cast<u32x4*>(cmx + kMaxWords * kSampThreads);
-    uint32_t* sid = reinterpret_cast<uint32_t*>(stage + kStageCap);
-    uint64_t* cand = s.keys + kGatherCap;
+    uint32_t* sid = reinterpret_cast<uint32_t*>(stage + kWaveStage * kSampWaves);
+    uint64_t* cand = s.keys + kCandOff;
 #pragma unroll
     for (int b = tid; b < kSelBins; b += kSampThreads) hist[b] = 0;
     if (tid < 16) red[64 + tid] = 0;
-    if (tid == 0) s.n_gather = 0;
     __syncthreads();
-    // 1. keys, samples, chunk maxima, the row's largest and smallest key
+    // 1. samples, chunk maxima and the row's flags from the raw 16-bit
+    // patterns, two per packed op. A signed 16-bit maximum of the raw
+    // patterns is the true maximum of any set holding a value >= +0 (sign-
+    // magnitude order is integer order there, and every negative pattern is
+    // below every non-negative one); in a set of negatives it is some element
+    // of the set, which is all a sample needs. A positive NaN or +inf shows in
+    // it; a negative NaN shows in the unsigned maximum (above -inf's pattern).
     // A chunk past the row's end (its load was clamped onto the row's last
-    // chunk) counts as -inf in the maxima, so it is never sampled and never
-    // gathered; its duplicate keys cannot lower the minimum below a real one.
-    uint32_t t0 = 0, mn = 0xFFFFFFFFu, pend = 0;  // packed: each half-lane's largest and smallest key
+    // chunk) counts as -inf, so it is never sampled or gathered.
+    uint32_t t0 = 0x80008000u, um = 0, pend = 0;  // packed: each half-lane's signed and unsigned maxima
 #pragma unroll
     for (int j = 0; j < kRegChunks; ++j) {
       const u32x4 w = ch[j];
-      const uint32_t x0 = pk_key(w[0]), x1 = pk_key(w[1]), x2 = pk_key(w[2]), x3 = pk_key(w[3]);
-      ch[j] = u32x4{x0, x1, x2, x3};
-      uint32_t mj = pk_max(pk_max(x0, x1), pk_max(x2, x3));
-      if (tid + j * kSampThreads >= n8) mj = kNegKeys;
-      t0 = pk_max(t0, mj);
-      mn = pk_min(mn, pk_min(pk_min(x0, x1), pk_min(x2, x3)));
-      if (j & 1) cmx[(j >> 1) * kSampThreads + tid] = pend | (hmax(mj) << 16);
-      else pend = hmax(mj);
+      uint32_t sm = pk_smax(pk_smax(w[0], w[1]), pk_smax(w[2], w[3]));
+      um = pk_max(um, pk_max(pk_max(w[0], w[1]), pk_max(w[2], w[3])));
+      if (__builtin_expect((j + 1) * kSampThreads > n8, 0)) {  // (uniform: the row may end in this span)
+        if (tid + j * kSampThreads >= n8) sm = kNegPair;
+      }
+      t0 = pk_smax(t0, sm);
+      const uint32_t cm = hmax(pk_key(sm));  // the chunk's largest key if it holds a value >= +0
+      if (j & 1) cmx[(j >> 1) * kSampThreads + tid] = pend | (cm << 16);
+      else pend = cm;
     }
     if (kRegChunks & 1) cmx[(kMaxWords - 1) * kSampThreads + tid] = pend;
-    uint32_t wmx = hmax(t0), wmn = min(mn & 0xFFFFu, mn >> 16);
+    const uint32_t tk = pk_key(t0);
+    uint32_t wmx = hmax(tk), wum = hmax(um);
     for (int o = 32; o > 0; o >>= 1) {
       wmx = max(wmx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wmx), o, 64)));
-      wmn = min(wmn, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wmn), o, 64)));
+      wum = max(wum, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wum), o, 64)));
     }
     if (lane == 0) {
       red[wave] = wmx;
-      red[16 + wave] = wmn;
+      red[16 + wave] = wum;
     }
-    const uint32_t s0 = t0 & 0xFFFFu, s1 = t0 >> 16;  // this thread's two samples
+    const uint32_t s0 = tk & 0xFFFFu, s1 = tk >> 16;  // this thread's two samples (keys)
     atomicAdd(&hist[s0 >> 4], 1u);
     atomicAdd(&hist[s1 >> 4], 1u);
     __syncthreads();
-    uint32_t kmx = 0, kmn = 0xFFFFu;
+    uint32_t kmx = 0, kum = 0;
 #pragma unroll
     for (int w = 0; w < kSampWaves; ++w) {
       kmx = max(kmx, red[w]);
-      kmn = min(kmn, red[16 + w]);
+      kum = max(kum, red[16 + w]);
     }
-    if (kmx >= Inf16<T>::kPosKey || kmn < Inf16<T>::kNegKey || kmx <= Inf16<T>::kNegKey) return -1;  // (uniform)
+    // A NaN or +inf, or no sign of anything above -inf (for a row of
+    // negatives the signed maximum may not be the row's): the other paths.
+    if (kmx >= Inf16<T>::kPosKey || kum > Inf16<T>::kNegBits || kmx <= Inf16<T>::kNegKey) return -1;  // (uniform)
     // 2. thread t holds bins 4095 - 4t down to 4092 - 4t: a scan in descending order
     const int b0 = kSelBins - 1 - 4 * tid;
     const uint32_t h0 = hist[b0], h1 = hist[b0 - 1], h2 = hist[b0 - 2], h3 = hist[b0 - 3];
@@ -585,7 +607,19 @@ struct RowSampler {
     }
     uint32_t K = (bin << 4) | low;  // >= the -inf key: the row holds no NaN
     if (K == 0x8000u) K = 0x7FFFu;   // +0: -0 has the same value
-    // 3. the chunks holding a key >= K (from the chunk maxima), staged in LDS
+    if (K <= 0x8000u) {  // (uniform) a cut at or below zero: every chunk's exact largest key
+#pragma unroll
+      for (int j = 0; j < kRegChunks; ++j) {
+        const u32x4 w = ch[j];
+        uint32_t mj = pk_max(pk_max(pk_key(w[0]), pk_key(w[1])), pk_max(pk_key(w[2]), pk_key(w[3])));
+        if (tid + j * kSampThreads >= n8) mj = kNegKeys;
+        if (j & 1) cmx[(j >> 1) * kSampThreads + tid] = pend | (hmax(mj) << 16);
+        else pend = hmax(mj);
+      }
+      if (kRegChunks & 1) cmx[(kMaxWords - 1) * kSampThreads + tid] = pend;
+    }
+    // 3. the chunks holding a key >= K (from the chunk maxima), staged in
+    // the wave's own LDS region (ballot offsets)
     uint32_t mask = 0;
 #pragma unroll
     for (int w2 = 0; w2 < kMaxWords; ++w2) {
@@ -598,59 +632,77 @@ struct RowSampler {
     uint32_t wmask = mask;
     for (int o = 1; o < 64; o <<= 1) wmask |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(wmask), o, 64));
     wmask = __builtin_amdgcn_readfirstlane(wmask);  // (uniform: the wave's hot chunks)
+    u32x4* my_stage = stage + wave * kWaveStage;
+    uint32_t* my_sid = sid + wave * kWaveStage;
+    uint32_t nst = 0;  // (uniform) chunks this wave staged
 #pragma unroll
     for (int j = 0; j < kRegChunks; ++j) {
       if (!(wmask & (1u << j))) continue;  // (uniform)
       const bool hot = (mask >> j) & 1u;
       const uint64_t b = __ballot(hot);
-      uint32_t base0 = 0;
-      if (lane == 0) base0 = atomicAdd(&s.n_gather, static_cast<uint32_t>(__popcll(b)));
-      const uint32_t base = __builtin_amdgcn_readfirstlane(base0);
-      if (hot) {
-        const uint32_t at = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(b >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b), 0u));
-        if (at < static_cast<uint32_t>(kStageCap)) {
-          stage[at] = ch[j];
-          sid[at] = static_cast<uint32_t>(tid + j * kSampThreads);
-        }
+      const uint32_t at = nst + lane_rank(b);
+      if (hot && at < static_cast<uint32_t>(kWaveStage)) {
+        my_stage[at] = ch[j];
+        my_sid[at] = static_cast<uint32_t>(tid + j * kSampThreads);
       }
+      nst += static_cast<uint32_t>(__popcll(b));
     }
+    if (lane == 0) red[80 + wave] = nst;
     __syncthreads();
-    const uint32_t nst = s.n_gather;
-    if (nst > static_cast<uint32_t>(kStageCap)) return -1;  // (uniform)
+    uint32_t total = 0;
+    bool over = false;
+#pragma unroll
+    for (int w = 0; w < kSampWaves; ++w) {
+      total += red[80 + w];
+      over = over || red[80 + w] > static_cast<uint32_t>(kWaveStage);
+    }
+    if (over) return -1;  // (uniform)
     const float kc0 = 1.4426950408889634f / t;  // (16-bit rows order by the logit)
     // 4. wave 0: the staged chunks' keys >= K become candidates; for at most
     // 64 it ranks and decides at once
     if (wave == 0) {
       uint32_t nc = 0;  // (uniform) candidates written
-      for (uint32_t i0 = 0; i0 < nst; i0 += 64) {
+      for (uint32_t i0 = 0; i0 < total; i0 += 64) {
         const uint32_t i = i0 + lane;
-        const u32x4 w = i < nst ? stage[i] : u32x4{0, 0, 0, 0};
-        const uint32_t id = i < nst ? sid[i] : 0u;
+        uint32_t base = 0, reg = 0;  // staged chunk i: region `reg`, whose chunks start at `base`
+#pragma unroll
+        for (int w = 1; w < kSampWaves; ++w) {
+          uint32_t pre = 0;
+#pragma unroll
+          for (int w3 = 0; w3 < w; ++w3) pre += red[80 + w3];
+          if (i >= pre) {
+            base = pre;
+            reg = static_cast<uint32_t>(w);
+          }
+        }
+        u32x4 w = u32x4{0, 0, 0, 0};
+        uint32_t id = 0;
+        if (i < total) {
+          const u32x4 raw = stage[reg * kWaveStage + (i - base)];
+          w = u32x4{pk_key(raw[0]), pk_key(raw[1]), pk_key(raw[2]), pk_key(raw[3])};
+          id = sid[reg * kWaveStage + (i - base)];
+        }
         uint32_t take = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t key = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu);
-          take |= (key >= K ? 1u : 0u) << e;
-        }
+        for (int e = 0; e < 4; ++e)
+          take |= ((w[e] & 0xFFFFu) >= K ? 1u : 0u) << (2 * e) | ((w[e] >> 16) >= K ? 1u : 0u) << (2 * e + 1);
+        if (i >= total) take = 0;
         const uint32_t cnt = __popc(take);
         uint32_t pre = 0, tot = 0;  // exclusive prefix of cnt (<= 8) over the wave, by bit planes
 #pragma unroll
         for (int bp = 0; bp < 4; ++bp) {
           const uint64_t bb = __ballot((cnt >> bp) & 1u);
-          pre += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bb >> 32),
-                                           __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bb), 0u))
-                 << bp;
+          pre += lane_rank(bb) << bp;
           tot += static_cast<uint32_t>(__popcll(bb)) << bp;
         }
         uint32_t at = nc + pre;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if ((take >> e) & 1u) {
-            const uint32_t key = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu);
-            if (at < static_cast<uint32_t>(kGatherCap)) cand[at] = rank_key(lo_f<T>(key_bits(key)), 8 * int64_t{id} + e);
-            ++at;
-          }
+        while (take) {  // (usually once)
+          const int e = __builtin_ctz(take);
+          take &= take - 1;
+          const uint32_t word = e >= 4 ? (e >= 6 ? w[3] : w[2]) : (e >= 2 ? w[1] : w[0]);
+          const uint32_t key = (word >> ((e & 1) * 16)) & 0xFFFFu;
+          if (at < static_cast<uint32_t>(kGatherCap)) cand[at] = cand_key(key, 8 * id + static_cast<uint32_t>(e));
+          ++at;
         }
         nc += tot;
       }
@@ -669,11 +721,11 @@ struct RowSampler {
         const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_ds_permute(rank * 4, static_cast<int>(kv)));
         const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_ds_permute(rank * 4, static_cast<int>(kv >> 32)));
         const uint64_t sorted = (static_cast<uint64_t>(hi) << 32) | lo;  // lane e: rank e
-        const uint64_t top = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(hi))))
-                              << 32) |
-                             static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lo)));
-        token = temp <= 0.f ? static_cast<int64_t>(static_cast<uint32_t>(top))  // greedy: rank 0
-                            : decide_lanes(sorted, lk, key_of_rank(top), kc0, p, u);
+        const uint32_t top_lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lo)));
+        const uint32_t top_hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(hi)));
+        token = temp <= 0.f ? static_cast<int64_t>(top_lo)  // greedy: rank 0
+                            : decide_lanes(sorted, lk, cand_value((static_cast<uint64_t>(top_hi) << 32) | top_lo),
+                                           kc0, p, u);
       }
       if (lane == 0) {
         s.found_index = token;
@@ -686,18 +738,20 @@ struct RowSampler {
     const uint32_t n = red[49];
     if (n > static_cast<uint32_t>(kGatherCap)) return -1;
     const int lk = static_cast<int>(min(k_eff, n));
+    const int n8c = static_cast<int>(min((n + 7) & ~7u, static_cast<uint32_t>(kGatherCap)));
     for (int i = tid; i < static_cast<int>(n); i += kSampThreads) {  // each candidate's rank among them
       const uint64_t kv = cand[i];
       int rank = 0, q = 0;
-      for (; q + 4 <= static_cast<int>(n); q += 4)
-        rank += (cand[q] < kv ? 1 : 0) + (cand[q + 1] < kv ? 1 : 0) + (cand[q + 2] < kv ? 1 : 0) +
-                (cand[q + 3] < kv ? 1 : 0);
+      for (; q + 8 <= n8c; q += 8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rank += cand[q + e] < kv ? 1 : 0;
+      }
       for (; q < static_cast<int>(n); ++q) rank += cand[q] < kv ? 1 : 0;
       if (rank < lk) s.keys[rank] = kv;
     }
     __syncthreads();
     if (temp <= 0.f) return static_cast<uint32_t>(s.keys[0]);  // greedy: the first index of the maximum
-    kmax = key_of_rank(s.keys[0]);
+    kmax = cand_value(s.keys[0]);
     kc = kc0;
     if (wave == 0) {
       const int64_t token = decide_wave(lk, p, u);
@@ -707,11 +761,28 @@ struct RowSampler {
     return s.found_index;
   }
 
+  // Candidate keys: (0xFFFF - key) << 32 | index, with -0's key folded into
+  // +0's. Ascending order is the stable descending sort's order (larger
+  // values first, ties by index), as for rank_key; cand_value gives back the
+  // logit (-0 as +0).
+  __device__ __forceinline__ static uint64_t cand_key(uint32_t key, uint32_t index) {
+    const uint32_t folded = key == 0x7FFFu ? 0x8000u : key;
+    return (static_cast<uint64_t>(0xFFFFu - folded) << 32) | index;
+  }
+  __device__ __forceinline__ static float cand_value(uint64_t ck) {
+    return lo_f<T>(key_bits(0xFFFFu - static_cast<uint32_t>(ck >> 32)));
+  }
+  // The lane's place among the lanes of a ballot below it.
+  __device__ __forceinline__ static uint32_t lane_rank(uint64_t b) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(b >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b), 0u));
+  }
+
   // decide_on_prefix(lk, lk, ...) on ranks held one per lane (lane e: rank e,
   // lk <= 64), with the row's maximum km: the same masses and comparisons.
   __device__ __forceinline__ int64_t decide_lanes(uint64_t sorted, int lk, float km, float kcv, double p,
                                                   double u) const {
-    const uint64_t m = lane < lk ? mass_of(key_of_rank(sorted), km, kcv) : 0;
+    const uint64_t m = lane < lk ? mass_of(cand_value(sorted), km, kcv) : 0;
     uint64_t incl = m;
     for (int o = 1; o < 64; o <<= 1) {
       const uint64_t up = __shfl_up(incl, o, 64);
@@ -745,7 +816,7 @@ struct RowSampler {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int e = 8 * lane + i;
-      m[i] = e < lk ? mass_key(key_of_rank(s.keys[e])) : 0;
+      m[i] = e < lk ? mass_key(cand_value(s.keys[e])) : 0;
       mine += m[i];
     }
     uint64_t incl = mine;
@@ -1087,11 +1158,14 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   // candidate pass decides from one read of the row, or sends it on.
   if constexpr (UNIT && sizeof(T) == 2) {
     if (a.cand && rs.chunked() && a.V <= kRegMaxV) {
-      u32x4 ch[kRegChunks];
-      rs.load_row(ch);  // (in flight while the row's parameters arrive)
+      // The row's parameters are loaded first: loads complete in order, so
+      // the test below waits for them alone while the row is in flight.
       const int64_t k = load_int(a.topk, a.topk_dt, r * a.topk_s);
+      const float pf = a.topp[r * a.topp_s], uf = a.unif[r * a.unif_s];
+      u32x4 ch[kRegChunks];
+      rs.load_row(ch);
       if (candidate_row(a, temp, k)) {
-        const int64_t token = rs.candidates(ch, temp, k, a.topp[r * a.topp_s], a.unif[r * a.unif_s]);
+        const int64_t token = rs.candidates(ch, temp, k, pf, uf);
         if (token >= 0) {
           if (tid == 0) a.out[r * a.out_s] = token;
           return;
