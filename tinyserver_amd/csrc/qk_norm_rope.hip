@@ -100,6 +100,27 @@ __device__ __forceinline__ void store8_nt(T* p, const float (&v)[8]) {
   }
 }
 
+// 8 elements copied as they are (16 bytes of a 16-bit type, 32 of fp32),
+// non-temporal both ways.
+template <typename T>
+struct RawRow {
+  u32x4 w[sizeof(T) / 2];
+};
+template <typename T>
+__device__ __forceinline__ RawRow<T> load_raw_nt(const T* p) {
+  RawRow<T> r;
+#pragma unroll
+  for (int i = 0; i < static_cast<int>(sizeof(T) / 2); ++i)
+    r.w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + i);
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ void store_raw_nt(T* p, const RawRow<T>& r) {
+#pragma unroll
+  for (int i = 0; i < static_cast<int>(sizeof(T) / 2); ++i)
+    __builtin_nontemporal_store(r.w[i], reinterpret_cast<u32x4*>(p) + i);
+}
+
 template <typename T, bool VEC>
 __device__ __forceinline__ void store8(T* p, int64_t stride, const float (&v)[8]) {
   if constexpr (VEC && sizeof(T) == 2) {
@@ -202,17 +223,22 @@ __global__ __launch_bounds__(256) void qk_norm_rope_token(NormRopeArgs<T> a) {
   const T* krow = a.k + t * a.k_st + d0;
   const T* vrow = a.v + t * a.v_st + d0;
   const bool store = a.k_cache != nullptr;
-  int64_t blk = 0, slot = 0;
-  const bool placed = store && a.addr.locate(t, a.BS, a.NB, blk, slot);
 
-  float x[R][8], vv[R][8];
+  // Every row load is issued before anything waits on one: q/k rows by an
+  // address select, v rows (when storing) for each round that holds a k
+  // head (a q lane of such a round reads v head 0's row and drops it). No
+  // load sits in a divergent branch, whose join would wait for all of them.
+  float x[R][8];
+  RawRow<T> vv[R];  // (copied to the cache as read)
 #pragma unroll
   for (int j = 0; j < R; ++j) {
     const int hh = min(g + 16 * j, H - 1);  // rows past the token's last head redo it (never stored)
-    if (hh < Hq) load8_nt<T>(qrow + hh * a.q_sh, x[j]);
-    else load8_nt<T>(krow + (hh - Hq) * a.k_sh, x[j]);
-    if (placed && hh >= Hq) load8_nt<T>(vrow + (hh - Hq) * a.v_sh, vv[j]);
+    load8_nt<T>(hh < Hq ? qrow + hh * a.q_sh : krow + (hh - Hq) * a.k_sh, x[j]);
+    if (store && 16 * j + 15 >= Hq) vv[j] = load_raw_nt<T>(vrow + max(hh - Hq, 0) * a.v_sh);  // (uniform test)
   }
+  // The token's cache slot: scalar loads, while the rows are in flight.
+  int64_t blk = 0, slot = 0;
+  const bool placed = store && a.addr.locate(t, a.BS, a.NB, blk, slot);
 #pragma unroll
   for (int j = 0; j < R; ++j) {
     const int hh = g + 16 * j;
@@ -228,7 +254,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_token(NormRopeArgs<T> a) {
     if (a.k_out) store8<T, true>(a.k_out + t * a.ko_st + h * a.ko_sh + d0, 1, o);
     if (placed) {
       store8_nt<T>(a.k_cache + blk * a.kc_b + h * a.kc_h + slot * a.kc_s + d0, o);
-      store8_nt<T>(a.v_cache + blk * a.vc_b + h * a.vc_h + slot * a.vc_s + d0, vv[j]);
+      store_raw_nt<T>(a.v_cache + blk * a.vc_b + h * a.vc_h + slot * a.vc_s + d0, vv[j]);
     }
   }
 }
