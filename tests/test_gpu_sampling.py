@@ -303,6 +303,30 @@ def test_candidate_path_large_k(dtype):
     assert torch.equal(got, full), (got.tolist(), full.tolist())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_candidate_path_negative_rows(dtype):
+    """Rows with no non-negative logit (shifted logits, log-probabilities,
+    shifted rows a third -inf), whose signed raw maxima are each set's
+    smallest element: the candidate pass takes its samples from the keys
+    instead. The oracle, and the histogram paths token for token."""
+    base, _, _, _, _ = _qwen3_batch(28, b=4)
+    shifted = base - 40.0
+    logp = torch.log_softmax(base / 0.8, dim=-1)
+    masked = shifted.clone()
+    masked[:, ::3] = -float("inf")
+    rows = torch.cat([shifted, logp, masked])
+    temperature = [0.8, 1.0, 0.0, 1.2] * 3
+    ks = [50, 1, 0, 400, 20, 128, 0, 50, 50, 3, 0, 300]
+    top_p = [0.9, 1.0, 1.0, 0.95, 0.5, 1.0, 1.0, 0.9, 0.9, 1.0, 1.0, 0.8]
+    g = torch.Generator().manual_seed(29)
+    uniforms = torch.rand(12, generator=g).tolist()
+    got, _ = _compare(rows, temperature, ks, top_p, uniforms, dtype=dtype, what=f"negative rows {dtype}")
+    t = lambda x, dt: torch.tensor(x, dtype=dt, device=DEV)
+    full = _single_kernel(rows.to(DEV, dtype), t(temperature, torch.float32), t(ks, torch.int64),
+                          t(top_p, torch.float32), t(uniforms, torch.float32))
+    assert torch.equal(got, full), (got.tolist(), full.tolist())
+
+
 @pytest.mark.parametrize("v", [8, 200, 1001, 4096 + 8, 155648, 155656])
 def test_candidate_path_short_and_odd_rows(v):
     """Short rows (most threads hold no chunk), a row whose length is not a

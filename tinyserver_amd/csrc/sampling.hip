@@ -509,7 +509,8 @@ struct RowSampler {
     const uint32_t k_eff = temp <= 0.f ? 1u : static_cast<uint32_t>(k);  // in [1, kFastK]
     // LDS: red = s.cnt ([0, 16) wave maxima, [16, 32) minima, [32, 48) bin
     // sums, [48] samples above the bin, [49] candidates, [64, 80) the
-    // low-bits histogram, [80, 96) chunks staged per wave); hist = s.wsum as kSelBins counts; cmx = each
+    // low-bits histogram, [80, 96) chunks staged per wave, [96, 112) wave
+    // maxima of a negative row's exact samples); hist = s.wsum as kSelBins counts; cmx = each
     // thread's chunk maxima (two 16-bit keys a word, word w of thread t at
     // w * kSampThreads + t) from s.pcnt on; staged chunks after them; the
     // candidates in s.keys[kCandOff, kCap); ranked keys in s.keys[0, k)
@@ -562,7 +563,7 @@ struct RowSampler {
       red[wave] = wmx;
       red[16 + wave] = wum;
     }
-    const uint32_t s0 = tk & 0xFFFFu, s1 = tk >> 16;  // this thread's two samples (keys)
+    uint32_t s0 = tk & 0xFFFFu, s1 = tk >> 16;  // this thread's two samples (keys)
     atomicAdd(&hist[s0 >> 4], 1u);
     atomicAdd(&hist[s1 >> 4], 1u);
     __syncthreads();
@@ -574,7 +575,42 @@ struct RowSampler {
     }
     // A NaN or +inf, or no sign of anything above -inf (for a row of
     // negatives the signed maximum may not be the row's): the other paths.
-    if (kmx >= Inf16<T>::kPosKey || kum > Inf16<T>::kNegBits || kmx <= Inf16<T>::kNegKey) return -1;  // (uniform)
+    if (kmx >= Inf16<T>::kPosKey || kum > Inf16<T>::kNegBits) return -1;  // a NaN or +inf (uniform)
+    bool exact_cmx = false;
+    if (kmx < 0x8000u) {  // (uniform)
+      // Every sample is negative, so the whole row is (a set holding a value
+      // >= +0 has a sample >= +0): the signed maxima are then each set's
+      // smallest element, which would put the cut far too low. Samples and
+      // chunk maxima are taken again from the keys (one more pass over the
+      // registers), and histogrammed instead.
+#pragma unroll
+      for (int b = tid; b < kSelBins; b += kSampThreads) hist[b] = 0;
+      uint32_t tkk = 0;
+#pragma unroll
+      for (int j = 0; j < kRegChunks; ++j) {
+        const u32x4 w = ch[j];
+        uint32_t mj = pk_max(pk_max(pk_key(w[0]), pk_key(w[1])), pk_max(pk_key(w[2]), pk_key(w[3])));
+        if (tid + j * kSampThreads >= n8) mj = kNegKeys;
+        tkk = pk_max(tkk, mj);
+        if (j & 1) cmx[(j >> 1) * kSampThreads + tid] = pend | (hmax(mj) << 16);
+        else pend = hmax(mj);
+      }
+      if (kRegChunks & 1) cmx[(kMaxWords - 1) * kSampThreads + tid] = pend;
+      exact_cmx = true;
+      uint32_t wm = hmax(tkk);
+      for (int o = 32; o > 0; o >>= 1) wm = max(wm, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wm), o, 64)));
+      if (lane == 0) red[96 + wave] = wm;
+      __syncthreads();
+      kmx = 0;
+#pragma unroll
+      for (int w = 0; w < kSampWaves; ++w) kmx = max(kmx, red[96 + w]);
+      if (kmx <= Inf16<T>::kNegKey) return -1;  // every logit -inf (uniform)
+      s0 = tkk & 0xFFFFu;
+      s1 = tkk >> 16;
+      atomicAdd(&hist[s0 >> 4], 1u);
+      atomicAdd(&hist[s1 >> 4], 1u);
+      __syncthreads();
+    }
     // 2. thread t holds bins 4095 - 4t down to 4092 - 4t: a scan in descending order
     const int b0 = kSelBins - 1 - 4 * tid;
     const uint32_t h0 = hist[b0], h1 = hist[b0 - 1], h2 = hist[b0 - 2], h3 = hist[b0 - 3];
@@ -607,7 +643,7 @@ struct RowSampler {
     }
     uint32_t K = (bin << 4) | low;  // >= the -inf key: the row holds no NaN
     if (K == 0x8000u) K = 0x7FFFu;   // +0: -0 has the same value
-    if (K <= 0x8000u) {  // (uniform) a cut at or below zero: every chunk's exact largest key
+    if (K <= 0x8000u && !exact_cmx) {  // (uniform) a cut at or below zero: every chunk's exact largest key
 #pragma unroll
       for (int j = 0; j < kRegChunks; ++j) {
         const u32x4 w = ch[j];
