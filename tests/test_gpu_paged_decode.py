@@ -263,6 +263,57 @@ def test_fused_decode_step(name):
         assert_close(out_b, ref, what=f"{name} fused step")
 
 
+@pytest.mark.parametrize("name", ["qwen3-0.6b-decode-bs4", "qwen3-8b-decode-bs64"])
+def test_decode_graph_replays(name):
+    """The decode step captured in a HIP graph, as a serving loop replays it:
+    the two-launch block (norm/RoPE/store, then attention) and the single-
+    launch step, each replayed three times onto freshly poisoned caches with
+    eager work between replays, equal to the eager calls in the output and
+    both caches."""
+    w = W.make(name, poison=True)
+    b = len(w.ctx_lens)
+    g = w.to(DEV)
+    sl = g.ctx_lens.to(torch.int32)
+    cu = torch.arange(b + 1, dtype=torch.int32, device=DEV)
+    kc_e, vc_e = g.k_cache.clone(), g.v_cache.clone()
+    qe, _ = qk_norm_rope_store(g.q, g.k, g.v, g.q_weight, g.k_weight, g.cos, g.sin, g.eps, kc_e, vc_e,
+                               g.block_tables, cu, g.positions, return_k=False)
+    out_e = paged_attention_forward(qe, kc_e, vc_e, g.block_tables, 16, sl)
+    kc, vc = g.k_cache.clone(), g.v_cache.clone()
+    q_out = torch.empty_like(qe)
+    out_a, out_f = torch.empty_like(out_e), torch.empty_like(out_e)
+
+    def block():
+        qk_norm_rope_store(g.q, g.k, g.v, g.q_weight, g.k_weight, g.cos, g.sin, g.eps, kc, vc, g.block_tables, cu,
+                           g.positions, q_out=q_out, return_k=False)
+        paged_attention_forward(q_out, kc, vc, g.block_tables, 16, sl, out=out_a)
+
+    def step():
+        paged_decode_step(g.q, g.k, g.v, g.q_weight, g.k_weight, g.cos, g.sin, g.eps, kc, vc, g.block_tables, sl,
+                          out=out_f)
+
+    for fn, out in ((block, out_a), (step, out_f)):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        for rep in range(3):
+            kc.copy_(g.k_cache)
+            vc.copy_(g.v_cache)
+            out.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(kc, kc_e) and torch.equal(vc, vc_e), (fn.__name__, rep, "cache")
+            assert torch.equal(out, out_e), (fn.__name__, rep, "output")
+            paged_attention_forward(qe, kc_e, vc_e, g.block_tables, 16, sl)  # eager work between replays
+            torch.cuda.synchronize()
+        del graph
+
+
 @pytest.mark.parametrize("group,block_size", [(8, 32), (1, 16), (4, 64)])
 def test_fused_decode_step_shapes(group, block_size):
     """The single-launch step on GQA groups 8 (two norm passes per unit) and 1
