@@ -471,11 +471,12 @@ struct RowSampler {
   //   2. K = the k-th largest sample (12-bit prefix histogram, then the low 4
   //      bits of the samples in that prefix), so at least k elements have key
   //      >= K; +0's key is lowered to take -0 too; a cut at or below zero
-  //      recomputes the chunk maxima from every key;
+  //      recomputes the chunk maxima from every key, and a row of negatives
+  //      takes its samples from the keys too;
   //   3. finds the chunks holding a key >= K from each chunk's maximum (kept
   //      in LDS by step 1), skipping with a scalar test every chunk no lane
-  //      of the wave holds one in, and stages those chunks in LDS (one atomic
-  //      per wave and chunk);
+  //      of the wave holds one in, and stages those chunks in the wave's own
+  //      LDS region (ballot offsets);
   //   4. wave 0 turns the staged chunks' keys >= K into candidates -- a
   //      prefix of the row in rank order that holds its first k ranks -- and,
   //      for at most 64, ranks them (a count: keys are distinct), moves each
@@ -507,7 +508,7 @@ struct RowSampler {
     constexpr int kMaxWords = (kRegChunks + 1) / 2;                // chunk maxima words per thread
     const int n8 = static_cast<int>(a.V >> 3);
     const uint32_t k_eff = temp <= 0.f ? 1u : static_cast<uint32_t>(k);  // in [1, kFastK]
-    // LDS: red = s.cnt ([0, 16) wave maxima, [16, 32) minima, [32, 48) bin
+    // LDS: red = s.cnt ([0, 16) wave maxima, [16, 32) unsigned maxima, [32, 48) bin
     // sums, [48] samples above the bin, [49] candidates, [64, 80) the
     // low-bits histogram, [80, 96) chunks staged per wave, [96, 112) wave
     // maxima of a negative row's exact samples); hist = s.wsum as kSelBins counts; cmx = each
