@@ -203,6 +203,18 @@ def test_qwen3_4b_mixed_step_one_launch():
     assert_close(out_d, ref_d, what=f"one launch: decode attention, all {len(cpu.decode.ctx_lens)} sequences")
 
 
+def test_one_prefill_workgroup_many_items():
+    """A single prefill workgroup takes every prefill item (6 sequences of
+    200..600 tokens, 2 kv heads: over a hundred items, more than the 64 it
+    resolves at a time), bit for bit against the scheduler-order step."""
+    cpu = W.make_mixed("mixed-plan", 22, decode_batch=3, ctx_lo=1, ctx_hi=200, prefill_seqs=6, len_lo=200, len_hi=600,
+                       num_heads=8, num_kv_heads=2, poison=True)
+    items = sum((int(n) + 31) // 32 for n in cpu.prefill.seq_lens) * 2
+    print(f"one prefill workgroup, {items} items", flush=True)
+    assert items > 2 * 64
+    _two_vs_one(cpu, prefill_workgroups=1)
+
+
 @pytest.mark.parametrize("num_heads,num_kv_heads,prefill_workgroups",
                          [(8, 2, 0), (8, 2, 3), (8, 2, 1000), (8, 4, 0)])
 def test_small_mixed_step_one_launch(num_heads, num_kv_heads, prefill_workgroups):

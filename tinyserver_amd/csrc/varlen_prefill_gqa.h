@@ -43,12 +43,19 @@ __device__ __forceinline__ void seq_range(const int32_t* cu, int64_t stride, int
   len = s1 - s0;
 }
 
+// The work-item plan: up to kPlanItems item descriptors of a workgroup (6
+// int32 each), computed kPlanItems at a time, and the level table (items
+// above each query-block level) they are found with, for calls of at most
+// kPlanSeqs sequences and kPlanLevels query blocks per sequence.
+constexpr int kPlanItems = 64, kPlanSeqs = 64, kPlanLevels = 256;
+
 // LDS bytes of prefill_gqa_body<D, NW>: NB K and NB V block slots of 32 rows,
-// the output staging (8 rows per wave) and the per-sequence query-block
-// counts.
+// the output staging (8 rows per wave), the per-sequence query-block counts
+// and the work-item plan.
 template <int D, int NW>
 constexpr int gqa_smem_bytes() {
-  return 2 * (NW == 2 ? 2 : 4) * (32 * 2 * D) + NW * 8 * (D + 8) * 2 + max_persist_seqs(NW) * 2;
+  return 2 * (NW == 2 ? 2 : 4) * (32 * 2 * D) + NW * 8 * (D + 8) * 2 + max_persist_seqs(NW) * 2 +
+         kPlanItems * 6 * 4 + kPlanLevels * 4;
 }
 
 // LDS-staged GQA flash attention on 32x32 tiles, persistent. A work item is
@@ -95,7 +102,9 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
   constexpr int VOFF = NB * BLKB;           // byte offset of the V slots
   constexpr int OOFF = 2 * NB * BLKB;       // byte offset of the output staging (8 rows per wave)
   constexpr int QOFF = OOFF + NW * 8 * ROWO * 2;  // byte offset of the per-sequence query-block counts
-  static_assert(QOFF + max_persist_seqs(NW) * 2 == gqa_smem_bytes<D, NW>(), "LDS layout and its size agree");
+  constexpr int PLOFF = QOFF + max_persist_seqs(NW) * 2;  // byte offset of the item plan
+  constexpr int LVOFF = PLOFF + kPlanItems * 6 * 4;       // byte offset of the level table
+  static_assert(LVOFF + kPlanLevels * 4 == gqa_smem_bytes<D, NW>(), "LDS layout and its size agree");
   static_assert(IPW >= 1 && IPW * NW == 2 * (32 / RPI), "a block step is a whole number of loads per wave");
   static_assert((A > 1 ? A - 1 : 0) * IPW <= 63, "outstanding loads fit the vmcnt field");
   // A row's running max only moves when it grows by more than this (log2
@@ -103,6 +112,8 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
   // rescaled rarely. l uses the same m, so the result is unchanged.
   constexpr float kRescale = 8.0f;
   uint16_t* const nqb_s = reinterpret_cast<uint16_t*>(smem + QOFF);  // query blocks of each sequence
+  int32_t* const plan_s = reinterpret_cast<int32_t*>(smem + PLOFF);   // item descriptors, 6 words each
+  int32_t* const lev_s = reinterpret_cast<int32_t*>(smem + LVOFF);    // items above each level
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, c = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -112,11 +123,10 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
   // ---- Work items: (query block, sequence, kv head) with a non-empty query
   // block, heaviest (latest) query blocks first: level Q holds query block Q
   // of every sequence that has one, in sequence order, kv head fastest.
-  // Workgroup w takes items w, w + grid, w + 2 grid, ...: with the heaviest
-  // first, that deals the work out evenly. (No work-queue atomic: a returning
-  // atomic holds up every load the wave issues after it until it completes,
-  // and under load that took longer than the imbalance it would remove.) The
-  // per-sequence counts live in LDS.
+  // The workgroups take them in rounds (item_of below), heaviest first. (No
+  // work-queue atomic: a returning atomic holds up every load the wave issues
+  // after it until it completes, and under load that took longer than the
+  // imbalance it would remove.) The per-sequence counts live in LDS.
   for (int b = tid; b < nseq; b += 64 * NW) {
     int64_t qs, ql;
     seq_range(cu_q, a.cuq_s, b, a.total_q, qs, ql);
@@ -140,6 +150,8 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
 
   struct Item {
     int b, kvh, q0, q_len, k_len, nblk;
+    int jm;     // first block that needs a mask (keys past k_len, or causal keys after a query)
+    int kfull;  // rows below min(k_len, 32 nblk) load without clamping
     int64_t q_start;
     const T* kb;
     const T* vb;
@@ -181,8 +193,93 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
     const int q_last = it.q0 + 32 < it.q_len ? it.q0 + 32 : it.q_len;
     const int kend = a.causal ? (it.k_len < q_last ? it.k_len : q_last) : it.k_len;
     it.nblk = (kend + 31) / 32;
+    it.jm = a.causal ? min(it.k_len / 32, Q) : it.k_len / 32;
+    it.kfull = min(it.k_len, it.nblk * 32);
     it.kb = static_cast<const T*>(a.k) + ks * a.k_st + it.kvh * a.k_sh;
     it.vb = static_cast<const T*>(a.v) + ks * a.v_st + it.kvh * a.v_sh;
+  };
+
+  // ---- The item plan. For calls of at most kPlanSeqs sequences and
+  // kPlanLevels query blocks per sequence, the level table lev_s[Q] =
+  // items_above(Q) is built once, and wave 0 resolves kPlanItems items at a
+  // time, one per lane (a binary search over the table, the rank-th
+  // sequence by a scan, its ranges by a vector load), into plan_s: the item
+  // loop then reads a descriptor from LDS instead of running the
+  // wave-cooperative search above for every item.
+  const bool planned = nseq <= kPlanSeqs && qb_max <= kPlanLevels;
+  if (planned) {
+    for (int Q = tid; Q < qb_max; Q += 64 * NW) {
+      int sum = 0;
+      for (int b = 0; b < nseq; ++b) sum += max(0, static_cast<int>(nqb_s[b]) - Q - 1);
+      lev_s[Q] = sum * Hkv;
+    }
+    __syncthreads();
+  }
+  // Round k of the deal gives workgroup w item k P + w when k is even and
+  // k P + P - 1 - w when it is odd (P workgroups, items heaviest first).
+  const int P = static_cast<int>(gridDim.x) - wg_base, wr = static_cast<int>(blockIdx.x) - wg_base;
+  auto item_of = [&](int k) { return k * P + ((k & 1) ? P - 1 - wr : wr); };
+  // Items of rounds k0 .. k0 + kPlanItems - 1 into plan_s (every wave calls it).
+  auto make_plan = [&](int k0) {
+    if (wave == 0) {
+      const int i = item_of(k0 + lane);
+      if (i < n_items) {
+        int lo = 0, hi = qb_max - 1;  // the smallest Q with lev_s[Q] <= i
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (lev_s[mid] <= i) hi = mid; else lo = mid + 1;
+        }
+        const int r = i - lev_s[lo];
+        int rank = r / Hkv;
+        const int kvh = r - rank * Hkv;
+        int b = 0;
+        for (int bb = 0; bb < nseq; ++bb)
+          if (static_cast<int>(nqb_s[bb]) > lo) {
+            if (rank == 0) { b = bb; break; }
+            --rank;
+          }
+        int64_t qs, ql, ks, kl;
+        seq_range(cu_q, a.cuq_s, b, a.total_q, qs, ql);
+        seq_range(cu_k, a.cuk_s, b, a.total_k, ks, kl);
+        int32_t* const e = plan_s + 6 * lane;
+        e[0] = b | (kvh << 16);
+        e[1] = lo;
+        e[2] = static_cast<int32_t>(qs);
+        e[3] = static_cast<int32_t>(ql);
+        e[4] = static_cast<int32_t>(ks);
+        e[5] = static_cast<int32_t>(kl);
+      }
+    }
+    __syncthreads();
+  };
+  // Item of round k from the plan (its descriptor is in plan_s).
+  auto resolve_planned = [&](int k, Item& it) {
+    const int32_t* const e = plan_s + 6 * (k % kPlanItems);
+    const int w0 = __builtin_amdgcn_readfirstlane(e[0]);
+    it.b = w0 & 0xFFFF;
+    it.kvh = w0 >> 16;
+    const int Q = __builtin_amdgcn_readfirstlane(e[1]);
+    const int64_t qs = __builtin_amdgcn_readfirstlane(e[2]), ks = __builtin_amdgcn_readfirstlane(e[4]);
+    it.q_start = qs;
+    it.q_len = __builtin_amdgcn_readfirstlane(e[3]);
+    it.k_len = __builtin_amdgcn_readfirstlane(e[5]);
+    it.q0 = Q * 32;
+    const int q_last = it.q0 + 32 < it.q_len ? it.q0 + 32 : it.q_len;
+    const int kend = a.causal ? (it.k_len < q_last ? it.k_len : q_last) : it.k_len;
+    it.nblk = (kend + 31) / 32;
+    it.jm = a.causal ? min(it.k_len / 32, Q) : it.k_len / 32;
+    it.kfull = min(it.k_len, it.nblk * 32);
+    it.kb = static_cast<const T*>(a.k) + ks * a.k_st + it.kvh * a.k_sh;
+    it.vb = static_cast<const T*>(a.v) + ks * a.v_st + it.kvh * a.v_sh;
+  };
+  // The item of round k (k: this workgroup's round; i = item_of(k)).
+  auto resolve_round = [&](int k, int i, Item& it) {
+    if (planned) {
+      if (k % kPlanItems == 0) make_plan(k);
+      resolve_planned(k, it);
+    } else {
+      resolve(i, it);
+    }
   };
 
   // ---- LDS layout of K/V: rows are stored unpadded, RB bytes each, with the
@@ -204,9 +301,8 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
   // rows, the others the V rows; every wave issues the same number of loads
   // per step. Rows past the sequence's end re-read its last key, which the
   // mask or a zero probability then ignores; so does the last step's K block
-  // (one past the end, a clamped copy of the last block). Blocks take slots
-  // in order across items: block j of an item whose first block is the
-  // workgroup's g-th goes to slot (g + j) % NB.
+  // (one past the end, a clamped copy of the last block). Block j of every
+  // item goes to slot j % NB.
   typedef __attribute__((address_space(3))) void lds_void;
   const bool k_wave = wave < NW / 2;
   const int row0w = (wave % (NW / 2)) * IPW * RPI;  // first row this wave loads
@@ -243,19 +339,52 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
       }
     }
   };
-  // Block step s of item `it` (first block: the workgroup's g-th).
-  auto load_step = [&](const Item& it, int g, int s) __attribute__((always_inline)) {
-    if (k_wave) load_block(it, s + 1, (g + s + 1) % NB);
-    else load_block(it, s, (g + s) % NB);
-  };
-  // K block 0 and steps 0 .. A - 1 (those that exist) of an item; nothing
-  // for an item without keys.
-  auto load_head = [&](const Item& it, int g) __attribute__((always_inline)) {
-    if (it.nblk == 0) return;
-    if (k_wave) load_block(it, 0, g % NB);
+  // K block 0 and block steps 0 .. A - 1 (those that exist) of an item;
+  // nothing for an item without keys. Block b of every item goes to slot
+  // b % NB.
+  // The K waves' part (K blocks 0 .. A) and the V waves' part (V blocks
+  // 0 .. A - 1) can be issued apart.
+  auto load_head_k = [&](const Item& it) __attribute__((always_inline)) {
+    if (it.nblk == 0 || !k_wave) return;
+    load_block(it, 0, 0);
 #pragma unroll
     for (int s0 = 0; s0 < A; ++s0)
-      if (s0 < it.nblk) load_step(it, g, s0);
+      if (s0 < it.nblk) load_block(it, s0 + 1, s0 + 1);
+  };
+  auto load_head_v = [&](const Item& it) __attribute__((always_inline)) {
+    if (it.nblk == 0 || k_wave) return;
+#pragma unroll
+    for (int s0 = 0; s0 < A; ++s0)
+      if (s0 < it.nblk) load_block(it, s0, s0);
+  };
+  auto load_head = [&](const Item& it) __attribute__((always_inline)) {
+    load_head_k(it);
+    load_head_v(it);
+  };
+  // The block loop's loads: step j + A of the item, issued in iteration j,
+  // whose slot phase S = j % NB is a compile-time constant there. The wave's
+  // row pointer and first key advance by one block per step, so a full
+  // block's loads take no address arithmetic beyond M0.
+  uint32_t doffs[IPW];  // doff[i] plus load i's row offset (< 2^32: strides checked on the host)
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) doffs[i] = doff[i] + static_cast<uint32_t>(i * RPI * st_b);
+  const char* rp = nullptr;  // this wave's first row of its next step's block
+  int rk = 0;                // that row's key index
+  auto loop_loads_start = [&](const Item& it) {
+    rk = (A + (k_wave ? 1 : 0)) * 32 + row0w;
+    rp = reinterpret_cast<const char*>(k_wave ? it.kb : it.vb) + rk * st_b;
+  };
+  auto load_step_c = [&](const Item& it, int j, auto S) __attribute__((always_inline)) {
+    constexpr int s = decltype(S)::value;
+    const int lds0 = (k_wave ? s * BLKB : VOFF + ((s + NB - 1) % NB) * BLKB) + row0w * RB;
+    if (rk + IPW * RPI <= it.kfull) {
+#pragma unroll
+      for (int i = 0; i < IPW; ++i) dma(rp, doffs[i], lds0 + i * 1024);
+    } else {
+      load_block(it, j + A + (k_wave ? 1 : 0), k_wave ? s : (s + NB - 1) % NB);
+    }
+    rp += 32 * st_b;
+    rk += 32;
   };
   // Wait until at most n of this wave's loads are in flight (they complete
   // in issue order; other memory operations issued among them only make the
@@ -280,12 +409,13 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
   // K operands of the block in slot ks: lane (h, c) reads key c, dims
   // 16jj + 8h..+8, i.e. chunk 2jj + h at position (2jj + h) ^ swz(c): byte
   // c RB + ((32 jj) ^ 16 (h ^ swz(c))), the XOR staying inside the row.
-  const int ka = c * RB + 16 * (h ^ swz(c));
-  u32x4 kop[KJ];
-  auto kread = [&](int ks) {
-    const int kb = ks * BLKB + ka;
+  int kaj[KJ];
 #pragma unroll
-    for (int jj = 0; jj < KJ; ++jj) kop[jj] = *reinterpret_cast<const u32x4*>(smem + (kb ^ (32 * jj)));
+  for (int jj = 0; jj < KJ; ++jj) kaj[jj] = (c * RB + 16 * (h ^ swz(c))) ^ (32 * jj);
+  u32x4 kop[KJ];
+  auto kread = [&](auto ks) {
+#pragma unroll
+    for (int jj = 0; jj < KJ; ++jj) kop[jj] = *reinterpret_cast<const u32x4*>(smem + ks * BLKB + kaj[jj]);
   };
   // S^T(block) = K Q^T: lane (h, c) gets query c's scores of keys
   // 8(e/4) + 4h + e%4 of the block.
@@ -297,12 +427,11 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
   };
   float m = kNegInfP, l = 0.f;  // query c's running max (log2 domain) and this lane's share of its sum
   f32x16 acc[NU];
-  // Masking, the running max and the (rare) rescale for block blk's scores.
-  auto softmax_max = [&](const Item& it, f32x16& sc, int blk) {
+  // Keys past k_len, and (causal) keys after the query, only occur in a
+  // sequence's last block or on the diagonal: a wave-uniform branch.
+  auto mask_block = [&](const Item& it, f32x16& sc, int blk) {
     const int kb0 = blk * 32;
-    // Keys past k_len, and (causal) keys after the query, only occur in a
-    // sequence's last block or on the diagonal: a wave-uniform branch.
-    if (kb0 + 32 > it.k_len || (a.causal && kb0 + 31 > it.q0)) {
+    if (blk >= it.jm) {
       const int qq = it.q0 + c;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -310,18 +439,30 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
         if (!(kk < it.k_len && (!a.causal || kk <= qq))) sc[e] = kNegInfP;
       }
     }
+  };
+  // Query c's max over the block (log2 units): the lane's 16 scores, then
+  // the other lane half's through v_permlane32_swap (no LDS round trip).
+  auto block_max = [&](const f32x16& sc) {
     float tmax = kNegInfP;
 #pragma unroll
     for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float mt = tmax * cs;
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * cs;
+  };
+  // The (rare) rescale when the max moves by more than kRescale. Row r of the
+  // accumulators takes row r's alpha from lane r; the bpermute addresses are
+  // formed here, behind an opaque copy, so they hold no registers elsewhere.
+  auto rescale = [&](float mt) {
     if (__any(mt > m + kRescale)) {
       const float m_new = fmaxf(m, mt);
       const float alpha = m_new == kNegInfP ? 1.f : fast_exp2(m - m_new);
       l *= alpha;
+      int lb = 16 * h;
+      asm volatile("" : "+v"(lb));
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float ar = __shfl(alpha, 8 * (e >> 2) + 4 * h + (e & 3), 64);
+        const float ar = __int_as_float(
+            __builtin_amdgcn_ds_bpermute(lb + 4 * (8 * (e >> 2) + (e & 3)), __float_as_int(alpha)));
 #pragma unroll
         for (int u = 0; u < NU; ++u) acc[u][e] *= ar;
       }
@@ -345,56 +486,87 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
       pop[s2] = u32x4{pack2<T>(p[8 * s2], p[8 * s2 + 1]), pack2<T>(p[8 * s2 + 2], p[8 * s2 + 3]),
                       pack2<T>(p[8 * s2 + 4], p[8 * s2 + 5]), pack2<T>(p[8 * s2 + 6], p[8 * s2 + 7])};
   };
-  // O += P V from the V block in slot vs: the B operand of step s, column
+  // V operands of the block in slot vs: the B operand of step s, column
   // tile u is V[keys 16s+4h+e, 16s+8+4h+e][dims 32u + c], read transposed.
   // Lane (h, c) with jl = c % 16 reads 8 bytes of row 4h + jl/4 (+8, +16s),
   // dims 32u + 16(c/16) + 4(jl%4): vofs[u] for the first row; the row 8
-  // further has swz XORed by 2, i.e. the byte offset XORed by 32.
+  // further has swz XORed by 2, i.e. the byte offset XORed by 32. They are
+  // read into registers one block ahead of their P V.
   int vofs[NU];
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
     const int jl = c & 15, r = 4 * h + (jl >> 2), ch = 4 * u + 2 * (c >> 4) + ((jl & 3) >> 1);
     vofs[u] = r * RB + 16 * (ch ^ swz(r)) + 8 * (jl & 1);
   }
-  auto pv = [&](int vs) {
-    const int vb = VOFF + vs * BLKB;
+  int vofx[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) vofx[u] = vofs[u] ^ 32;
+  u32x4 vop[2][NU];
+  auto vread = [&](auto vs) {
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
-        const int lo_b = vb + 16 * s2 * RB + vofs[u];
-        const int hi_b = vb + 16 * s2 * RB + 8 * RB + (vofs[u] ^ 32);
+        const int lo_b = VOFF + vs * BLKB + 16 * s2 * RB + vofs[u];
+        const int hi_b = VOFF + vs * BLKB + 16 * s2 * RB + 8 * RB + vofx[u];
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(smem + lo_b));
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(smem + hi_b));
         const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
-        acc[u] = mfma_k16x32<T>(pop[s2], u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}, acc[u]);
+        vop[s2][u] = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
       }
   };
+  // O += P V of the pending block, operands in registers.
+  auto pv = [&]() {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int u = 0; u < NU; ++u) acc[u] = mfma_k16x32<T>(pop[s2], vop[s2][u], acc[u]);
+  };
 
-  // Software pipeline, one 32-key block per iteration j. On entry S(j) is in
-  // registers, K block j + 1 and V block j are in their LDS slots. The wave
-  // issues block step j + A's loads (into the slots of K(j) and V(j - 1),
-  // both last read before the previous barrier), reads K(j + 1), does the
-  // max/rescale of S(j), then issues the S(j + 1) MFMAs interleaved with the
-  // exponentials of S(j), so the matrix pipe and the VALU work at once, and
-  // finally P(j) V(j). It then waits for step j + 1's rows and meets the
-  // other waves at the barrier. Steps past the last block are not issued;
-  // once they stop, fewer loads than kInFlight are younger than the one a
-  // block needs, so those blocks wait for all of them.
-  auto full = [&](const Item& it, int g, int j, f32x16& cur, f32x16& nxt) {
-    const bool issue = j + A < it.nblk;
-    if (issue) load_step(it, g, j + A);
-    kread((g + j + 1) % NB);
-    softmax_max(it, cur, j);
+  // Software pipeline, one 32-key block per iteration j, whose slot phase
+  // S = j % NB is a compile-time constant (the loop is unrolled NB times, so
+  // every LDS address is a lane offset plus an immediate). On entry S(j) is
+  // in registers, K block j + 1 and V block j are in their LDS slots, and
+  // (PREV) block j - 1's P and V operands are in registers. The wave issues
+  // block step j + A's loads (into the slots of K(j) and V(j - 1), both last
+  // read before the previous barrier) and reads K(j + 1); then P(j - 1)
+  // V(j - 1) runs on the matrix cores under S(j)'s max, and S(j + 1) under
+  // S(j)'s exponentials and the reads of V(j). It then waits for step
+  // j + 1's rows and meets the other waves at the barrier. Steps past the
+  // last block are not issued; once they stop, fewer loads than kInFlight
+  // are younger than the one a block needs, so those blocks wait for all of
+  // them.
+  f32x16 sca, scb;  // S of the even / odd blocks
+  auto full = [&](const Item& it, int j, auto S, auto prev) {
+    constexpr int s = decltype(S)::value;
+    f32x16& cur = (s & 1) ? scb : sca;
+    f32x16& nxt = (s & 1) ? sca : scb;
+    const bool issue = j < it.nblk - A;
+    if (issue) load_step_c(it, j, S);
+    kread(std::integral_constant<int, (s + 1) % NB>{});
+    mask_block(it, cur, j);
+    if constexpr (decltype(prev)::value) pv();
+    const float mt = block_max(cur);
+    if constexpr (decltype(prev)::value) {
+#pragma unroll
+      for (int i = 0; i < 2 * NU; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      }
+    }
+    rescale(mt);
     qk(nxt);
     softmax_exp(cur);
-    // One score MFMA, then a slice of the exponentials, and so on.
+    vread(S);
 #pragma unroll
     for (int jj = 0; jj < KJ; ++jj) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 64 / KJ, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 56 / KJ, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 4 * NU / KJ, 0);
     }
-    pv((g + j) % NB);
+    // P(j) is computed here, under S(j + 1): without this the compiler sinks
+    // the exponentials to their use after the barrier.
+    asm volatile("" : "+v"(pop[0]), "+v"(pop[1]), "+v"(l));
     if (issue) wait_loads(std::integral_constant<int, kInFlight>{});
     else wait_loads(std::integral_constant<int, 0>{});
     lds_barrier();
@@ -435,14 +607,15 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
   // ---- The item loop. The next item's K/V blocks and Q are fetched while
   // X's last block and its output are finished, so its first block is
   // usually in LDS when it starts.
-  int idx = static_cast<int>(blockIdx.x) - wg_base;
+  int round = 0;
+  int idx = item_of(0);
   Item X;
   if (idx < n_items) {
-    resolve(idx, X);
+    resolve_round(0, idx, X);
     load_q(X);
-    load_head(X, 0);
+    load_head(X);
   }
-  int g = 0;  // slot counter: X's block 0 is the workgroup's g-th block
+  using std::integral_constant;
   while (idx < n_items) {
 #pragma unroll
     for (int u = 0; u < NU; ++u)
@@ -451,49 +624,78 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
     m = kNegInfP;
     l = 0.f;
     // X's K(0) and step 0 (steps 1 .. A-1 may still be in flight).
-    if (X.nblk >= A) wait_loads(std::integral_constant<int, kInFlight>{});
-    else wait_loads(std::integral_constant<int, 0>{});
+    if (X.nblk >= A) wait_loads(integral_constant<int, kInFlight>{});
+    else wait_loads(integral_constant<int, 0>{});
     lds_barrier();
-    f32x16 sca, scb;  // S of the even / odd blocks
     // Unconditional, also for an item without keys (whose scores are never
     // used): every path into the block loop then consumes Q here, so the
     // compiler's wait for X's Q loads is placed here and not in the loop,
     // where it would also drain the K/V loads in flight.
-    kread(g % NB);
+    kread(integral_constant<int, 0>{});
     qk(sca);
     // Iteration 0's loads overwrite K(0)'s slot: every wave must have read it.
     lds_barrier();
+    loop_loads_start(X);
     int j = 0;
-    for (; j + 2 < X.nblk; j += 2) {
-      full(X, g, j, sca, scb);
-      full(X, g, j + 1, scb, sca);
+    if (X.nblk > 1) {
+      full(X, 0, integral_constant<int, 0>{}, std::false_type{});
+      j = 1;
+      // S(j) is in scb at the top of each round of NB blocks.
+      for (; j + NB < X.nblk; j += NB) {
+        full(X, j, integral_constant<int, 1 % NB>{}, std::true_type{});
+        full(X, j + 1, integral_constant<int, 2 % NB>{}, std::true_type{});
+        if constexpr (NB == 4) {
+          full(X, j + 2, integral_constant<int, 3>{}, std::true_type{});
+          full(X, j + 3, integral_constant<int, 0>{}, std::true_type{});
+        }
+      }
+      // The remaining blocks but the last, then the last block's scores into sca.
+      if (j + 1 < X.nblk) {
+        full(X, j, integral_constant<int, 1 % NB>{}, std::true_type{});
+        ++j;
+        if constexpr (NB == 4) {
+          if (j + 1 < X.nblk) {
+            full(X, j, integral_constant<int, 2>{}, std::true_type{});
+            ++j;
+            if (j + 1 < X.nblk) {
+              full(X, j, integral_constant<int, 3>{}, std::true_type{});
+              ++j;
+            } else {
+              sca = scb;
+            }
+          }
+        }
+      } else {
+        sca = scb;
+      }
     }
-    if (j + 1 < X.nblk) {
-      full(X, g, j, sca, scb);
-      sca = scb;  // the last block's scores, in one place
-      ++j;
-    }
-    // X's last block j, after all of X's loads have landed: fetch the next
-    // item's blocks and Q behind X's last block, then store X's output. (The
-    // next item's loads go to slots no wave reads any more: X's last V slot is
-    // not among them, and every other slot was last read before the block
-    // loop's final barrier.)
-    const int nidx = idx + (static_cast<int>(gridDim.x) - wg_base);
+    // X's last block j: its P V after the next item's loads are issued.
+    ++round;
+    const int nidx = item_of(round);
     Item Y;
-    if (nidx < n_items) resolve(nidx, Y);
+    // The next item, its Q and its K blocks (the K slots are free: X's last
+    // K read was before the loop's last barrier) are fetched first; its V
+    // blocks wait until every wave has read X's last V block.
+    if (nidx < n_items) {
+      resolve_round(round, nidx, Y);
+      load_q(Y);
+      load_head_k(Y);
+    }
     // (An item without keys has no block: its output is 0/0, as the
     // reference's.)
     if (X.nblk > 0) {
-      softmax_max(X, sca, j);
+      mask_block(X, sca, j);
+      if (X.nblk > 1) pv();
+      rescale(block_max(sca));
       softmax_exp(sca);
+      vread(j % NB);
     }
-    if (nidx < n_items) {
-      load_head(Y, g + X.nblk);
-      load_q(Y);
-    }
-    if (X.nblk > 0) pv((g + j) % NB);
+    // The next item's blocks go to slots 0 .. A: every wave must have read
+    // X's last V block (whichever slot it is in) before they are issued.
+    lds_barrier();
+    if (nidx < n_items) load_head_v(Y);
+    if (X.nblk > 0) pv();
     store_out(X);
-    g += X.nblk;
     X = Y;
     idx = nidx;
   }
