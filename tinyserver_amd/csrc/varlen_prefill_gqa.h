@@ -576,6 +576,9 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
   uint16_t* const ost = reinterpret_cast<uint16_t*>(smem + OOFF) + wave * 8 * ROWO;
   auto store_out = [&](const Item& it) {
     const float rl = 1.f / (l + __shfl_xor(l, 32, 64));  // 1 / query c's denominator
+    float scl[16];  // 1 / l of the rows of this lane's elements, all fetched at once
+#pragma unroll
+    for (int e = 0; e < 16; ++e) scl[e] = __shfl(rl, 8 * (e >> 2) + 4 * h + (e & 3), 64);
     T* const obase = static_cast<T*>(a.out) + it.q_start * a.o_st + (it.kvh * NW + wave) * a.o_sh;
 #pragma unroll
     for (int R = 0; R < 4; ++R) {
@@ -583,7 +586,7 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
 #pragma unroll
       for (int e = 4 * R; e < 4 * R + 4; ++e) {
         const int rr = 4 * h + (e & 3);  // row inside the round
-        const float sc = __shfl(rl, 8 * R + rr, 64);
+        const float sc = scl[e];
 #pragma unroll
         for (int u = 0; u < NU; ++u) ost[rr * ROWO + 32 * u + c] = from_float<T>(acc[u][e] * sc).x;
       }
