@@ -187,3 +187,44 @@ def test_many_short_sequences():
                                  True).cpu()
     ref = ov.flash_attn_varlen_func(q, k, v, cq, ck, max(lens), max(lens), True)
     assert_close(out, ref, what="1000 short sequences")
+
+
+def _run(lens, q, k, v, causal=True):
+    cu = _cu(lens).to(DEV)
+    return flash_attn_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), cu, cu, max(lens), max(lens), causal).cpu()
+
+
+def test_item_plan_limits_match():
+    """The persistent kernel resolves work items from a per-workgroup plan
+    for calls of at most 64 sequences and 256 query tiles per sequence, and
+    by a wave-cooperative search otherwise. A call just past each limit (65
+    sequences; a sequence of 257 tiles) must give its other sequences the
+    same bits as a call within the limit, and the 64-sequence call must match
+    the oracle."""
+    g = torch.Generator().manual_seed(45)
+    lens = torch.randint(1, 201, (65,), generator=g).tolist()
+    q, k, v, _, _ = _inputs(lens, lens, 32, 8, 128, torch.bfloat16, seed=46)
+    t64 = sum(lens[:64])
+    print(f"65 vs 64 sequences ({sum(lens)} / {t64} tokens)", flush=True)
+    out65 = _run(lens, q, k, v)
+    out64 = _run(lens[:64], q[:t64], k[:t64], v[:t64])
+    assert torch.equal(out65[:t64], out64), "65-sequence call vs 64-sequence call"
+    ref = ov.flash_attn_varlen_func(q[:t64], k[:t64], v[:t64], _cu(lens[:64]), _cu(lens[:64]), max(lens[:64]),
+                                    max(lens[:64]), True)
+    assert_close(out64, ref, what="64 sequences vs oracle")
+
+    lens = [40, 300, 8193]  # 257 query tiles in the last sequence
+    q, k, v, _, _ = _inputs(lens, lens, 32, 8, 128, torch.bfloat16, seed=47)
+    print("a 257-tile sequence beside two short ones", flush=True)
+    out_long = _run(lens, q, k, v)
+    out_short = _run(lens[:2], q[:340], k[:340], v[:340])
+    assert torch.equal(out_long[:340], out_short), "short sequences beside a 257-tile one vs alone"
+    scale = 128 ** -0.5
+    got, want = [], []
+    for r in (340, 340 + 8191, 340 + 8192):
+        for h in (0, 31):
+            kk, vv = k[340:r + 1, h // 4].double(), v[340:r + 1, h // 4].double()
+            p = torch.softmax((kk @ q[r, h].double()) * scale, 0)
+            want.append(p @ vv)
+            got.append(out_long[r, h].double())
+    assert_close(torch.stack(got), torch.stack(want), what="257-tile sequence, sampled rows")
