@@ -455,6 +455,15 @@ def bench_mixed(name, steps, warmup, copies=3):
 
     step_us = time_region(step, steps, warmup)[0] * 1e3
     step_one_us = time_region(step_one, steps, warmup)[0] * 1e3
+    # The GPU time of each form without the host's enqueue cost (its eager
+    # launches of small batches are host-bound).
+    step_graph_us = _graph_us_per_call(step, steps, warmup)
+    step_one_graph_us = _graph_us_per_call(step_one, steps, warmup)
+    graph_parts = {k: _graph_us_per_call(f, steps, warmup)
+                   for k, f in (("prefill_norm_rope_store", pre_store), ("prefill_attention", pre_attn),
+                                ("decode_norm_rope_store", dec_store), ("decode_attention", dec_attn),
+                                ("packed_norm_rope_store", packed_store), ("mixed_attention", one_attn),
+                                ("one_kernel", lambda i: one_attn(i, cus)))}
     t = {k: time_region(f, steps, warmup)[0] * 1e3
          for k, f in (("prefill_norm_rope_store", pre_store), ("prefill_attention", pre_attn),
                       ("decode_norm_rope_store", dec_store), ("decode_attention", dec_attn))}
@@ -475,16 +484,19 @@ def bench_mixed(name, steps, warmup, copies=3):
     return {
         "workload": name, "prefill_seqs": len(p.seq_lens), "prefill_tokens": T, "decode_batch": B,
         "sum_ctx": int(d.ctx_lens.sum()), "pool_pages": int(m.k_cache.shape[0]),
-        "step_us": step_us, "sum_of_launches_us": sum(t.values()),
+        "step_us": step_us, "step_graph_us": step_graph_us, "launch_graph_us": graph_parts,
+        "sum_of_launches_us": sum(t.values()),
         "tokens_per_s": (T + B) / (step_us * 1e-6), "launches": launches,
         "order": "prefill norm/RoPE/store -> varlen attention -> decode norm/RoPE/store -> paged attention",
         "one_launch": {
-            "step_us": step_one_us, "tokens_per_s": (T + B) / (step_one_us * 1e-6),
+            "step_us": step_one_us, "step_graph_us": step_one_graph_us,
+            "tokens_per_s": (T + B) / (step_one_us * 1e-6),
             "order": "norm/RoPE/store of both batches' tokens -> mixed_attention (varlen attention + paged "
                      "attention in one kernel, + the decode merge)",
             "norm_rope_store_us": t_one["norm_rope_store"],
             "mixed_attention_us": t_one["mixed_attention"],
-            "mixed_attention_path": "one kernel" if T <= 512 else "two launches (prefill batch over 512 tokens)",
+            "mixed_attention_path": ("one kernel" if T <= 512 and B * d.block_tables.shape[1] * W.PAGE <= 131072
+                                     else "two launches (more than 512 prefill tokens or 131072 decode table tokens)"),
             "one_kernel_us": t_one["one_kernel"],
             "separate_attention_sum_us": t["prefill_attention"] + t["decode_attention"],
             "roofline": {"decode_hbm": _roof_hbm(dbytes, t_one["one_kernel"]),

@@ -210,8 +210,10 @@ int tsa_varlen_prefill(const tsa_view* out, const tsa_view* q, const tsa_view* k
  * decode workgroups (0: one per CU) beside the prefill workgroups, so that
  * each CU runs one of each. prefill_workgroups > 0 asks for that kernel with
  * that many prefill workgroups; 0 takes it for prefill batches of at most 512
- * tokens (the two roles slow each other down on a shared CU, so it pays for
- * short prefill chunks only) and issues the two calls otherwise. */
+ * tokens beside decode block tables spanning at most 131072 tokens (batch x
+ * table width x page size; the two roles slow each other down on a shared
+ * CU, so it pays only when both are small) and issues the two calls
+ * otherwise. */
 int tsa_mixed_attention(const tsa_view* prefill_out, const tsa_view* prefill_q, const tsa_view* prefill_k,
                         const tsa_view* prefill_v, const tsa_view* cu_seqlens, int64_t max_seqlen,
                         double prefill_scale, const tsa_view* out, const tsa_view* query,

@@ -1056,15 +1056,21 @@ namespace tsa {
 
 constexpr int kMixedLds = gqa_smem_bytes<128, 4>();
 // Automatic choice (prefill_workgroups == 0): one kernel only for prefill
-// batches of at most this many tokens. Sharing a CU, the two roles slow each
-// other down -- the LDS-staged prefill's loads wait behind the decode's HBM
-// stream -- so one launch pays only when the prefill is a short chunk beside
-// the decode. Measured on Qwen3-4B heads (one launch vs two):
-//   4 decode (ctx 128-512) + 322 prefill tokens       29.0 vs 37.8 us
-//   120 decode (ctx 256-8192) + 402 prefill tokens    343-346 vs 354.7 us
-//   8 decode (ctx 256-2048) + 2583 prefill tokens     66.9 vs 63.1 us
-//   120 decode (ctx 256-8192) + 5760 prefill tokens   419.4 vs 396.1 us
+// batches of at most kMixedAutoMaxTokens tokens beside a decode batch whose
+// block tables span at most kMixedAutoMaxDecodeTokens tokens (batch x table
+// width x page size, a bound the host knows without reading seq_lens).
+// Sharing a CU, the two roles slow each other down -- the LDS-staged
+// prefill's loads wait behind the decode's HBM stream -- so one launch pays
+// only when both halves are small. Measured on Qwen3-4B heads, one kernel vs
+// the two launches, both replayed from a captured graph:
+//   4 decode (ctx 128-512) + 322 prefill tokens        23.1 vs 26.7 us
+//   16 decode (ctx 256-2048) + 365 prefill tokens      30.3 vs 35.4 us
+//   32 decode (ctx 256-4096) + 402 prefill tokens      67.5 vs 70.7 us
+//   64 decode (ctx 256-4096) + 402 prefill tokens     118.9 vs 117.9 us
+//   120 decode (ctx 256-8192) + 402 prefill tokens    350.3 vs 339.6 us
+//   120 decode (ctx 256-8192) + 5760 prefill tokens   436.1 vs 402.0 us
 constexpr int64_t kMixedAutoMaxTokens = 512;
+constexpr int64_t kMixedAutoMaxDecodeTokens = 131072;
 static_assert(kMixedLds >= 64 * 1024, "the mixed kernel's LDS also holds the decode tile prefixes (at most 64 KB)");
 static_assert(kThreads == 64 * 4 && TSA_DECODE_WAVES_PER_EU == 2,
               "the decode and prefill roles share a 4-wave workgroup compiled for two waves per SIMD");
@@ -1113,11 +1119,13 @@ extern "C" int tsa_mixed_attention(const tsa_view* prefill_out, const tsa_view* 
   // One launch when the decode takes the head_dim-128, 16-token-page,
   // contiguous-row stream kernel, the prefill varlen_prefill_gqa<T, 128, 4>
   // in the same dtype, both halves have work, and the caller asks for it
-  // (prefill_workgroups > 0) or the prefill is a short chunk; else the two
+  // (prefill_workgroups > 0) or both halves are small; else the two
   // launches.
+  const bool small = pa.total_q <= kMixedAutoMaxTokens &&
+                     int64_t{a.B} * a.max_blocks * a.BS <= kMixedAutoMaxDecodeTokens;
   const bool one = dmfma && a.D == 128 && a.BS % 16 == 0 && a.kc_s == a.D && a.vc_s == a.D && a.B > 0 &&
                    pa.nseq > 0 && pa.Hq > 0 && pa.total_q > 0 && prefill_q->dtype == dt &&
-                   prefill_takes_gqa4(pa, pmfma) && (prefill_workgroups > 0 || pa.total_q <= kMixedAutoMaxTokens);
+                   prefill_takes_gqa4(pa, pmfma) && (prefill_workgroups > 0 || small);
   if (!one) {
     if (int rc = prefill_launch(pa, pmfma, prefill_q->dtype, max_seqlen, st)) return rc;
     switch (dt) {

@@ -50,9 +50,10 @@ def mixed_attention(
     head_dim 128 and 4 q-heads per kv head, in the decode's dtype (each CU
     then runs one decode and one prefill workgroup). ``prefill_workgroups``
     > 0 asks for it with that many prefill workgroups; 0 takes it when the
-    prefill batch has at most 512 tokens (a short chunk beside the decode,
-    where it is faster) and the two launches otherwise. Same results either
-    way.
+    prefill batch has at most 512 tokens and the decode's block tables span
+    at most 131072 tokens (batch x table width x page size): both halves
+    small, where it is faster. Otherwise the two launches. Same results
+    either way.
     """
     if prefill_q.dim() != 3 or prefill_k.dim() != 3 or prefill_v.dim() != 3:
         raise ValueError("q, k, v must be 3D tensors")
