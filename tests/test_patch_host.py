@@ -12,7 +12,11 @@
   (server/model/inference_context.py:18-21, decode entries holding only
   "block_table" as engine.py:579-582 builds them), read through the engine
   module's getter when that module imports;
-* the patched forward has no CPU path.
+* the patched forward has no CPU path;
+* the device-resident block tables (BlockTableMirror) equal the padded
+  tables the reference builds, step after step, while uploading only the
+  blocks appended since a list was last seen (the BlockManager's lists only
+  grow in place, server/model/block_manager.py:102-159).
 """
 
 import sys
@@ -26,6 +30,7 @@ import torch
 from tinyserver_amd.inference_context import InferenceContext, get_inference_context, inference_context
 from tinyserver_amd.patches import device_metadata
 from tinyserver_amd.patches import qwen3 as patch_mod
+from tinyserver_amd.patches.block_tables import BlockTableMirror
 
 CPU = torch.device("cpu")
 
@@ -38,8 +43,6 @@ def test_prefill_metadata():
     assert m.block_tables.dtype == torch.int32 and m.block_tables.tolist() == [[4, 9, 0], [2, 0, 0], [0, 1, 7]]
     assert m.cu_seqlens.tolist() == [0, 3, 4, 9] and m.max_seqlen == 5
     assert m.positions is None and m.seq_lens is None
-    # one packed buffer, so one host-to-device transfer
-    assert m.block_tables.untyped_storage().data_ptr() == m.cu_seqlens.untyped_storage().data_ptr()
 
 
 def test_decode_metadata():
@@ -169,3 +172,77 @@ def test_patched_forward_reads_the_engine_context(engine_module):
     engine_module.current = EngineContext("prefill", [{"num_tokens": 2, "block_table": [0]}])
     with torch.no_grad(), pytest.raises(ValueError, match="sum to 2"):
         patched(input_ids=torch.tensor([[1, 2, 3]]), position_ids=torch.tensor([[0, 1, 2]]), use_cache=False)
+
+
+def _padded(tables):
+    width = max(max((len(t) for t in tables), default=0), 1)
+    return [list(t) + [0] * (width - len(t)) for t in tables]
+
+
+def test_block_table_mirror_follows_the_lists():
+    """A run of steps as the BlockManager drives its lists (allocate a fresh
+    list, append one block every few steps, free = a new empty list, batches
+    changing composition), on a mirror small enough to evict and grow: every
+    gathered table equals the zero-padded tables, and a decode step uploads
+    only the blocks appended since the step before."""
+    g = torch.Generator().manual_seed(5)
+    mirror = BlockTableMirror(CPU, rows=4, width=2)
+    live = {}  # sequence -> its block list
+    next_block = 0
+
+    def new_list(n):
+        nonlocal next_block
+        blocks = list(range(next_block, next_block + n))
+        next_block += n
+        return blocks
+
+    for step in range(200):
+        r = torch.rand(3, generator=g).tolist()
+        if r[0] < 0.15 or not live:  # a new sequence: allocate
+            live[step] = new_list(int(1 + 6 * r[1]))
+        if r[2] < 0.1 and len(live) > 1:  # a sequence finishes: free replaces its list
+            seq = sorted(live)[int(r[1] * len(live))]
+            live[seq] = []
+            del live[seq]
+        for seq, blocks in live.items():  # decode growth: one block now and then
+            if (seq + step) % 7 == 0:
+                blocks.append(next_block)
+                next_block += 1
+        batch = [live[s] for s in sorted(live) if (s + step) % 5 != 0] or [next(iter(live.values()))]
+        before = mirror.uploaded
+        appended = sum(len(b) - mirror.entries[id(b)].synced for b in batch
+                       if id(b) in mirror.entries and mirror.entries[id(b)].blocks is b)
+        new = sum(len(b) for b in batch if id(b) not in mirror.entries or mirror.entries[id(b)].blocks is not b)
+        tables, extra = mirror.gather(batch, [len(batch)])
+        assert tables.dtype == torch.int32 and tables.tolist() == _padded(batch), step
+        assert extra.tolist() == [len(batch)]
+        assert mirror.uploaded - before == appended + new  # appended tails and unseen lists only
+    assert mirror.table.shape[0] > 4 or len(mirror.entries) <= 4
+
+
+def test_block_table_mirror_rewrites_a_changed_list():
+    mirror = BlockTableMirror(CPU, rows=2, width=4)
+    a, b = [5, 6, 7], [8]
+    assert mirror.gather([a, b])[0].tolist() == [[5, 6, 7], [8, 0, 0]]
+    a[-1] = 9  # the last synced entry changed in place
+    b.clear()  # shrank
+    assert mirror.gather([a, b])[0].tolist() == [[5, 6, 9], [0, 0, 0]]
+    c = [1, 2]  # a third list takes an evicted row: no stale entries past its end
+    assert mirror.gather([c])[0].tolist() == [[1, 2]]
+    assert mirror.gather([c, a])[0].tolist() == [[1, 2, 0], [5, 6, 9]]
+
+
+def test_decode_steps_upload_appended_blocks_only():
+    """Through device_metadata: after the first step, steps upload only the
+    blocks the sequences gained."""
+    lists = [[3, 4], [5]]
+    ctx = InferenceContext("decode", [{"block_table": t} for t in lists])
+    m = device_metadata(ctx, torch.tensor([[20, 3]]), 2, CPU)
+    mirror = patch_mod._mirrors[CPU]
+    assert m.block_tables.tolist() == [[3, 4], [5, 0]]
+    before = mirror.uploaded
+    lists[1].append(6)
+    ctx = InferenceContext("decode", [{"block_table": t} for t in lists])
+    m = device_metadata(ctx, torch.tensor([[21, 4]]), 2, CPU)
+    assert m.block_tables.tolist() == [[3, 4], [5, 6]] and m.cu_seqlens.tolist() == [0, 1, 2]
+    assert mirror.uploaded - before == 1

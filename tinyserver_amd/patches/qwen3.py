@@ -19,9 +19,10 @@ loop (one launch per sequence at decode, a Python mapping loop at prefill),
 then the attention kernel. Here one fused kernel does QK RMSNorm + RoPE +
 the paged K/V store of every token (store before attend: the new token takes
 part in attention), then varlen prefill or paged decode attention runs. The
-block tables, cu_seqlens and positions are built on the host and copied to
-the device once per forward (the first layer builds them, the others reuse
-them), not once per layer and per sequence.
+metadata is built once per forward (the first layer builds it, the others
+reuse it), not once per layer and per sequence: the block tables live on the
+device (block_tables.BlockTableMirror) and a step uploads only the blocks
+appended since the last one, with cu_seqlens, in one transfer.
 
 Same errors as the reference: ValueError for prefill lengths that do not sum
 to the flattened length or are not positive (:182-187) and for a missing
@@ -37,10 +38,12 @@ import weakref
 from dataclasses import dataclass
 from typing import Any, Callable
 
+import numpy as np
 import torch
 
 from .. import inference_context as _own_context
 from ..kernels import flash_attn_varlen_func, paged_attention_forward, paged_decode_step, qk_norm_rope_store
+from .block_tables import BlockTableMirror
 
 ENGINE_CONTEXT_MODULE = "server.model.inference_context"
 
@@ -95,6 +98,9 @@ class DeviceMetadata:
     table_slots: int = 0            # sum of the block tables' lengths (host-side size of the step's KV)
 
 
+# The device-resident block tables, one mirror per device.
+_mirrors: dict[torch.device, BlockTableMirror] = {}
+
 # The last build: (weak reference to its context, position_ids, key, metadata).
 # One entry suffices: the layers of a forward run one after another on the
 # engine's single thread (the reference's own assumption for its context,
@@ -105,9 +111,10 @@ _last_build: tuple | None = None
 def device_metadata(ctx: Any, position_ids: torch.Tensor | None, num_tokens: int,
                     device: torch.device) -> DeviceMetadata:
     """Build the padded block tables, cu_seqlens and, for a decode step, the
-    positions and sequence lengths, with the reference's checks. The tables
-    and cu_seqlens are packed into one int32 buffer on the host and copied in
-    one transfer; the device tensors are views of it.
+    positions and sequence lengths, with the reference's checks. The block
+    tables come from the device's BlockTableMirror, which uploads only the
+    blocks appended since it last saw each sequence's list; cu_seqlens rides
+    in the same transfer.
 
     ``ctx`` is any object with ``mode`` and ``sequences`` (the reference's
     InferenceContext, server/model/inference_context.py:18-21). The layers of
@@ -136,22 +143,19 @@ def device_metadata(ctx: Any, position_ids: torch.Tensor | None, num_tokens: int
         if len(seqs) != num_tokens:
             raise ValueError(f"Decode step has {num_tokens} tokens for {len(seqs)} sequences")
         lengths = [1] * len(seqs)
-    width = max(max((len(s["block_table"]) for s in seqs), default=0), 1)
-    n_tab = len(seqs) * width
-    packed = torch.zeros(n_tab + len(seqs) + 1, dtype=torch.int32)  # [tables | cu_seqlens]
-    tables = packed[:n_tab].view(len(seqs), width)
-    for i, s in enumerate(seqs):
-        bt = s["block_table"]
-        if len(bt):
-            tables[i, : len(bt)] = torch.as_tensor(bt, dtype=torch.int32)
-    packed[n_tab + 1:] = torch.as_tensor(lengths, dtype=torch.int32).cumsum(0)
+    tables = [s["block_table"] for s in seqs]
+    cu = np.zeros(len(seqs) + 1, dtype=np.int64)
+    np.cumsum(lengths, out=cu[1:])
+    mirror = _mirrors.get(device)
+    if mirror is None:
+        mirror = _mirrors[device] = BlockTableMirror(device)
+    block_tables, cu_seqlens = mirror.gather(tables, cu)
     positions = seq_lens = None
     if ctx.mode != "prefill":
         positions = position_ids.reshape(-1).to(device=device, dtype=torch.int32)
         seq_lens = positions + 1
-    dev = packed.to(device)
-    meta = DeviceMetadata(dev[:n_tab].view(len(seqs), width), dev[n_tab:], max(lengths, default=0), positions,
-                          seq_lens, sum(len(s["block_table"]) for s in seqs))
+    meta = DeviceMetadata(block_tables, cu_seqlens, max(lengths, default=0), positions, seq_lens,
+                          sum(len(t) for t in tables))
     try:
         ref = weakref.ref(ctx)
     except TypeError:  # (e.g. a slotted class without __weakref__): no caching
