@@ -84,6 +84,21 @@ def test_fused_store(mode):
     else:
         w = W.make("qwen3-4b-prefill-8seq", poison=True)
         cu, pos = w.cu_seqlens, None
+    _store_and_check(w, cu, pos)
+
+
+# Head layouts around the 8-lanes-per-row kernel's edges (a token's H rows
+# on 8*H lanes in whole waves): waves holding both q and k rows (Hq not a
+# multiple of 8), dead lanes in the last wave (H not a multiple of 8), the
+# 32B shape (9 waves), H = 128 (1024 lanes, the largest it takes) and
+# H = 136 (past it: the per-row kernel).
+@pytest.mark.parametrize("hq,hkv", [(6, 2), (12, 4), (5, 1), (40, 8), (64, 8), (120, 8), (128, 8)])
+def test_fused_store_head_layouts(hq, hkv):
+    w = W.make_prefill("heads", 12, 3, hq, hkv, 5, 40, poison=True)
+    _store_and_check(w, w.cu_seqlens, None)
+
+
+def _store_and_check(w, cu, pos):
     kc, vc = w.k_cache.to(DEV), w.v_cache.to(DEV)
     qg, kg = qk_norm_rope_store(w.q.to(DEV), w.k.to(DEV), w.v.to(DEV), w.q_weight.to(DEV), w.k_weight.to(DEV),
                                 w.cos.to(DEV), w.sin.to(DEV), w.eps, kc, vc, w.block_tables.to(DEV), cu.to(DEV),

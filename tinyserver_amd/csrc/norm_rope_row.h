@@ -83,4 +83,84 @@ __device__ __forceinline__ void norm_rope_row(const float (&x)[8], const float (
   }
 }
 
+// Two values rounded to T (a pair shares one v_cvt_pk) and widened again.
+template <typename T>
+__device__ __forceinline__ void round2_t(float& a, float& b) {
+  const uint32_t p = pack2<T>(a, b);
+  a = lo_f<T>(p);
+  b = hi_f<T>(p);
+}
+
+// The same row computation for head_dim 128 and a 16-bit T in another lane
+// layout: 8 lanes per row, lane c holding dims 8c..8c+7 (chunk 0) and
+// 64+8c..64+8c+7 (chunk 1) as packed pairs. A dim's RoPE partner (d +- 64)
+// is then in the same lane, and one DPP instruction serves the 8 rows of a
+// wave. The arithmetic, its rounding points and the order of the sum of
+// squares are those of norm_rope_row, so the two agree bit for bit: the
+// CPU order's accumulator k = c % 4 takes chunks k, k+4, k+8, k+12, which
+// are lane k's chunk 0, lane k+4's chunk 0, lane k's chunk 1 and lane
+// k+4's chunk 1. Every lane must run this (lanes 8r..8r+7 form a row).
+template <typename T>
+__device__ __forceinline__ void norm_rope_row_d128x8(const u32x4 (&xp)[2], const u32x4 (&wp)[2], const u32x4 (&cp)[2],
+                                                     const u32x4 (&sp)[2], float eps, u32x4 (&op)[2]) {
+  static_assert(sizeof(T) == 2, "16-bit element types only");
+  float x[2][8];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[j][2 * i] = lo_f<T>(xp[j][i]);
+      x[j][2 * i + 1] = hi_f<T>(xp[j][i]);
+    }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float s0 = __fmul_rn(x[0][e], x[0][e]), s1 = __fmul_rn(x[1][e], x[1][e]);
+    float acc = __fadd_rn(s0, dpp_row_shl<4>(s0));
+    acc = __fadd_rn(acc, s1);
+    acc = __fadd_rn(acc, dpp_row_shl<4>(s1));
+    float v = acc;
+    v = __fadd_rn(v, dpp_row_shl<1>(acc));
+    v = __fadd_rn(v, dpp_row_shl<2>(acc));
+    v = __fadd_rn(v, dpp_row_shl<3>(acc));
+    ss = __fadd_rn(ss, v);  // meaningful in lane 0 of each 8-lane row
+  }
+  // Broadcast lane 0 of each 8-lane row: quad_perm(0,0,0,0) fills lanes
+  // 0-3 (and 8-11) from lane 0 (8), then row_shr:4 restricted to banks 1
+  // and 3 copies lanes 0-3 (8-11) into lanes 4-7 (12-15).
+  int b = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, ss), 0x00, 0xF, 0xF, false);
+  b = __builtin_amdgcn_update_dpp(b, b, 0x114, 0xF, 0xA, false);
+  ss = __builtin_bit_cast(float, b);
+  const float var = __fdiv_rn(ss, 128.0f);
+  const float rinv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
+
+  float z[2][8];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float y0 = __fmul_rn(x[j][2 * i], rinv), y1 = __fmul_rn(x[j][2 * i + 1], rinv);
+      round2_t<T>(y0, y1);
+      float z0 = __fmul_rn(lo_f<T>(wp[j][i]), y0), z1 = __fmul_rn(hi_f<T>(wp[j][i]), y1);
+      round2_t<T>(z0, z1);
+      z[j][2 * i] = z0;
+      z[j][2 * i + 1] = z1;
+    }
+  // rotate_half: dims < 64 (chunk 0) pair with -z[d + 64], dims >= 64 with z[d - 64].
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float c0 = lo_f<T>(cp[j][i]), c1 = hi_f<T>(cp[j][i]);
+      const float s0 = lo_f<T>(sp[j][i]), s1 = hi_f<T>(sp[j][i]);
+      const float r0 = j == 0 ? -z[1][2 * i] : z[0][2 * i];
+      const float r1 = j == 0 ? -z[1][2 * i + 1] : z[0][2 * i + 1];
+      float a0 = __fmul_rn(z[j][2 * i], c0), a1 = __fmul_rn(z[j][2 * i + 1], c1);
+      round2_t<T>(a0, a1);
+      float b0 = __fmul_rn(r0, s0), b1 = __fmul_rn(r1, s1);
+      round2_t<T>(b0, b1);
+      op[j][i] = pack2<T>(__fadd_rn(a0, b0), __fadd_rn(a1, b1));
+    }
+}
+
 }  // namespace tsa

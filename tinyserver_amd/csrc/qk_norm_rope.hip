@@ -14,11 +14,15 @@
 // single rounding exactly as torch does it; fp32 arithmetic uses the _rn
 // intrinsics so no multiply-add is contracted across a rounding point.
 //
-// Layout: one lane owns 8 consecutive elements of a (token, head) row, so a
-// D=128 row is 16 lanes and the RoPE partner elements (i +- D/2) sit in lane
-// c ^ (D/16), one cross-lane exchange away. Rows are ordered token-major
+// Layout (the per-row and per-token kernels): one lane owns 8 consecutive
+// elements of a (token, head) row, so a D=128 row is 16 lanes and the RoPE
+// partner elements (i +- D/2) sit in lane c ^ (D/16), one cross-lane exchange
+// away. The 16-bit head-dim-128 kernel (qk_norm_rope_rows8) gives a lane 16
+// elements, dims d and d + 64, so a row is 8 lanes and the partner is local. Rows are ordered token-major
 // (all Hq + Hkv heads of a token are adjacent) so a token's cos/sin and its
 // block-table lookup are shared by neighbouring lanes.
+#include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "kv_store.h"
@@ -199,9 +203,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs<T> a) {
 
 static bool vec_ok(const tsa_view* v) { return v == nullptr || v->data == nullptr || rows_vec16(v); }
 
-// Head-dim-128 path: one workgroup per token, 16 groups of 16 lanes; group g
-// takes the token's rows (heads, q first then k) g, g + 16, ..., at most R of
-// them. The token is workgroup-uniform, so its cos/sin are loaded once per
+// Head-dim-128 path for fp32 (and for 16-bit types whose head strides do not
+// fit the 8-lanes-per-row kernel's int offsets): one workgroup per token, 16
+// groups of 16 lanes; group g takes the token's rows (heads, q first then k)
+// g, g + 16, ..., at most R of them. The token is workgroup-uniform, so its cos/sin are loaded once per
 // lane and its cache slot is found with scalar loads, and the rows of a lane
 // differ only by a head stride. The q/k/v rows are read once and the cache
 // rows are not read back here, so those go non-temporal; the rotated q and k
@@ -259,6 +264,77 @@ __global__ __launch_bounds__(256) void qk_norm_rope_token(NormRopeArgs<T> a) {
   }
 }
 
+// Head-dim-128 path for 16-bit types: one workgroup per token and 8 lanes
+// per (token, head) row, 8*H lanes for a token's H = Hq + Hkv rows (q first,
+// then k), rounded up to whole waves. Lane c of a row holds dims 8c..8c+7
+// and 64+8c..64+8c+7 (norm_rope_row_d128x8), so no row needs a second pass
+// and a wave's VALU work serves 8 rows. The token is workgroup-uniform: its
+// cos/sin rows, its cache slot (scalar loads) and the scalar part of every
+// address are shared, and the per-lane part is a head offset the host has
+// checked fits 32 bits. Q/K/V rows are read once and the cache rows are not
+// read back here, so those go non-temporal; the rotated q and k stay
+// ordinary stores (the attention reads them next).
+template <typename T>
+__global__ __launch_bounds__(1024) void qk_norm_rope_rows8(NormRopeArgs<T> a) {
+  const int t = blockIdx.x;
+  const int Hq = static_cast<int>(a.Hq), H = static_cast<int>(a.Hq + a.Hkv);
+  const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
+  const int hh = min(r, H - 1);  // lanes past the last row redo it (never stored)
+  const bool is_k = hh >= Hq;
+  const int h = is_k ? hh - Hq : hh;
+  const int d0 = 8 * c;
+  const bool store = a.k_cache != nullptr;
+
+  const T* src = is_k ? a.k + t * a.k_st + (h * static_cast<int>(a.k_sh) + d0)
+                      : a.q + t * a.q_st + (h * static_cast<int>(a.q_sh) + d0);
+  const T* w = (is_k ? a.kw : a.qw) + d0;
+  const T* cs = a.cos + t * a.cos_st + d0;
+  const T* sn = a.sin + t * a.sin_st + d0;
+  u32x4 xp[2], wp[2], cp[2], sp[2];
+  RawRow<T> vv[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    xp[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 64 * j));
+    wp[j] = *reinterpret_cast<const u32x4*>(w + 64 * j);
+    cp[j] = *reinterpret_cast<const u32x4*>(cs + 64 * j);
+    sp[j] = *reinterpret_cast<const u32x4*>(sn + 64 * j);
+  }
+  const T* vrow = a.v + t * a.v_st + (max(hh - Hq, 0) * static_cast<int>(a.v_sh) + d0);
+  if (store && is_k) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) vv[j] = load_raw_nt<T>(vrow + 64 * j);
+  }
+  // The token's cache slot (scalar loads, while the rows are in flight), in
+  // the waves that hold a k row.
+  int64_t blk = 0, slot = 0;
+  const bool placed =
+      store && __builtin_amdgcn_ballot_w64(is_k) != 0 && a.addr.locate(t, a.BS, a.NB, blk, slot);
+
+  u32x4 op[2];
+  norm_rope_row_d128x8<T>(xp, wp, cp, sp, a.eps, op);
+  if (r >= H) return;
+  if (!is_k) {
+    T* dst = a.q_out + t * a.qo_st + (h * static_cast<int>(a.qo_sh) + d0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) *reinterpret_cast<u32x4*>(dst + 64 * j) = op[j];
+    return;
+  }
+  if (a.k_out) {
+    T* dst = a.k_out + t * a.ko_st + (h * static_cast<int>(a.ko_sh) + d0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) *reinterpret_cast<u32x4*>(dst + 64 * j) = op[j];
+  }
+  if (placed) {
+    T* kd = a.k_cache + (blk * a.kc_b + slot * a.kc_s) + (h * static_cast<int>(a.kc_h) + d0);
+    T* vd = a.v_cache + (blk * a.vc_b + slot * a.vc_s) + (h * static_cast<int>(a.vc_h) + d0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      __builtin_nontemporal_store(op[j], reinterpret_cast<u32x4*>(kd + 64 * j));
+      store_raw_nt<T>(vd + 64 * j, vv[j]);
+    }
+  }
+}
+
 // Largest element offset a view reaches (0 for an absent view).
 static int64_t max_offset(const tsa_view* v) {
   if (!v || !v->data) return 0;
@@ -275,6 +351,18 @@ static int launch_norm_rope(const NormRopeArgs<T>& a, bool vec, bool idx32, hipS
   // Unit innermost strides everywhere (vec) and at most 80 heads per token:
   // the token-per-workgroup kernel.
   const int64_t H = a.Hq + a.Hkv;
+  if constexpr (D == 128 && sizeof(T) == 2) {
+    // Every per-lane head offset (head index x head stride, plus the row's
+    // 128 elements) must fit an int for the 8-lanes-per-row kernel.
+    const int64_t hs = std::max({std::abs(a.q_sh) * a.Hq, std::abs(a.qo_sh) * a.Hq, std::abs(a.k_sh) * a.Hkv,
+                                 std::abs(a.ko_sh) * a.Hkv, std::abs(a.v_sh) * a.Hkv, std::abs(a.kc_h) * a.Hkv,
+                                 std::abs(a.vc_h) * a.Hkv});
+    if (vec && a.T_ <= INT32_MAX && H <= 128 && hs + D < INT32_MAX) {
+      const int threads = static_cast<int>((8 * H + 63) / 64 * 64);
+      qk_norm_rope_rows8<T><<<dim3(static_cast<uint32_t>(a.T_)), dim3(threads), 0, stream>>>(a);
+      return check_launch("tsa_qk_norm_rope");
+    }
+  }
   if constexpr (D == 128) {
     if (vec && a.T_ <= INT32_MAX && H <= 80) {
       const dim3 grid(static_cast<uint32_t>(a.T_));
