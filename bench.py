@@ -15,7 +15,8 @@ Also measured (in "secondary"), each with its roofline and a CPU baseline:
   qwen3-0.6b-decode-bs4     the reference's CPU-runnable decode case
   qwen3-32b-decode-bs32     32k-context decode
   qwen3-8b-prefill-16seq    varlen prefill (TFLOP/s against 2.5 PFLOP/s bf16
-                            dense) and its fused norm/RoPE/store (GB/s)
+                            dense), its fused norm/RoPE/store (GB/s) and
+                            the standalone K/V store (GB/s), mapped and paged
   qwen3-4b-mixed            the continuous-batching step on one shared pool,
                             in scheduler order: the prefill batch's
                             norm/RoPE/store and varlen attention, then the
@@ -124,6 +125,12 @@ def norm_store_bytes(tokens, hq, hkv, d=128, elem=2):
     and the two weights; write the rotated q and k and the K/V cache rows."""
     return (elem * tokens * d * (hq + 2 * hkv) + 2 * elem * tokens * d + 2 * elem * d
             + elem * tokens * d * (hq + hkv) + 2 * elem * tokens * hkv * d)
+
+
+def kv_store_bytes(tokens, hkv, d=128, elem=2):
+    """Algorithmic bytes of the paged K/V store: read the new K and V rows,
+    write them into the pool."""
+    return 4 * elem * tokens * hkv * d
 
 
 def _roof_hbm(nbytes, us):
@@ -329,7 +336,8 @@ def bench_decode(name, steps, warmup, num_workgroups=0, copies=3, with_block=Fal
 
 def bench_prefill(name, steps, warmup):
     from tinyserver_amd import workloads as W
-    from tinyserver_amd.kernels import flash_attn_varlen_func, qk_norm_rope_store
+    from tinyserver_amd.kernels import (flash_attn_varlen_func, qk_norm_rope_store, store_kv_cache_batched,
+                                        store_kv_cache_paged)
 
     dev = torch.device("cuda:0")
     w = W.make(name, device=dev)
@@ -351,6 +359,28 @@ def bench_prefill(name, steps, warmup):
     ns_us = time_region(norm_store, steps, warmup)[0] * 1e3
     ns_bytes = norm_store_bytes(T, hq, hkv)
 
+    # The standalone K/V store, as the reference's prefill calls it: the new
+    # rows as a contiguous (Hkv, T, D) copy and int64 block/slot mappings
+    # (server/model/patches/qwen3.py:296-313), and the one-launch form with
+    # device-side addressing from the block tables and cu_seqlens.
+    k_src, v_src = w.k.transpose(0, 1).contiguous(), w.v.transpose(0, 1).contiguous()
+    page = w.k_cache.shape[2]
+    seq_of = torch.repeat_interleave(torch.arange(len(w.seq_lens), device=dev), w.seq_lens.to(dev))
+    pos = torch.arange(T, device=dev) - w.cu_seqlens.long()[seq_of]
+    block_mapping = w.block_tables.long()[seq_of, pos // page]
+    slot_mapping = pos % page
+
+    def kv_store_mapped(i):
+        store_kv_cache_batched(k_src, v_src, w.k_cache, w.v_cache, block_mapping, slot_mapping)
+
+    def kv_store_paged(i):
+        store_kv_cache_paged(w.k.transpose(0, 1), w.v.transpose(0, 1), w.k_cache, w.v_cache, w.block_tables,
+                             w.cu_seqlens)
+
+    kv_bytes = kv_store_bytes(T, hkv)
+    kvm_us = time_region(kv_store_mapped, steps, warmup)[0] * 1e3
+    kvp_us = time_region(kv_store_paged, steps, warmup)[0] * 1e3
+
     def block(i):
         qr, kr = qk_norm_rope_store(w.q, w.k, w.v, w.q_weight, w.k_weight, w.cos, w.sin, w.eps, w.k_cache,
                                     w.v_cache, w.block_tables, w.cu_seqlens)
@@ -365,6 +395,8 @@ def bench_prefill(name, steps, warmup):
         "roofline": {**_roof_mfma(flops, us), "kernel": "varlen_prefill_gqa"},
         "norm_rope_store_us": ns_us, "norm_rope_store_gbs": ns_bytes / (ns_us * 1e-6) / 1e9,
         "norm_rope_store_roofline": _roof_hbm(ns_bytes, ns_us),
+        "kv_store_mapped_us": kvm_us, "kv_store_mapped_roofline": _roof_hbm(kv_bytes, kvm_us),
+        "kv_store_paged_us": kvp_us, "kv_store_paged_roofline": _roof_hbm(kv_bytes, kvp_us),
         "block_us_per_call": block_us,
     }, w
 
