@@ -50,11 +50,12 @@ __device__ __forceinline__ void seq_range(const int32_t* cu, int64_t stride, int
 constexpr int kPlanItems = 64, kPlanSeqs = 64, kPlanLevels = 256;
 
 // LDS bytes of prefill_gqa_body<D, NW>: NB K and NB V block slots of 32 rows,
-// the output staging (8 rows per wave), the per-sequence query-block counts
-// and the work-item plan.
+// the output staging (one 32-dim column tile of the 32 queries per wave),
+// the per-sequence query-block counts and the work-item plan.
+constexpr int kOutStage = 32 * 64;  // bytes of output staging per wave
 template <int D, int NW>
 constexpr int gqa_smem_bytes() {
-  return 2 * (NW == 2 ? 2 : 4) * (32 * 2 * D) + NW * 8 * (D + 8) * 2 + max_persist_seqs(NW) * 2 +
+  return 2 * (NW == 2 ? 2 : 4) * (32 * 2 * D) + NW * kOutStage + max_persist_seqs(NW) * 2 +
          kPlanItems * 6 * 4 + kPlanLevels * 4;
 }
 
@@ -75,13 +76,15 @@ constexpr int gqa_smem_bytes() {
 //     reads key c, dims 16jj + 8h..+8 (the swizzle puts the 16 rows of a
 //     128-bit read in 16 distinct bank quads) and holds query c's Q slice in
 //     registers; it gets query c's scores of keys 8(e/4) + 4h + e%4;
-//   O(32 queries x 32 dims) += P V over two 16-key steps s: the P operand's
-//     k-slots 8h..8h+7 are keys 16s+4h+0..3 and 16s+8+4h+0..3, i.e. the score
-//     accumulators 8s..8s+7 of the same lane, so P goes to the operand in
-//     registers; the V operand comes from two ds_read_b64_tr_b16, in which a
-//     16-lane group whose lane 4e+q reads dims 4q..4q+3 of key row e gets, in
-//     lane j, element e = V[key e][dim j]. V stays row-major in LDS, and the
-//     swizzle keeps these reads free of bank conflicts too.
+//   O^T(32 dims x 32 queries) += V^T P^T over two 16-key steps s: the P^T
+//     operand's k-slots 8h..8h+7 are keys 16s+4h+0..3 and 16s+8+4h+0..3,
+//     i.e. the score accumulators 8s..8s+7 of the same lane, so P goes to the
+//     operand in registers; the V^T operand comes from two ds_read_b64_tr_b16,
+//     in which a 16-lane group whose lane 4e+q reads dims 4q..4q+3 of key row
+//     e gets, in lane j, element e = V[key e][dim j]. V stays row-major in
+//     LDS, and the swizzle keeps these reads free of bank conflicts too.
+//     Lane (h, c) accumulates query c's outputs, so the softmax's row scales
+//     (the rescale and 1/l) are the lane's own.
 // Scores, probabilities and the output accumulators all stay in VGPRs (at most
 // 256 per wave, two waves per SIMD); the workgroups sharing a CU drift apart,
 // so one workgroup's softmax overlaps another's MFMAs.
@@ -92,7 +95,6 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
   constexpr int NU = D / 32;              // 32-dim column tiles of the output
   constexpr int CPR = D / 8;              // 16-byte chunks per K/V row
   constexpr int RB = 2 * D;               // bytes per K/V row in LDS (unpadded)
-  constexpr int ROWO = D + 8;             // output staging row stride, elements
   constexpr int BLKB = 32 * RB;           // bytes per 32-row K or V block
   // K/V block slots in LDS and the prefetch distance in blocks: the loads
   // of a block are issued A iterations before it is needed.
@@ -100,8 +102,8 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
   constexpr int RPI = 1024 / RB;          // rows per 1 KB load instruction
   constexpr int IPW = 2 * (32 / RPI) / NW;  // load instructions per wave per block step
   constexpr int VOFF = NB * BLKB;           // byte offset of the V slots
-  constexpr int OOFF = 2 * NB * BLKB;       // byte offset of the output staging (8 rows per wave)
-  constexpr int QOFF = OOFF + NW * 8 * ROWO * 2;  // byte offset of the per-sequence query-block counts
+  constexpr int OOFF = 2 * NB * BLKB;       // byte offset of the output staging
+  constexpr int QOFF = OOFF + NW * kOutStage;  // byte offset of the per-sequence query-block counts
   constexpr int PLOFF = QOFF + max_persist_seqs(NW) * 2;  // byte offset of the item plan
   constexpr int LVOFF = PLOFF + kPlanItems * 6 * 4;       // byte offset of the level table
   static_assert(LVOFF + kPlanLevels * 4 == gqa_smem_bytes<D, NW>(), "LDS layout and its size agree");
@@ -449,23 +451,17 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
     return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * cs;
   };
-  // The (rare) rescale when the max moves by more than kRescale. Row r of the
-  // accumulators takes row r's alpha from lane r; the bpermute addresses are
-  // formed here, behind an opaque copy, so they hold no registers elsewhere.
+  // The (rare) rescale when the max moves by more than kRescale; a lane's
+  // accumulators are its own query's, so they take its own alpha.
   auto rescale = [&](float mt) {
     if (__any(mt > m + kRescale)) {
       const float m_new = fmaxf(m, mt);
       const float alpha = m_new == kNegInfP ? 1.f : fast_exp2(m - m_new);
       l *= alpha;
-      int lb = 16 * h;
-      asm volatile("" : "+v"(lb));
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float ar = __int_as_float(
-            __builtin_amdgcn_ds_bpermute(lb + 4 * (8 * (e >> 2) + (e & 3)), __float_as_int(alpha)));
+      for (int u = 0; u < NU; ++u)
 #pragma unroll
-        for (int u = 0; u < NU; ++u) acc[u][e] *= ar;
-      }
+        for (int e = 0; e < 16; ++e) acc[u][e] *= alpha;
       m = m_new;
     }
   };
@@ -515,12 +511,16 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
         vop[s2][u] = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
       }
   };
-  // O += P V of the pending block, operands in registers.
+  // O^T += V^T P^T of the pending block, operands in registers. The P and
+  // V operand registers serve as B and A: lane (h, c) holds P[query c][k-slots
+  // 8h..8h+7] and V[k-slots 8h..8h+7][dim 32u + c], which are the B operand
+  // of P^T and the A operand of V^T. So lane (h, c) accumulates query c's
+  // outputs, dims 32u + 8(e/4) + 4h + e%4: its row scales are its own.
   auto pv = [&]() {
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int u = 0; u < NU; ++u) acc[u] = mfma_k16x32<T>(pop[s2], vop[s2][u], acc[u]);
+      for (int u = 0; u < NU; ++u) acc[u] = mfma_k16x32<T>(vop[s2][u], pop[s2], acc[u]);
   };
 
   // Software pipeline, one 32-key block per iteration j, whose slot phase
@@ -572,34 +572,34 @@ __device__ __forceinline__ void prefill_gqa_body(PrefillArgs a, const int32_t* _
     lds_barrier();
   };
   // The output tile of a finished item, normalised and stored through this
-  // wave's 8-row staging area in four rounds of 8 rows, as 16-byte chunks.
-  uint16_t* const ost = reinterpret_cast<uint16_t*>(smem + OOFF) + wave * 8 * ROWO;
+  // wave's staging area (32 rows of 64 bytes) in NU rounds, one 32-dim
+  // column tile per round: each lane writes its query's four 4-dim runs as
+  // 8-byte pieces, then the wave stores whole 64-byte row segments as
+  // 16-byte chunks. Chunk q of row r sits at position q ^ ((r >> 2) & 3),
+  // which keeps a wave's writes within two-way bank conflicts.
+  char* const ost = smem + OOFF + wave * kOutStage;
   auto store_out = [&](const Item& it) {
     const float rl = 1.f / (l + __shfl_xor(l, 32, 64));  // 1 / query c's denominator
-    float scl[16];  // 1 / l of the rows of this lane's elements, all fetched at once
-#pragma unroll
-    for (int e = 0; e < 16; ++e) scl[e] = __shfl(rl, 8 * (e >> 2) + 4 * h + (e & 3), 64);
     T* const obase = static_cast<T*>(a.out) + it.q_start * a.o_st + (it.kvh * NW + wave) * a.o_sh;
+    const int wsw = (c >> 2) & 3;
 #pragma unroll
-    for (int R = 0; R < 4; ++R) {
+    for (int u = 0; u < NU; ++u) {
       __builtin_amdgcn_sched_barrier(0);  // one round's addresses at a time
 #pragma unroll
-      for (int e = 4 * R; e < 4 * R + 4; ++e) {
-        const int rr = 4 * h + (e & 3);  // row inside the round
-        const float sc = scl[e];
-#pragma unroll
-        for (int u = 0; u < NU; ++u) ost[rr * ROWO + 32 * u + c] = from_float<T>(acc[u][e] * sc).x;
+      for (int g = 0; g < 4; ++g) {
+        const u32x2 w = {pack2<T>(acc[u][4 * g] * rl, acc[u][4 * g + 1] * rl),
+                         pack2<T>(acc[u][4 * g + 2] * rl, acc[u][4 * g + 3] * rl)};
+        *reinterpret_cast<u32x2*>(ost + c * 64 + 16 * (g ^ wsw) + 8 * h) = w;
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 #pragma unroll
-      for (int i = 0; i < 8 * CPR / 64; ++i) {
-        const int chunk = lane + 64 * i;
-        const int r = chunk / CPR, ch = chunk % CPR;
-        const int row = it.q0 + 8 * R + r;
-        const u32x4 w = *reinterpret_cast<const u32x4*>(ost + r * ROWO + 8 * ch);
-        if (row < it.q_len) *reinterpret_cast<u32x4*>(obase + row * a.o_st + 8 * ch) = w;
+      for (int i = 0; i < 2; ++i) {
+        const int id = lane + 64 * i, r = id >> 2, q = id & 3;
+        const int row = it.q0 + r;
+        const u32x4 w = *reinterpret_cast<const u32x4*>(ost + r * 64 + 16 * (q ^ ((r >> 2) & 3)));
+        if (row < it.q_len) *reinterpret_cast<u32x4*>(obase + row * a.o_st + 32 * u + 8 * q) = w;
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
