@@ -350,6 +350,7 @@ def bench_prefill(name, steps, warmup):
         flash_attn_varlen_func(q_rot, k_rot, w.v, w.cu_seqlens, w.cu_seqlens, w.max_seqlen, w.max_seqlen, True, out=out)
 
     us = time_region(attn, steps, warmup)[0] * 1e3
+    spread = _spread(time_each(attn, max(20, min(steps, 200)), warmup + steps))
     flops = W.prefill_flops(w.seq_lens, hq)
 
     def norm_store(i):
@@ -357,6 +358,7 @@ def bench_prefill(name, steps, warmup):
                            w.block_tables, w.cu_seqlens)
 
     ns_us = time_region(norm_store, steps, warmup)[0] * 1e3
+    ns_spread = _spread(time_each(norm_store, max(20, min(steps, 200)), warmup + steps))
     ns_bytes = norm_store_bytes(T, hq, hkv)
 
     # The standalone K/V store, as the reference's prefill calls it: the new
@@ -389,11 +391,14 @@ def bench_prefill(name, steps, warmup):
     block_us = time_region(block, steps, warmup)[0] * 1e3
     return {
         "workload": name, "tokens": T, "gflop": flops / 1e9,
-        "us_per_call": us, "tflops": flops / (us * 1e-6) / 1e12,
+        "us_per_call": us, "us_per_call_median": spread["median"], "us_per_call_p10": spread["p10"],
+        "us_per_call_p90": spread["p90"], "tflops": flops / (us * 1e-6) / 1e12,
         "pct_peak_mfma": 100.0 * flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
         "tokens_per_s": T / (us * 1e-6),
         "roofline": {**_roof_mfma(flops, us), "kernel": "varlen_prefill_gqa"},
-        "norm_rope_store_us": ns_us, "norm_rope_store_gbs": ns_bytes / (ns_us * 1e-6) / 1e9,
+        "norm_rope_store_us": ns_us, "norm_rope_store_us_median": ns_spread["median"],
+        "norm_rope_store_us_p10": ns_spread["p10"], "norm_rope_store_us_p90": ns_spread["p90"],
+        "norm_rope_store_gbs": ns_bytes / (ns_us * 1e-6) / 1e9,
         "norm_rope_store_roofline": _roof_hbm(ns_bytes, ns_us),
         "kv_store_mapped_us": kvm_us, "kv_store_mapped_roofline": _roof_hbm(kv_bytes, kvm_us),
         "kv_store_paged_us": kvp_us, "kv_store_paged_roofline": _roof_hbm(kv_bytes, kvp_us),
