@@ -543,11 +543,14 @@ def bench_mixed(name, steps, warmup, copies=3):
     }, m
 
 
-def bench_sampling(steps, warmup, batch=64, vocab=151936):
+def bench_sampling(steps, warmup, batch=64, vocab=151936, copies=16):
     """sample_tokens over a Qwen3-vocab batch: bf16 logits (N(0, 2.5) plus a
-    few boosted tokens per row), temperature 0.8, seeded uniforms; three
-    filter settings. One launch per call, timed eagerly and replayed from a
-    captured graph."""
+    few boosted tokens per row), seeded uniforms; four filter settings, the
+    last the reference server's default request (temperature 1.0, top_p
+    0.95, top_k 0: server/api/schema.py:11-15). The calls rotate over
+    `copies` copies of the logits (16 x 19.4 MB, past the 256 MB MALL), so
+    each call reads its row from HBM. One launch per call, timed eagerly and
+    replayed from a captured graph."""
     from tinyserver_amd.kernels import sample_tokens
 
     dev = torch.device("cuda:0")
@@ -555,6 +558,7 @@ def bench_sampling(steps, warmup, batch=64, vocab=151936):
     logits = torch.randn(batch, vocab, generator=g) * 2.5
     logits.scatter_add_(1, torch.randint(0, vocab, (batch, 8), generator=g), torch.rand(batch, 8, generator=g) * 12)
     logits = logits.to(dev, torch.bfloat16)
+    pool = [logits] + [logits.clone() for _ in range(copies - 1)]
     temperature = torch.full((batch,), 0.8, device=dev)
     top_k = torch.full((batch,), 50, dtype=torch.int64, device=dev)
     top_p = torch.full((batch,), 0.9, device=dev)
@@ -562,24 +566,28 @@ def bench_sampling(steps, warmup, batch=64, vocab=151936):
     out = torch.empty(batch, dtype=torch.int64, device=dev)
     cases = {}
     nbytes = batch * vocab * 2
-    for label, k, pp in (("topk50_topp0.9", 50, 0.9), ("topp0.9", 0, 0.9), ("full", 0, 1.0)):
+    for label, temp, k, pp in (("topk50_topp0.9", 0.8, 50, 0.9), ("topp0.9", 0.8, 0, 0.9), ("full", 0.8, 0, 1.0),
+                               ("server_default_t1_topp0.95", 1.0, 0, 0.95)):
+        temperature.fill_(temp)
         top_k.fill_(k)
         top_p.fill_(pp)
 
         def call(i):
-            sample_tokens(logits, temperature, top_k, top_p, uniforms, out=out)
+            sample_tokens(pool[i % copies], temperature, top_k, top_p, uniforms, out=out)
 
         us = time_region(call, steps, warmup)[0] * 1e3
-        gus = _graph_us_per_call(lambda i: sample_tokens(logits, temperature, top_k, top_p, uniforms, out=out),
-                                 steps, warmup)
-        cases[label] = {"us_per_call": us, "graph_us_per_call": gus, "logits_gbs": nbytes / (gus * 1e-6) / 1e9,
+        gus = _graph_us_per_call(call, steps, warmup)
+        cases[label] = {"temperature": temp, "top_k": k, "top_p": pp, "us_per_call": us, "graph_us_per_call": gus,
+                        "logits_gbs": nbytes / (gus * 1e-6) / 1e9,
                         "roofline": {**_roof_hbm(nbytes, gus), "kernel": "sample_tokens_kernel",
-                                     "note": "per call in a captured graph of 20 calls (the eager "
-                                             "us_per_call also holds the Python enqueue)"}}
+                                     "note": f"per call in a captured graph of 20 calls over {copies} logits "
+                                             "copies (the eager us_per_call also holds the Python enqueue)"}}
+    temperature.fill_(0.8)
     top_k.fill_(50)
     top_p.fill_(0.9)
-    return {"workload": f"sample_tokens bs{batch} vocab{vocab} bf16", "batch": batch, "vocab": vocab, **cases}, \
-        (logits, temperature, top_k, top_p, uniforms)
+    del pool
+    return {"workload": f"sample_tokens bs{batch} vocab{vocab} bf16", "batch": batch, "vocab": vocab,
+            "logits_copies": copies, **cases}, (logits, temperature, top_k, top_p, uniforms)
 
 
 def _graph_us_per_call(fn, steps, warmup, calls=20):
@@ -649,8 +657,51 @@ def _free():
     torch.cuda.empty_cache()
 
 
-def _progress(name):
-    print(f"bench: {name} done", file=sys.stderr, flush=True)
+def _fmt_cpu(cpu):
+    """The CPU baselines of a result, as 'cpu(literal) 1.2e+06 us' pieces."""
+    if not isinstance(cpu, dict):
+        return ""
+    parts = []
+    for variant in ("literal", "vectorized"):
+        c = cpu.get(variant)
+        if isinstance(c, dict) and ("us_per_layer" in c or "us_per_call" in c):
+            parts.append(f"cpu({variant}) {c.get('us_per_layer', c.get('us_per_call')):.0f} us")
+    if "us_per_call" in cpu:
+        parts.append(f"cpu {cpu['us_per_call']:.0f} us")
+    return " ".join(parts)
+
+
+def _summary(name, s):
+    """One short line per workload: time per call, roofline fraction, CPU
+    baseline time (the whole result is in the JSON line)."""
+    bits = [name]
+    if "roofline" in s and "us_per_call" in s:  # decode or prefill
+        r = s["roofline"]
+        bits.append(f"{s['us_per_call']:.1f} us {r['bound']} {r['frac']:.3f}")
+        if "graph_us_per_call" in s:
+            bits.append(f"graph {s['graph_us_per_call']:.1f} us")
+        if "block_graph_us_per_call" in s:
+            bits.append(f"block graph {s['block_graph_us_per_call']:.1f} us eager {s['block_us_per_call']:.1f} us")
+        if "norm_rope_store_roofline" in s:
+            bits.append(f"norm/rope/store {s['norm_rope_store_us']:.1f} us "
+                        f"hbm {s['norm_rope_store_roofline']['frac']:.3f}")
+    if "step_graph_us" in s:  # mixed step
+        bits.append(f"step graph {s['step_graph_us']:.1f} us, one-store form {s['one_launch']['step_graph_us']:.1f} us")
+        for k, v in s["launches"].items():
+            bits.append(f"{k} {v['us']:.1f} us {v['roofline']['bound']} {v['roofline']['frac']:.3f}")
+    for k, v in s.items():  # sampling cases
+        if isinstance(v, dict) and "graph_us_per_call" in v and "roofline" in v:
+            bits.append(f"{k} graph {v['graph_us_per_call']:.1f} us hbm {v['roofline']['frac']:.3f}")
+    cpu = s.get("cpu_baseline")
+    if isinstance(cpu, dict) and ("prefill" in cpu or "decode" in cpu):
+        bits += [f"{half}: {_fmt_cpu(cpu[half])}" for half in ("prefill", "decode") if half in cpu]
+    elif cpu:
+        bits.append(_fmt_cpu(cpu))
+    return " | ".join(b for b in bits if b)
+
+
+def _progress(name, s):
+    print(f"bench: {_summary(name, s)}", file=sys.stderr, flush=True)
 
 
 def secondaries(steps, warmup, cpu, cpu_s):
@@ -664,7 +715,7 @@ def secondaries(steps, warmup, cpu, cpu_s):
         s["cpu_baseline"] = {"literal": cpu_decode_baseline(w, True, cpu_s),
                              "vectorized": cpu_decode_baseline(w, False, cpu_s)}
     sec["qwen3-0.6b-decode-bs4"] = _round(s)
-    _progress("qwen3-0.6b-decode-bs4")
+    _progress("qwen3-0.6b-decode-bs4", sec["qwen3-0.6b-decode-bs4"])
     del w
     _free()
     # 32k-context decode (one pool copy: 4.3 GB, far past the MALL)
@@ -673,7 +724,7 @@ def secondaries(steps, warmup, cpu, cpu_s):
         s["cpu_baseline"] = {"literal": cpu_decode_baseline(w, True, cpu_s),
                              "vectorized": cpu_decode_baseline(w, False, cpu_s)}
     sec["qwen3-32b-decode-bs32"] = _round(s)
-    _progress("qwen3-32b-decode-bs32")
+    _progress("qwen3-32b-decode-bs32", sec["qwen3-32b-decode-bs32"])
     del w
     _free()
     # varlen prefill
@@ -684,7 +735,7 @@ def secondaries(steps, warmup, cpu, cpu_s):
                                    "(606 MB in bf16) and its SDPA scores every pair: not a bounded sample"},
             "vectorized": cpu_prefill_baseline(w, False, cpu_s)}
     sec["qwen3-8b-prefill-16seq"] = _round(s)
-    _progress("qwen3-8b-prefill-16seq")
+    _progress("qwen3-8b-prefill-16seq", sec["qwen3-8b-prefill-16seq"])
     del w
     _free()
     # the continuous-batching step on one shared pool
@@ -696,18 +747,18 @@ def secondaries(steps, warmup, cpu, cpu_s):
             "decode": {"literal": cpu_decode_baseline(m.decode, True, cpu_s),
                        "vectorized": cpu_decode_baseline(m.decode, False, cpu_s)}}
     sec["qwen3-4b-mixed"] = _round(s)
-    _progress("qwen3-4b-mixed")
+    _progress("qwen3-4b-mixed", sec["qwen3-4b-mixed"])
     del m
     _free()
     s, m = bench_mixed("qwen3-4b-mixed-chunk", steps, min(warmup, 3))
     sec["qwen3-4b-mixed-chunk"] = _round(s)
-    _progress("qwen3-4b-mixed-chunk")
+    _progress("qwen3-4b-mixed-chunk", sec["qwen3-4b-mixed-chunk"])
     del m
     _free()
     # the headline batch on the server's default 256-token pages
     s, w = bench_decode(HEADLINE, steps, min(warmup, 3), with_block=True, page=256)
     sec["qwen3-8b-decode-bs64-page256"] = _round(s)
-    _progress("qwen3-8b-decode-bs64-page256")
+    _progress("qwen3-8b-decode-bs64-page256", sec["qwen3-8b-decode-bs64-page256"])
     del w
     _free()
     # batched sampling
@@ -715,7 +766,7 @@ def secondaries(steps, warmup, cpu, cpu_s):
     if cpu:
         s["cpu_baseline"] = cpu_sampling_baseline(*args, cpu_s)
     sec["sampling-qwen3-vocab-bs64"] = _round(s)
-    _progress("sampling-qwen3-vocab-bs64")
+    _progress("sampling-qwen3-vocab-bs64", sec["sampling-qwen3-vocab-bs64"])
     return sec
 
 
@@ -817,6 +868,12 @@ def main():
     if not args.no_cpu_baseline:
         lit = cpu_decode_baseline(w, True, 10.0)
         line["cpu_baseline"] = {**lit, "vectorized": cpu_decode_baseline(w, False, 5.0)}
+    print(f"bench: {HEADLINE} (headline) {line['us_per_layer']:.1f} us hbm {line['roofline']['frac']:.3f} | wall "
+          f"{line['ms_per_step'] * 1e3:.1f} us/step | graph {head['graph_us_per_call']:.1f} us | block graph "
+          f"{head['block_graph_us_per_call']:.1f} us eager {head['block_us_per_call']:.1f} us"
+          + (f" | cpu(literal) {line['cpu_baseline']['us_per_layer']:.0f} us cpu(vectorized) "
+             f"{line['cpu_baseline']['vectorized']['us_per_layer']:.0f} us" if "cpu_baseline" in line else ""),
+          file=sys.stderr, flush=True)
     del w
     _free()
     if not args.no_secondary:

@@ -160,9 +160,12 @@ int tsa_paged_decode(const tsa_view* out, const tsa_view* query, const tsa_view*
  * harnesses that forbid hipMalloc). It has no counterpart in the reference.
  * Same arguments, kernels and results as tsa_paged_decode; the partials and
  * tile prefix live in a 16 MiB array the library holds on each GPU it runs on
- * until the process ends, so it allocates nothing. A call whose workspace
- * (tsa_paged_decode_workspace_bytes) would exceed 16 MiB is rejected with
- * TSA_ERR_INVALID before any device work. All calls on one GPU share that
+ * until the process ends, so it allocates nothing. Every argument is checked
+ * before any device work. A call served by the MFMA stream kernel whose
+ * workspace (tsa_paged_decode_workspace_bytes) would exceed 16 MiB is then
+ * rejected with TSA_ERR_INVALID; calls served by the generic kernel (fp32,
+ * other head_dims, more than 16 q-heads per kv head, strided rows) take no
+ * scratch and are accepted as tsa_paged_decode accepts them. All calls on one GPU share that
  * GPU's array: calls ordered on one stream are fine; calls that overlap on
  * one GPU (concurrent streams, threads) race and must not be issued. */
 int tsa_paged_decode_noalloc(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache,

@@ -121,6 +121,35 @@ def test_noalloc_rejects_oversized_before_device_work():
     assert str(need) in msg
 
 
+def test_noalloc_checks_arguments_first():
+    """tsa_paged_decode_noalloc runs every argument check before it looks up
+    its scratch (no device is touched): a malformed call gets the same
+    message tsa_paged_decode gives."""
+    q, kc = _v((4, 8, 128)), _v((10, 2, 16, 128))
+    bt, sl = _v((4, 2), torch.int32), _v((4,), torch.int32)
+    bad = _v((4, 7, 128))
+    rc, msg = _call("tsa_paged_decode_noalloc", R(bad), R(bad), R(kc), R(kc), R(bt), R(sl), 0.1, 0, None)
+    assert rc == _lib.TSA_ERR_INVALID and "multiple" in msg
+    rc, msg = _call("tsa_paged_decode_noalloc", R(q), R(q), R(kc), R(kc), R(_v((3, 2), torch.int32)), R(sl), 0.1,
+                    0, None)
+    assert rc == _lib.TSA_ERR_INVALID and "num_seqs" in msg
+
+
+def test_mixed_attention_shim_rank_checks():
+    """The Python shim checks the cache and table ranks before it sizes the
+    workspace: wrong ranks raise ValueError, as paged_attention_forward's do."""
+    from tinyserver_amd.kernels import mixed_attention
+
+    pq, pk = torch.zeros(10, 8, 128), torch.zeros(10, 2, 128)
+    cu = torch.tensor([0, 4, 10], dtype=torch.int32)
+    q, kc = torch.zeros(4, 8, 128), torch.zeros(10, 2, 16, 128)
+    bt, sl = torch.zeros(4, 2, dtype=torch.int32), torch.ones(4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="4D"):
+        mixed_attention(pq, pk, pk, cu, 6, q, kc[0], kc[0], bt, sl)
+    with pytest.raises(ValueError, match="2D"):
+        mixed_attention(pq, pk, pk, cu, 6, q, kc, kc, bt[0], sl)
+
+
 def test_prefill_validation():
     q, k = _v((10, 6, 64)), _v((10, 4, 64))
     cu = _v((3,), torch.int32)

@@ -231,6 +231,19 @@ def test_many_sequences():
     assert_close(out, ref, what="1000 sequences")
 
 
+@pytest.mark.parametrize("batch", [4095, 4096, 12000])
+def test_any_batch_size(batch):
+    """Batches on both sides of the per-wave LDS tile-prefix limit (4095
+    sequences); larger ones read the prefix from the workspace. 1-40 tokens
+    per sequence, GQA 2, against the oracle."""
+    g = torch.Generator().manual_seed(47 + batch)
+    lens = torch.randint(1, 41, (batch,), generator=g).tolist()
+    q, kc, vc, bt, sl = _random_paged_inputs(lens, 4, 2, 128, 16, torch.bfloat16, seed=48)
+    out = _run(q, kc, vc, bt, 16, sl).cpu()
+    ref = op.paged_attention_forward(q, kc, vc, bt, 16, sl)
+    assert_close(out, ref, what=f"{batch} sequences")
+
+
 @pytest.mark.parametrize("name", ["qwen3-0.6b-decode-bs4", "qwen3-8b-decode-bs64"])
 def test_fused_decode_step(name):
     """paged_decode_step (norm/RoPE + store + attention, fused) against the

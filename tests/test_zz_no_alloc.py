@@ -2,8 +2,9 @@
 through the C ABI, against tsa_paged_decode with a caller workspace: the
 same kernels on the same inputs give bit-identical outputs. Two calls in a
 row, the second with a smaller batch (the scratch keeps the first call's
-contents, which the second must not see), then the first shape again; plus
-a call that needs more scratch than the library holds, rejected before any
+contents, which the second must not see), then the first shape again; calls
+the generic kernel serves (fp32, head_dim 96), which take no scratch; plus a
+call that needs more scratch than the library holds, rejected before any
 device work.
 """
 
@@ -67,3 +68,20 @@ def test_noalloc_rejects_oversized_calls():
     sl = torch.ones(8192, dtype=torch.int32, device=DEV)
     with pytest.raises(ValueError, match="bytes of scratch"):
         _noalloc(q, kc, kc, bt, sl)
+
+
+def test_noalloc_generic_kernel_calls():
+    """Calls the generic kernel serves need no scratch: fp32 and head_dim 96
+    are accepted and equal the workspace entry point, bit for bit."""
+    f32 = tuple(t.float() if t.is_floating_point() else t for t in _case("qwen3-0.6b-decode-bs4"))
+    g = torch.Generator(device="cpu").manual_seed(5)
+    q96 = torch.randn(3, 8, 96, generator=g).to(torch.bfloat16).to(DEV)
+    kc96 = torch.randn(12, 2, 16, 96, generator=g).to(torch.bfloat16).to(DEV)
+    vc96 = torch.randn(12, 2, 16, 96, generator=g).to(torch.bfloat16).to(DEV)
+    bt96 = torch.randperm(12, generator=g)[:12].reshape(3, 4).to(torch.int32).to(DEV)
+    sl96 = torch.tensor([1, 40, 64], dtype=torch.int32, device=DEV)
+    for args in (f32, (q96, kc96, vc96, bt96, sl96), f32):
+        got = _noalloc(*args)
+        ref = paged_attention_forward(*args[:4], 16, args[4])
+        torch.cuda.synchronize()
+        assert_bitexact(got, ref, f"noalloc generic kernel, {args[0].dtype}, head_dim {args[0].shape[-1]}")

@@ -284,11 +284,15 @@ struct TileCursor {
 // loads.
 // decode_stream_body runs workgroup blockIdx.x of that grid (the first
 // workgroups of the launch); lds_i is the workgroup's LDS: kWaves tile prefixes of B + 1 ints, then (fused step)
-// kWaves areas of kFusedWaveBytes at the next 16-byte boundary.
-template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED>
+// kWaves areas of kFusedWaveBytes at the next 16-byte boundary. With GPREF
+// (batches whose prefixes would not fit in LDS) the waves read the tile
+// prefix that decode_tile_prefix wrote to the workspace instead, and the
+// workgroup takes no LDS.
+template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED, bool GPREF = false>
 __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* __restrict__ bt,
                                                    const int32_t* __restrict__ sl, float* __restrict__ part,
                                                    int* lds_i) {
+  static_assert(!(GPREF && FUSED), "the fused step keeps its tile prefixes in LDS");
   constexpr int KJ = D / 32;  // k-steps of the score MFMA
   a.bt = bt;
   a.seq_lens = sl;
@@ -298,10 +302,16 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
   // Wave-uniform (scalar) so tile indices, block-table reads and page bases
   // stay in SGPRs and the table lookups are scalar loads.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  int* pref = lds_i + wave * (a.B + 1);  // this wave's copy, [B + 1]
-  tile_prefix_wave(a, pref);
-  if (blockIdx.x == 0 && wave == 0)
-    for (int i = lane; i <= a.B; i += 64) a.pref_out[i] = pref[i];
+  const int* pref;
+  if constexpr (GPREF) {
+    pref = a.pref_out;  // [B + 1], written by decode_tile_prefix before this launch
+  } else {
+    int* const mine = lds_i + wave * (a.B + 1);  // this wave's copy, [B + 1]
+    tile_prefix_wave(a, mine);
+    if (blockIdx.x == 0 && wave == 0)
+      for (int i = lane; i <= a.B; i += 64) a.pref_out[i] = mine[i];
+    pref = mine;
+  }
 
   // Fused step: this wave's LDS area (weights, then the unit ring). Data
   // arrives by LDS DMA (global_load_lds_dwordx4: lane l's 16 bytes land at
@@ -338,10 +348,25 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
   // empty sequences), then the kv head and the tile inside it.
   TileCursor cur;
   {
-    int l0 = 0, h0 = a.B;  // answer in [l0, h0)
-    while (h0 - l0 > 1) {
-      const int mid = (l0 + h0) >> 1;
-      if (static_cast<int64_t>(Hkv) * pref[mid] <= lo) l0 = mid; else h0 = mid;
+    int l0 = 0, h0 = a.B;  // answer in [l0, h0): Hkv pref[l0] <= lo < Hkv pref[h0]
+    if constexpr (GPREF) {
+      // The prefix is in global memory: each step probes 64 evenly spaced
+      // entries at once (one load per lane) and keeps the interval between
+      // the last probe <= lo and the next, so a batch of B sequences takes
+      // about log64(B) dependent loads instead of log2(B).
+      while (h0 - l0 > 1) {
+        const int step = (h0 - l0 + 63) / 64;
+        const int idx = l0 + lane * step;
+        const bool le = idx < h0 && static_cast<int64_t>(Hkv) * pref[idx] <= lo;
+        const int cnt = __builtin_popcountll(__ballot(le));  // >= 1: the probe at l0
+        l0 = __builtin_amdgcn_readfirstlane(l0 + (cnt - 1) * step);
+        h0 = min(h0, l0 + step);
+      }
+    } else {
+      while (h0 - l0 > 1) {
+        const int mid = (l0 + h0) >> 1;
+        if (static_cast<int64_t>(Hkv) * pref[mid] <= lo) l0 = mid; else h0 = mid;
+      }
     }
     cur.s = __builtin_amdgcn_readfirstlane(l0);
     cur.n = __builtin_amdgcn_readfirstlane(pref[cur.s + 1] - pref[cur.s]);
@@ -649,12 +674,40 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
   else stream(std::false_type{});
 }
 
-template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED>
+template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED, bool GPREF>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TSA_DECODE_WAVES_PER_EU)))
 void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ sl,
                          float* __restrict__ part) {
   extern __shared__ int lds_i[];
-  decode_stream_body<T, D, PAGE16, CONTIG, FUSED>(a, bt, sl, part, lds_i);
+  decode_stream_body<T, D, PAGE16, CONTIG, FUSED, GPREF>(a, bt, sl, part, lds_i);
+}
+
+// The exclusive tile prefix over the sequences (pref_out[0..B], pref_out[B]
+// = total) for batches whose per-wave LDS copies would not fit: one
+// workgroup, thread t summing a contiguous run of ceil(B / 1024) sequences,
+// a scan of the 1024 run totals in LDS, then each run written out.
+constexpr int kPrefixThreads = 1024;
+__global__ __launch_bounds__(kPrefixThreads) void decode_tile_prefix(DecodeArgs a) {
+  __shared__ int tot[kPrefixThreads];
+  const int t = threadIdx.x;
+  const int per = (a.B + kPrefixThreads - 1) / kPrefixThreads;
+  const int s0 = min(a.B, t * per), s1 = min(a.B, s0 + per);
+  int local = 0;
+  for (int s = s0; s < s1; ++s) local += tiles_of(a, s);
+  tot[t] = local;
+  __syncthreads();
+  for (int off = 1; off < kPrefixThreads; off <<= 1) {  // inclusive Hillis-Steele scan
+    const int add = t >= off ? tot[t - off] : 0;
+    __syncthreads();
+    tot[t] += add;
+    __syncthreads();
+  }
+  int run = tot[t] - local;
+  for (int s = s0; s < s1; ++s) {
+    a.pref_out[s] = run;
+    run += tiles_of(a, s);
+  }
+  if (t == kPrefixThreads - 1) a.pref_out[a.B] = tot[t];
 }
 
 // out[s, kvh * G + hd] = sum_v 2^(m_v - M) acc_v / sum_v 2^(m_v - M) l_v over
@@ -838,6 +891,11 @@ static int launch_merge(const DecodeArgs& a, hipStream_t stream) {
   return check_launch("tsa_paged_decode");
 }
 
+// The stream kernel keeps kWaves copies of the tile prefix (B + 1 ints
+// each) in LDS up to this batch; larger batches read one copy from the
+// workspace (decode_tile_prefix).
+static bool prefix_in_lds(int64_t B) { return static_cast<int64_t>(kWaves) * (B + 1) * 4 <= 64 * 1024; }
+
 // LDS bytes of the fused stream kernel: kWaves tile prefixes, then the
 // per-wave fused areas at the next 16-byte boundary.
 static size_t fused_lds_bytes(int64_t B) {
@@ -853,16 +911,28 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream, bool fuse
     return check_launch("tsa_paged_decode");
   }
   if constexpr (sizeof(T) == 2) {
-    const size_t lds = static_cast<size_t>(kWaves) * (a.B + 1) * sizeof(int);
+    const bool gpref = !prefix_in_lds(a.B);
+    const size_t lds = gpref ? 0 : static_cast<size_t>(kWaves) * (a.B + 1) * sizeof(int);
     const bool page16 = a.BS % 16 == 0;
     const bool contig = a.kc_s == a.D && a.vc_s == a.D;
     const dim3 grid(a.W);
-#define TSA_DECODE_LAUNCH(DD, P16, CT) \
-  paged_decode_stream<T, DD, P16, CT, false><<<grid, dim3(kThreads), lds, stream>>>(a, a.bt, a.seq_lens, a.part)
-    if (fused) {  // checked by the caller: head_dim 128, 16-token pages, contiguous rows
+    if (gpref) {
+      decode_tile_prefix<<<dim3(1), dim3(kPrefixThreads), 0, stream>>>(a);
+      if (int rc = check_launch("tsa_paged_decode")) return rc;
+    }
+#define TSA_DECODE_LAUNCH(DD, P16, CT)                                                                              \
+  do {                                                                                                              \
+    if (gpref)                                                                                                      \
+      paged_decode_stream<T, DD, P16, CT, false, true><<<grid, dim3(kThreads), 0, stream>>>(a, a.bt, a.seq_lens,  \
+                                                                                              a.part);              \
+    else                                                                                                            \
+      paged_decode_stream<T, DD, P16, CT, false, false><<<grid, dim3(kThreads), lds, stream>>>(a, a.bt, a.seq_lens, \
+                                                                                                 a.part);           \
+  } while (0)
+    if (fused) {  // checked by the caller: head_dim 128, 16-token pages, contiguous rows, prefixes in LDS
       const size_t lds_f = fused_lds_bytes(a.B);
-      paged_decode_stream<T, 128, true, true, true><<<grid, dim3(kThreads), lds_f, stream>>>(a, a.bt, a.seq_lens,
-                                                                                           a.part);
+      paged_decode_stream<T, 128, true, true, true, false><<<grid, dim3(kThreads), lds_f, stream>>>(
+          a, a.bt, a.seq_lens, a.part);
     } else if (a.D == 128) {
       if (page16 && contig) TSA_DECODE_LAUNCH(128, true, true);
       else if (page16) TSA_DECODE_LAUNCH(128, true, false);
@@ -893,12 +963,12 @@ extern "C" size_t tsa_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num
 }
 
 namespace tsa {
-// Checks shared by both decode entry points; fills a (and mfma: whether the
-// stream kernel serves the call).
-static int prepare_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache, const tsa_view* v_cache,
-                          const tsa_view* block_tables, const tsa_view* seq_lens, double softmax_scale, void* workspace,
-                          size_t workspace_bytes, int32_t num_workgroups, DecodeArgs& a, bool& mfma,
-                          const char* workspace_name = "workspace") {
+// Checks shared by the decode entry points; fills a (and mfma: whether the
+// stream kernel serves the call, plan: its grid and workspace layout). No
+// device work and no workspace yet.
+static int check_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache, const tsa_view* v_cache,
+                        const tsa_view* block_tables, const tsa_view* seq_lens, double softmax_scale,
+                        int32_t num_workgroups, DecodeArgs& a, bool& mfma, DecodePlan& plan) {
   TSA_REQUIRE(view_ok(query, 3), "query must be a 3D tensor (num_seqs, num_heads, head_dim)");
   TSA_REQUIRE(view_ok(out, 3), "out must be a 3D tensor shaped like query");
   TSA_REQUIRE(view_ok(k_cache, 4) && view_ok(v_cache, 4),
@@ -942,22 +1012,40 @@ static int prepare_decode(const tsa_view* out, const tsa_view* query, const tsa_
   a.max_blocks = static_cast<int32_t>(block_tables->size[1]); a.D = static_cast<int32_t>(D);
   a.scale_log2 = static_cast<float>(softmax_scale * 1.4426950408889634);
 
-  // The MFMA path keeps a per-wave tile prefix of B + 1 ints in LDS.
-  mfma = (dt == TSA_BF16 || dt == TSA_F16) && (D == 64 || D == 128) && a.G <= 16 &&
-                    static_cast<int64_t>(kWaves) * (B + 1) * 4 <= 64 * 1024 &&
-                    rows_vec16(query) && rows_vec16(k_cache) && rows_vec16(v_cache) && out->stride[2] == 1;
+  mfma = (dt == TSA_BF16 || dt == TSA_F16) && (D == 64 || D == 128) && a.G <= 16 && rows_vec16(query) &&
+         rows_vec16(k_cache) && rows_vec16(v_cache) && out->stride[2] == 1;
+  plan = DecodePlan{};
   if (mfma) {
-    const DecodePlan plan = make_plan(B, Hq, Hkv, D, num_workgroups);
+    plan = make_plan(B, Hq, Hkv, D, num_workgroups);
     a.W = plan.W;
     a.NW = kWaves * plan.W;
-    TSA_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total,
-                "%s of %zu bytes is too small: %zu needed", workspace_name, workspace_bytes, plan.total);
-    TSA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "%s must be 256-byte aligned", workspace_name);
-    char* ws = static_cast<char*>(workspace);
-    a.part = reinterpret_cast<float*>(ws);
-    a.pref_out = reinterpret_cast<int32_t*>(ws + plan.part_bytes);
   }
   return TSA_OK;
+}
+
+// The stream kernel's partials and tile prefix in the workspace (only the
+// stream path takes one).
+static int bind_workspace(DecodeArgs& a, bool mfma, const DecodePlan& plan, void* workspace, size_t workspace_bytes,
+                          const char* workspace_name) {
+  if (!mfma) return TSA_OK;
+  TSA_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total, "%s of %zu bytes is too small: %zu needed",
+              workspace_name, workspace_bytes, plan.total);
+  TSA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "%s must be 256-byte aligned", workspace_name);
+  char* ws = static_cast<char*>(workspace);
+  a.part = reinterpret_cast<float*>(ws);
+  a.pref_out = reinterpret_cast<int32_t*>(ws + plan.part_bytes);
+  return TSA_OK;
+}
+
+// check_decode, then the caller's workspace.
+static int prepare_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache, const tsa_view* v_cache,
+                          const tsa_view* block_tables, const tsa_view* seq_lens, double softmax_scale, void* workspace,
+                          size_t workspace_bytes, int32_t num_workgroups, DecodeArgs& a, bool& mfma) {
+  DecodePlan plan;
+  if (int rc = check_decode(out, query, k_cache, v_cache, block_tables, seq_lens, softmax_scale, num_workgroups, a,
+                            mfma, plan))
+    return rc;
+  return bind_workspace(a, mfma, plan, workspace, workspace_bytes, "workspace");
 }
 }  // namespace tsa
 
@@ -1127,6 +1215,7 @@ extern "C" int tsa_mixed_attention(const tsa_view* prefill_out, const tsa_view* 
   const bool small = pa.total_q <= kMixedAutoMaxTokens &&
                      int64_t{a.B} * a.max_blocks * a.BS <= kMixedAutoMaxDecodeTokens;
   const bool one = dmfma && a.D == 128 && a.BS % 16 == 0 && a.kc_s == a.D && a.vc_s == a.D && a.B > 0 &&
+                   prefix_in_lds(a.B) &&
                    pa.nseq > 0 && pa.Hq > 0 && pa.total_q > 0 && prefill_q->dtype == dt &&
                    prefill_takes_gqa4(pa, pmfma) && (prefill_workgroups > 0 || small);
   if (!one) {
@@ -1217,25 +1306,25 @@ extern "C" int tsa_paged_decode_noalloc(const tsa_view* out, const tsa_view* que
                                         const tsa_view* v_cache, const tsa_view* block_tables,
                                         const tsa_view* seq_lens, double softmax_scale, int32_t num_workgroups,
                                         void* stream) {
-  // The size limit first, before any device work: the scratch a call needs
-  // is the workspace tsa_paged_decode would take.
-  if (view_ok(query, 3) && view_ok(k_cache, 4) && k_cache->size[1] > 0 && query->size[1] % k_cache->size[1] == 0 &&
-      num_workgroups >= 0 && query->size[0] > 0 && query->size[1] > 0) {
-    const size_t need =
-        make_plan(query->size[0], query->size[1], k_cache->size[1], query->size[2], num_workgroups).total;
-    TSA_REQUIRE(need <= kNoAllocScratchBytes,
-                "tsa_paged_decode_noalloc: this call needs %zu bytes of scratch, beyond the %zu bytes the library "
-                "holds per GPU; use tsa_paged_decode with a caller workspace",
-                need, kNoAllocScratchBytes);
-  }
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  void* ws = nullptr;
-  if (int rc = noalloc_scratch(st, &ws)) return rc;
+  // Every argument check first, before any device work; the scratch limit
+  // and the device's scratch address only where the stream kernel takes a
+  // workspace (the generic kernel needs none).
   DecodeArgs a;
   bool mfma = false;
-  if (int rc = prepare_decode(out, query, k_cache, v_cache, block_tables, seq_lens, softmax_scale, ws,
-                              kNoAllocScratchBytes, num_workgroups, a, mfma, "the no-allocation scratch"))
+  DecodePlan plan;
+  if (int rc = check_decode(out, query, k_cache, v_cache, block_tables, seq_lens, softmax_scale, num_workgroups, a,
+                            mfma, plan))
     return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (mfma) {
+    TSA_REQUIRE(plan.total <= kNoAllocScratchBytes,
+                "tsa_paged_decode_noalloc: this call needs %zu bytes of scratch, beyond the %zu bytes the library "
+                "holds per GPU; use tsa_paged_decode with a caller workspace",
+                plan.total, kNoAllocScratchBytes);
+    void* ws = nullptr;
+    if (int rc = noalloc_scratch(st, &ws)) return rc;
+    if (int rc = bind_workspace(a, mfma, plan, ws, kNoAllocScratchBytes, "the no-allocation scratch")) return rc;
+  }
   switch (query->dtype) {
     case TSA_BF16: return launch_decode<bf16_t>(a, mfma, st);
     case TSA_F16: return launch_decode<f16_t>(a, mfma, st);

@@ -61,6 +61,12 @@ def mixed_attention(
         raise ValueError("num_heads_q must be divisible by num_heads_k for GQA")
     if query.dim() != 3:
         raise ValueError("query must be 3D tensor (num_seqs, num_heads, head_dim)")
+    if k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise ValueError("k_cache and v_cache must be 4D tensors (num_blocks, num_kv_heads, block_size, head_dim)")
+    if block_tables.dim() != 2:
+        raise ValueError(f"block_tables must be a 2D tensor, but got shape {block_tables.shape}")
+    if cu_seqlens.dim() != 1:
+        raise ValueError("cu_seqlens must be a 1D tensor")
     dev = _lib.require_device(prefill_q, prefill_k, prefill_v, cu_seqlens, query, k_cache, v_cache, block_tables,
                               seq_lens)
     if prefill_scale is None:

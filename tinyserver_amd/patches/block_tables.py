@@ -24,6 +24,12 @@ uploaded whole again. Changing an entry other than the last one in place,
 which the BlockManager never does, is not detected. Entries not in the
 current batch are evicted least recently used first when rows run out; the
 mirror grows when a batch needs more rows or a longer table than it has.
+
+One stream per mirror: the scatter of a step's changed entries and the
+gather of its table run on whatever stream is current, and nothing orders
+them against another stream's use of the mirror. The reference engine runs
+every forward on one stream, and the glue keeps one mirror per device; a
+caller that drives steps from several streams needs one mirror per stream.
 """
 
 from __future__ import annotations
