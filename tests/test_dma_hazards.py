@@ -26,7 +26,7 @@ import pytest
 
 from tinyserver_amd import _build as B
 
-DMA_SOURCES = ["paged_decode.hip", "varlen_prefill.hip"]
+DMA_SOURCES = ["paged_decode.hip", "varlen_prefill.hip", "varlen_prefill_w64.hip"]
 VALU_SGPR_WS = 5  # VALU writes an SGPR -> VMEM reads it
 SALU_M0_WS = 1  # SALU writes M0 -> LDS DMA reads it
 

@@ -19,7 +19,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libtsa.so"
-SOURCES = ["tsa_common.hip", "kv_store.hip", "qk_norm_rope.hip", "paged_decode.hip", "varlen_prefill.hip", "sampling.hip"]
+SOURCES = ["tsa_common.hip", "kv_store.hip", "qk_norm_rope.hip", "paged_decode.hip", "varlen_prefill.hip",
+           "varlen_prefill_w64.hip", "sampling.hip"]
 ARCH = "gfx950"
 # Packed-fp32 VALU instructions are disabled: the compiler may not form them.
 CFLAGS = [

@@ -267,6 +267,14 @@ static int launch_persistent(const PrefillArgs& a, hipStream_t stream) {
 // per-sequence query-block counts in 16 bits (every sequence's length is at
 // most total_q). Both need a positive scale (the masked-score sentinel).
 constexpr int64_t kMaxStride = int64_t{1} << 24;
+// varlen_prefill_w64 (varlen_prefill_w64.hip): head_dim 128, groups of a
+// multiple of 4 q-heads, its per-sequence tile counts in LDS, 16-bit tile
+// counts.
+static bool takes_w64(const PrefillArgs& a) {
+  return a.D == 128 && a.G % 4 == 0 && a.scale_log2 > 0.f && a.k_st < kMaxStride && a.v_st < kMaxStride &&
+         a.nseq <= kW64MaxSeqsHost && a.total_q <= int64_t{65535} * 64 && a.Hkv * (a.G / 4) < 32768 &&
+         prefill_w64_enabled();
+}
 static bool takes_gqa(const PrefillArgs& a) {
   return (a.G == 2 || a.G == 4 || a.G == 8) && a.scale_log2 > 0.f && a.k_st < kMaxStride && a.v_st < kMaxStride &&
          a.nseq <= max_persist_seqs(a.G) && a.total_q <= int64_t{65535} * 32;
@@ -280,6 +288,7 @@ static int launch_prefill(PrefillArgs& a, bool mfma, int64_t total_q, int64_t ma
     return check_launch("tsa_varlen_prefill");
   }
   if constexpr (sizeof(T) == 2) {
+    if (takes_w64(a)) return prefill_w64_launch(a, sizeof(T) == 2 && std::is_same<T, bf16_t>::value, stream);
     if (takes_gqa(a)) {
       if (a.D == 128) {
         if (a.G == 2) return launch_persistent<T, 128, 2>(a, stream);

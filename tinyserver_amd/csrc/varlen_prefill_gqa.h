@@ -714,5 +714,9 @@ int prefill_prepare(const tsa_view* out, const tsa_view* q, const tsa_view* k, c
                     int64_t max_seqlen_k, int32_t causal, double softmax_scale, PrefillArgs& a, bool& mfma);
 int prefill_launch(PrefillArgs& a, bool mfma, int dtype, int64_t max_seqlen_q, hipStream_t stream);
 bool prefill_takes_gqa4(const PrefillArgs& a, bool mfma);
+// varlen_prefill_w64.hip: its launch (bf16 or f16) and its sequence limit.
+constexpr int kW64MaxSeqsHost = 2048;
+int prefill_w64_launch(const PrefillArgs& a, bool bf16, hipStream_t stream);
+bool prefill_w64_enabled();
 
 }  // namespace tsa
