@@ -271,7 +271,8 @@ constexpr int64_t kMaxStride = int64_t{1} << 24;
 // multiple of 4 q-heads, its per-sequence tile counts in LDS, 16-bit tile
 // counts.
 static bool takes_w64(const PrefillArgs& a) {
-  return a.D == 128 && a.G % 4 == 0 && a.scale_log2 > 0.f && a.k_st < kMaxStride && a.v_st < kMaxStride &&
+  return a.D == 128 && a.G % 4 == 0 && a.scale_log2 > 0.f && a.q_st < kMaxStride && a.k_st < kMaxStride &&
+         a.v_st < kMaxStride &&
          a.nseq <= kW64MaxSeqsHost && a.total_q <= int64_t{65535} * 64 && a.Hkv * (a.G / 4) < 32768 &&
          prefill_w64_enabled();
 }

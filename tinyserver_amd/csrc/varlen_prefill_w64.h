@@ -338,40 +338,57 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
     rp += 32 * st_b;
     rk += 32;
   };
-  // This wave's Q for an item into its Q area: load (t, jj) holds, in lane
-  // (h, c), query q0 + 32t + c's dims 16jj + 8h..+8 (rows past q_len repeat
-  // the last row; their outputs are never stored). 16 loads.
+  // This wave's Q for an item into its Q area, each 32-query tile laid out
+  // as a K block (tile t at t * 8 KB, row r = query q0 + 32t + r), whole
+  // rows per load: load i of a tile fetches rows 4i .. 4i+3, lane l the chunk
+  // (l % 16) ^ swz(4i + l / 16) of row 4i + l / 16 (swz(4i + l / 16) =
+  // 4(l / 16) + i % 4). Rows past q_len repeat the last row; their outputs
+  // are never stored. 16 loads, each of 8 whole 128-byte lines.
   const uint32_t q_lds = smem_lds + QOFF + wave * kW64QArea;
+  const int64_t qst_b = a.q_st * static_cast<int64_t>(sizeof(T));
+  const uint32_t q_rpart = static_cast<uint32_t>(lrow * qst_b);
+  const uint32_t q_cpart = 16u * static_cast<uint32_t>((lane % CPR) ^ (lrow << 2));
   auto dma_q = [&](const Item& it) __attribute__((always_inline)) {
+    const char* const qb = reinterpret_cast<const char*>(it.qb);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const int row = min(it.q0 + 32 * t + c, it.q_len - 1);
-      const T* src = it.qb + static_cast<int64_t>(row) * a.q_st + 8 * h;
+      const int r0 = it.q0 + 32 * t;
+      if (r0 + 32 <= it.q_len) {
+        const char* const tb = qb + r0 * qst_b;
 #pragma unroll
-      for (int jj = 0; jj < KJ; ++jj) dma16(src + 16 * jj, q_lds + (t * KJ + jj) * 1024);
+        for (int i = 0; i < 8; ++i)
+          dma16_sv(tb + 4 * i * qst_b, q_rpart + (q_cpart ^ (16u * (i & 3))), q_lds + t * BLKB + i * 1024);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int row = min(r0 + 4 * i + lrow, it.q_len - 1);
+          dma16(qb + row * qst_b + (q_cpart ^ (16u * (i & 3))), q_lds + t * BLKB + i * 1024);
+        }
+      }
     }
   };
   constexpr int kQLoads = 2 * KJ;
   auto wait_loads = [&](auto n) { wait_vmcnt<decltype(n)::value>(); };
 
+  // K operands of the block in slot ks: lane (h, c) reads key c, dims
+  // 16jj + 8h..+8 (chunk 2jj + h at position (2jj + h) ^ swz(c)).
+  int kaj[KJ];
+#pragma unroll
+  for (int jj = 0; jj < KJ; ++jj) kaj[jj] = (c * RB + 16 * (h ^ swz(c))) ^ (32 * jj);
   // Q stays in AGPRs for the whole item: the score MFMAs read their B
   // operand from there, which leaves the VGPRs to the softmax and the K/V
-  // operands.
+  // operands. Lane (h, c) takes query c's dims 16jj + 8h..+8, read as a K
+  // operand is.
   u32x4 qop[2][KJ];
   auto read_q = [&]() {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int jj = 0; jj < KJ; ++jj) {
-        qop[t][jj] = *reinterpret_cast<const u32x4*>(smem + QOFF + wave * kW64QArea + (t * KJ + jj) * 1024 + 16 * lane);
+        qop[t][jj] = *reinterpret_cast<const u32x4*>(smem + QOFF + wave * kW64QArea + t * BLKB + kaj[jj]);
         in_agpr(qop[t][jj]);
       }
   };
-  // K operands of the block in slot ks: lane (h, c) reads key c, dims
-  // 16jj + 8h..+8 (chunk 2jj + h at position (2jj + h) ^ swz(c)).
-  int kaj[KJ];
-#pragma unroll
-  for (int jj = 0; jj < KJ; ++jj) kaj[jj] = (c * RB + 16 * (h ^ swz(c))) ^ (32 * jj);
   u32x4 kop[KJ];
   auto kread1 = [&](auto ks, int jj) __attribute__((always_inline)) {
     kop[jj] = *reinterpret_cast<const u32x4*>(smem + static_cast<int>(ks) * BLKB + kaj[jj]);
@@ -465,17 +482,18 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
   // ---- One half-iteration: the softmax of tile t (its scores are in sc[t],
   // their max in mt[t]) under 16 MFMA slots of tile o = 1 - t: slots 0-7 the
   // score MFMAs of o's next block (QK), slots 8-15 the P.V MFMAs of o's
-  // previous block. Slot g issues its MFMA, the operand reads of the next
-  // block (K after a QK, V after a P.V; the H0 half only), the fma of score
-  // g, the exponential of score g-1, the l term of score g-2 and, every
-  // other slot, the P operand of a finished pair; slots 12-15 also take the
-  // max of o's new scores (its QK MFMAs finished by then: >= 11 wait states
-  // after the last one), and slot 10 masks them where needed.
-  // The fences hold this order, so every instruction's inputs were produced
-  // at least one slot earlier.
-  auto half = [&](const Item& it, int t, int mblk, auto reads, auto kslot, auto vslot, bool do_qk)
+  // previous block. Slot g issues its MFMA, operand reads (H0: K of the next
+  // block after each QK; H1: the V operands of the block, pair g in QK slot
+  // g, eight slots before the P.V MFMA that uses it, so each half reads half
+  // of the wave's LDS bytes), the fma of score g, the exponential of score
+  // g-1, the l term of score g-2 and, every other slot, the P operand of a
+  // finished pair; slots 12-15 also take the max of o's new scores (its QK
+  // MFMAs finished by then: >= 11 wait states after the last one), and slot
+  // 10 masks them where needed. The fences hold this order, so every
+  // instruction's inputs were produced at least one slot earlier.
+  auto half = [&](const Item& it, int t, int mblk, auto kslot, auto vslot, bool do_qk)
                   __attribute__((always_inline)) {
-    constexpr bool READS = decltype(reads)::value;
+    constexpr bool KREADS = decltype(kslot)::value >= 0, VREADS = decltype(vslot)::value >= 0;
     const int o = 1 - t;
     rescale_check(t);
     const float mm = m[t] == kNegInfP ? 0.f : m[t];
@@ -484,16 +502,20 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
     for (int g = 0; g < 16; ++g) {
       if (g < 8) {
         if (do_qk) qk1(o, g);
-        if constexpr (READS) kread1(kslot, g);
+        if constexpr (KREADS) kread1(kslot, g);
+        if constexpr (VREADS) vread1(vslot, g / NU, g % NU);
       } else {
         pv1(o, (g - 8) / NU, (g - 8) % NU);
         in_agpr(acc[o][(g - 8) % NU]);  // keeps the MFMA in its slot
-        if constexpr (READS) vread1(vslot, (g - 8) / NU, (g - 8) % NU);
       }
       x[g] = fmaf(sc[t][g], cs, -mm);
       if (g >= 1) p[g - 1] = fast_exp2(x[g - 1]);
       if (g >= 2) lp[t][g & 1] += p[g - 2];
-      if (g >= 3 && (g & 1)) pop[t][(g - 3) >> 3][((g - 3) & 7) >> 1] = pack2<T>(p[g - 3], p[g - 2]);
+      if (g >= 3 && (g & 1)) {
+        uint32_t pk = pack2<T>(p[g - 3], p[g - 2]);
+        asm volatile("" : "+v"(pk));
+        pop[t][(g - 3) >> 3][((g - 3) & 7) >> 1] = pk;
+      }
       // Blocks from jm on may hold keys past k_len or (causal) past the
       // query: a uniform branch, rarely taken.
       if (g == 10 && do_qk && mblk >= it.jm) {
@@ -503,7 +525,8 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
       if (g >= 12 && do_qk) max_part(o, g - 12);
       // The slot's results, pinned here: nothing of it can sink into a later
       // slot or past the mask branch.
-      asm volatile("" : "+v"(lp[t][0]), "+v"(lp[t][1]));
+      asm volatile("" : "+v"(lp[t][0]), "+v"(lp[t][1]), "+v"(x[g]));
+      if (g >= 1) asm volatile("" : "+v"(p[g - 1]));
       if (g >= 12 && do_qk) asm volatile("" : "+v"(mxa), "+v"(mxb));
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -521,23 +544,23 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
   // ---- One iteration j: on entry S0(j) is in sc[0] with its max in mt[0],
   // P1(j-1) in pop[1], K(j) in kop and V(j-1) in vop (zeros before the
   // first block); step j's loads (K(j + 1), V(j)) were issued A iterations
-  // ago. H0(j): softmax of tile 0, block j | QK1(j), PV1(j-1), reads K(j+1)
-  // and V(j); H1(j): softmax of tile 1, block j | QK0(j+1), PV0(j). In the
+  // ago. H0(j): softmax of tile 0, block j | QK1(j), PV1(j-1), reads K(j+1);
+  // H1(j): softmax of tile 1, block j | QK0(j+1), reads V(j), PV0(j). In the
   // last iteration the K(j + 1) read and QK0(j+1) are not used (the slot
   // holds a clamped copy of the last block). S is the slot phase j % NB, a
   // compile-time constant.
   auto iter = [&](const Item& it, int j, auto S) __attribute__((always_inline)) {
     // Step j has landed for every wave: wait for this wave's loads of it,
     // meet the others, then issue step j + A (its slots were last read in
-    // H0(j + A - NB) < H0(j), before this barrier).
+    // iteration j + A - NB < j, before this barrier).
     const bool issue = j + A < it.nblk;
     if (issue) wait_loads(std::integral_constant<int, kInFlight>{});
     else wait_loads(std::integral_constant<int, 0>{});
     lds_barrier();
     constexpr int s = decltype(S)::value;
     if (issue) load_step_c(it, j, S);
-    half(it, 0, j, std::true_type{}, std::integral_constant<int, (s + 1) % NB>{}, S, true);
-    half(it, 1, j + 1, std::false_type{}, std::integral_constant<int, 0>{}, S, true);
+    half(it, 0, j, std::integral_constant<int, (s + 1) % NB>{}, std::integral_constant<int, -1>{}, true);
+    half(it, 1, j + 1, std::integral_constant<int, -1>{}, S, true);
   };
 
   // The output of a finished item, in whole 128-byte lines: each tile goes
