@@ -40,6 +40,9 @@
  *                           that batches them together (the reference's
  *                           scheduler issues them apart, scheduler.py:128-227)
  *   tsa_sample_tokens       server/model/sampling.py:119-194 (sample_tokens)
+ *   tsa_sample_tokens_ws    the same, with a workspace that lets a small
+ *                           batch spread each row over several workgroups
+ *   tsa_sample_tokens_workspace_bytes  its size
  */
 #ifndef TSA_API_H
 #define TSA_API_H
@@ -237,6 +240,24 @@ int tsa_mixed_attention(const tsa_view* prefill_out, const tsa_view* prefill_q, 
 int tsa_sample_tokens(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature,
                       const tsa_view* top_k, const tsa_view* top_p, const tsa_view* uniforms,
                       void* stream);
+
+/* Bytes of the workspace tsa_sample_tokens_ws takes for `batch` rows of
+ * `vocab` logits; 0 when such a batch never splits its rows. */
+size_t tsa_sample_tokens_workspace_bytes(int64_t batch, int64_t vocab);
+
+/* sample_tokens (server/model/sampling.py:119-194), as tsa_sample_tokens,
+ * with a workspace (256-byte aligned, at least
+ * tsa_sample_tokens_workspace_bytes(B, V) bytes, contents arbitrary; NULL:
+ * tsa_sample_tokens). For a batch of at most 256 rows of at least 16384
+ * bf16/f16 logits in 16-byte aligned rows, the rows that take the histogram
+ * path (temperature > 0 and not top-k/greedy candidate rows: the server's
+ * default top-p request among them) have their statistics and histogram
+ * passes spread over several workgroups per row (two more launches on
+ * `stream`); the tokens are those of tsa_sample_tokens. Calls that share a
+ * workspace must be ordered on one stream. */
+int tsa_sample_tokens_ws(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature,
+                         const tsa_view* top_k, const tsa_view* top_p, const tsa_view* uniforms,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

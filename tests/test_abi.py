@@ -201,3 +201,17 @@ def test_workspace_plan():
     n = lib.tsa_paged_decode_workspace_bytes(2, 8, 2, 128, 64, 16, 10)
     assert n >= (2 * 2 + 4 * 10) * 4 * (128 + 2) * 4 + 3 * 4
     assert lib.tsa_paged_decode_workspace_bytes(0, 8, 2, 128, 64, 16, 10) == 0
+
+
+def test_sampling_workspace_plan():
+    lib = _lib.load()
+    # Split rows: 512 / B segments per row (2 .. 16), each a 32-byte
+    # statistics record and 2048 buckets of a 4-byte count and an 8-byte mass.
+    segs = 64 * 8
+    assert lib.tsa_sample_tokens_workspace_bytes(64, 151936) >= segs * (32 + 2048 * 12)
+    assert lib.tsa_sample_tokens_workspace_bytes(1, 151936) >= 16 * (32 + 2048 * 12)
+    assert lib.tsa_sample_tokens_workspace_bytes(256, 151936) >= 256 * 2 * (32 + 2048 * 12)
+    # No split: a batch that fills the device one row per workgroup, or short rows.
+    assert lib.tsa_sample_tokens_workspace_bytes(257, 151936) == 0
+    assert lib.tsa_sample_tokens_workspace_bytes(64, 4096) == 0
+    assert lib.tsa_sample_tokens_workspace_bytes(0, 151936) == 0

@@ -18,7 +18,11 @@ against the oracle in the cases above and against the histogram paths
 (TSA_SAMPLE_CANDIDATES=0) on the same rows token for token, and its edge rows
 (too many candidates, -0 beside +0, the largest top_k it takes and the next,
 flat rows with many candidates, short and odd-sized rows) against the
-oracle.
+oracle. A batch of at most 256 rows of >= 16384 16-bit logits (most cases
+here) spreads each histogram row's statistics and histogram passes over
+several workgroups (sample_tokens' workspace); those rows are checked
+against the oracle above and, token for token, against the one-workgroup
+launch, including the server's default request.
 """
 
 import os
@@ -338,6 +342,75 @@ def test_candidate_path_short_and_odd_rows(v):
     k = min(5, v - 1)
     _compare(rows, [1.0, 0.0, 0.7, 1.0, 1.3, 0.9], [k, 0, 1, k, 3 if v > 3 else 1, 2], [0.9, 1.0, 1.0, 0.5, 1.0, 0.8],
              [0.1, 0.5, 0.6, 0.99, 0.3, 0.0], dtype=torch.bfloat16, what=f"v={v}")
+
+
+def _one_workgroup(logits, temperature, top_k, top_p, uniforms):
+    """tsa_sample_tokens without a workspace: every row on one workgroup."""
+    out = torch.empty(logits.shape[0], dtype=torch.int64, device=DEV)
+    views = [_lib.view(x) for x in (out, logits, temperature, top_k, top_p, uniforms)]
+    _lib.check(_lib.load().tsa_sample_tokens(*map(_lib.ref, views), _lib.stream_of(logits.device)), "one workgroup")
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("b", [1, 3, 64, 256])
+def test_split_rows_match_one_workgroup(dtype, b):
+    """A batch of at most 256 rows of >= 16384 16-bit logits spreads its
+    histogram rows' statistics and histogram passes over several workgroups
+    per row (16 segments at b = 1 and 3, 8 at 64, 2 at 256): token for token
+    the one-workgroup path's, for rows of every kind (the server's default
+    request, top-p only, full, top_k > 512 with top-p, top-k and greedy rows
+    that take the candidate pass)."""
+    g = torch.Generator().manual_seed(31 + b)
+    v = 151936
+    logits = torch.randn(b, v, generator=g) * 2.5
+    logits.scatter_add_(1, torch.randint(0, v, (b, 8), generator=g), torch.rand(b, 8, generator=g) * 12)
+    kinds = [(1.0, 0, 0.95), (0.8, 0, 0.9), (1.3, 0, 1.0), (0.7, 2000, 0.8), (1.0, 50, 0.9), (0.0, 0, 1.0)]
+    temperature = [kinds[i % 6][0] for i in range(b)]
+    top_k = [kinds[i % 6][1] for i in range(b)]
+    top_p = [kinds[i % 6][2] for i in range(b)]
+    uniforms = torch.rand(b, generator=g).tolist()
+    t = lambda x, dt: torch.tensor(x, dtype=dt, device=DEV)
+    args = (logits.to(DEV, dtype), t(temperature, torch.float32), t(top_k, torch.int64), t(top_p, torch.float32),
+            t(uniforms, torch.float32))
+    assert _lib.load().tsa_sample_tokens_workspace_bytes(b, v) > 0
+    split = sample_tokens(*args).cpu()
+    assert torch.equal(split, _one_workgroup(*args)), (split.tolist(), _one_workgroup(*args).tolist())
+
+
+def test_server_default_request():
+    """The reference server's default request (temperature 1.0, top_p 0.95,
+    top_k 0: server/api/schema.py:11-15) over a 64-row Qwen3-vocab bf16
+    batch, through the split rows: against the oracle and the one-workgroup
+    path."""
+    logits, _, _, _, uniforms = _qwen3_batch(27)
+    b = logits.shape[0]
+    _compare(logits, [1.0] * b, [0] * b, [0.95] * b, uniforms, torch.bfloat16, what="server default")
+    t = lambda x, dt: torch.tensor(x, dtype=dt, device=DEV)
+    args = (logits.to(DEV, torch.bfloat16), t([1.0] * b, torch.float32), t([0] * b, torch.int64),
+            t([0.95] * b, torch.float32), t(uniforms, torch.float32))
+    assert torch.equal(sample_tokens(*args).cpu(), _one_workgroup(*args))
+
+
+def test_split_workspace_checks():
+    """tsa_sample_tokens_ws: a workspace smaller than asked for is refused; a
+    NULL one is the one-workgroup launch."""
+    lib = _lib.load()
+    logits, temperature, top_k, top_p, uniforms = _qwen3_batch(28, b=8)
+    t = lambda x, dt: torch.tensor(x, dtype=dt, device=DEV)
+    args = (logits.to(DEV, torch.bfloat16), t(temperature, torch.float32), t(top_k, torch.int64),
+            t(top_p, torch.float32), t(uniforms, torch.float32))
+    out = torch.empty(8, dtype=torch.int64, device=DEV)
+    views = [_lib.view(x) for x in (out, *args)]
+    need = lib.tsa_sample_tokens_workspace_bytes(8, logits.shape[1])
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    with pytest.raises(ValueError, match="workspace too small"):
+        _lib.check(lib.tsa_sample_tokens_ws(*map(_lib.ref, views), ws.data_ptr(), need - 1, _lib.stream_of(ws.device)),
+                   "ws")
+    _lib.check(lib.tsa_sample_tokens_ws(*map(_lib.ref, views), None, 0, _lib.stream_of(ws.device)), "ws")
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), _one_workgroup(*args))
 
 
 def test_graph_replays_match_eager():

@@ -67,6 +67,8 @@ SIGNATURES = {
         [_V] * 5 + [c_int64, c_double] + [_V] * 6 + [c_double, c_void_p, c_size_t, c_int32, c_int32, c_void_p],
     ),
     "tsa_sample_tokens": (c_int, [_V, _V, _V, _V, _V, _V, c_void_p]),
+    "tsa_sample_tokens_workspace_bytes": (c_size_t, [c_int64, c_int64]),
+    "tsa_sample_tokens_ws": (c_int, [_V, _V, _V, _V, _V, _V, c_void_p, c_size_t, c_void_p]),
 }
 
 ABI_VERSION = 1

@@ -62,6 +62,130 @@ struct SampleArgs {
   const float* unif; int64_t unif_s;
   int64_t* out; int64_t out_s;
   int cand;  // 1: top-k and greedy rows may take the register-resident candidate pass
+  // Rows split over S workgroups (split_row; S = 0: none): per (row,
+  // segment) the statistics record and the partial histogram.
+  struct SplitStat* stat;
+  uint32_t* pcnt;
+  uint64_t* pmass;
+  int S;
+};
+
+// ---- Rows split over several workgroups. A histogram row (temperature >
+// 0, not a candidate row) of 16-bit logits in 8-logit chunks has its two
+// full passes -- the statistics, then the count and mass histogram -- run
+// by S workgroups, each over a contiguous range of the row's chunks
+// (sample_split_stats, sample_split_hist); sample_tokens_kernel then merges
+// the S records and partial histograms instead of making those passes
+// itself and decides as before. The statistics' tie rules (first index of
+// the maximum, last of the minimum) and the exact fixed-point mass sums are
+// order-free, so the merged values -- and the tokens -- are the one-
+// workgroup path's.
+constexpr int kSplitThreads = 256;
+constexpr int kMaxSegments = 16;  // workgroups per split row, at most
+struct SplitStat {
+  float mx, mn, fmn;
+  int imx, imn, inan;
+  int pad[2];
+};
+
+// f(w, ch) for chunks ch = first, first + step, ... < end of a row, in
+// increasing order, kLoadBatch loads issued before any is used: a pass over
+// a row is then bound by bandwidth rather than by one load's latency per
+// chunk.
+constexpr int kLoadBatch = 8;
+template <typename F>
+__device__ __forceinline__ void each_chunk(const u32x4* r4, int first, int end, int step, F f) {
+  for (int base = first; base < end; base += kLoadBatch * step) {
+    u32x4 w[kLoadBatch];
+#pragma unroll
+    for (int j = 0; j < kLoadBatch; ++j) {
+      const int ch = base + j * step;
+      w[j] = ch < end ? r4[ch] : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < kLoadBatch; ++j) {
+      const int ch = base + j * step;
+      if (ch < end) f(w[j], ch);
+    }
+  }
+}
+
+// Statistics of a thread's 8-logit chunks, visited in increasing order: the
+// maximum and its first index (rank 0), the minimum and the last index of
+// it (the last rank), the finite minimum and the first NaN. A strict >
+// keeps the first index of a maximum and <= the last of a minimum.
+struct ChunkStats {
+  float mx, mn, fmn;
+  int imx, imn, inan;
+  __device__ __forceinline__ void init(int V) {
+    mx = -INFINITY;
+    mn = INFINITY;
+    fmn = INFINITY;
+    imx = V;
+    imn = -1;
+    inan = V;
+  }
+  template <typename T>
+  __device__ __forceinline__ void add(const u32x4 w, int ch, int V) {
+    float l[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      l[2 * e] = lo_f<T>(w[e]);
+      l[2 * e + 1] = hi_f<T>(w[e]);
+    }
+    // cmax propagates NaN (v_maximum3_f32): a chunk holding a NaN never
+    // passes cmax > mx, and records its first NaN instead.
+    float cmax = l[0], cmin = l[0], cfin = l[0] != -INFINITY ? l[0] : INFINITY;
+#pragma unroll
+    for (int e = 1; e < 8; ++e) {
+      cmax = __builtin_elementwise_maximum(cmax, l[e]);
+      cmin = fminf(cmin, l[e]);
+      cfin = fminf(cfin, l[e] != -INFINITY ? l[e] : INFINITY);
+    }
+    fmn = fminf(fmn, cfin);
+    if (cmax != cmax && inan == V) {
+      int first = 7;
+#pragma unroll
+      for (int e = 7; e >= 0; --e)
+        if (l[e] != l[e]) first = e;
+      inan = 8 * ch + first;
+    }
+    if (cmax > mx) {
+      int first = 0;
+#pragma unroll
+      for (int e = 7; e >= 0; --e)
+        if (l[e] == cmax) first = e;
+      mx = cmax;
+      imx = 8 * ch + first;
+    }
+    if (cmin <= mn) {
+      int last = 7;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (l[e] == cmin) last = e;
+      mn = cmin;
+      imn = 8 * ch + last;
+    }
+  }
+  // Combine with the statistics of other elements (in any order).
+  __device__ __forceinline__ void merge(float omx, int oimx, float omn, int oimn, float ofm, int onan) {
+    if (omx > mx || (omx == mx && oimx < imx)) {
+      mx = omx;
+      imx = oimx;
+    }
+    if (omn < mn || (omn == mn && oimn > imn)) {
+      mn = omn;
+      imn = oimn;
+    }
+    fmn = fminf(fmn, ofm);
+    inan = min(inan, onan);
+  }
+  __device__ __forceinline__ void merge(const SplitStat& o) { merge(o.mx, o.imx, o.mn, o.imn, o.fmn, o.inan); }
+  __device__ __forceinline__ void wave_reduce() {
+    for (int o = 32; o > 0; o >>= 1)
+      merge(__shfl_xor(mx, o, 64), __shfl_xor(imx, o, 64), __shfl_xor(mn, o, 64), __shfl_xor(imn, o, 64),
+            __shfl_xor(fmn, o, 64), __shfl_xor(inan, o, 64));
+  }
 };
 
 __device__ __forceinline__ int64_t load_int(const void* p, int dt, int64_t i) {
@@ -105,6 +229,12 @@ constexpr int kSelBins = 4096;        // 12-bit key prefixes
 // top-k cut falls inside the row, with top_k <= kFastK.
 __device__ __forceinline__ bool candidate_row(const SampleArgs& a, float temp, int64_t k) {
   return temp <= 0.f || (k > 0 && k <= kFastK && k < a.V);
+}
+
+// The rows whose statistics and histogram sample_split_stats and
+// sample_split_hist make (a.S > 1: the launch split rows).
+__device__ __forceinline__ bool split_row(const SampleArgs& a, float temp, int64_t k) {
+  return a.S > 1 && temp > 0.f && !(a.cand && a.V <= kRegMaxV && candidate_row(a, temp, k));
 }
 
 // Two 16-bit floats (one word) -> two order-preserving 16-bit keys, larger
@@ -192,10 +322,7 @@ struct RowSampler {
     if constexpr (UNIT && sizeof(T) == 2) {
       if (chunked()) {
         const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
-        const int n8 = static_cast<int>(a.V >> 3);
-#pragma unroll 8
-        for (int ch = tid; ch < n8; ch += kSampThreads) {
-          const u32x4 w = r4[ch];
+        each_chunk(r4, tid, static_cast<int>(a.V >> 3), kSampThreads, [&](const u32x4 w, int ch) {
           float l[8];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -208,10 +335,10 @@ struct RowSampler {
             cmax = fmaxf(cmax, l[e]);
             cmin = fminf(cmin, l[e]);
           }
-          if (cmax < lo || cmin > hi) continue;  // (kByLogit: keys are the logits)
+          if (cmax < lo || cmin > hi) return;  // (kByLogit: keys are the logits)
 #pragma unroll
           for (int e = 0; e < 8; ++e) f(8 * ch + e, l[e]);
-        }
+        });
         return;
       }
     }
@@ -237,16 +364,13 @@ struct RowSampler {
     if constexpr (UNIT && sizeof(T) == 2) {
       if (chunked()) {
         const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
-        const int n8 = static_cast<int>(a.V >> 3);
-#pragma unroll 8
-        for (int ch = tid; ch < n8; ch += kSampThreads) {
-          const u32x4 w = r4[ch];
+        each_chunk(r4, tid, static_cast<int>(a.V >> 3), kSampThreads, [&](const u32x4 w, int ch) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float l = (e & 1) ? hi_f<T>(w[e >> 1]) : lo_f<T>(w[e >> 1]);
             f(8 * ch + e, kByLogit ? l : __fdiv_rn(l, t));
           }
-        }
+        });
         return;
       }
     }
@@ -255,6 +379,7 @@ struct RowSampler {
   __device__ __forceinline__ float key_to_x(float k) const { return kByLogit ? __fdiv_rn(k, t) : k; }
   float kmax;  // row maximum of key_at
   float kc;    // log2(e) / t for 16-bit logits, log2(e) for fp32 (keys are x)
+  int64_t srow = -1;  // >= 0: the shared histogram is the sum of this row's split partials
   // 2^40 exp(x - xmax) from a key (mass_of): the single-histogram path's
   // mass; the row maximum weighs exactly 2^40.
   __device__ __forceinline__ uint64_t mass_key(float kv) const { return mass_of(kv, kmax, kc); }
@@ -295,6 +420,22 @@ struct RowSampler {
 
   // Bitonic sort of s.keys[0, n) ascending, padded to a power of two.
   __device__ __forceinline__ void sort_keys(int n) {
+    if (n <= 512) {
+      // Few keys (a bucket of tied or close logits): each of the first n
+      // threads counts the keys below its own -- the keys are distinct (they
+      // hold the index) -- and writes it to that rank: two barriers instead
+      // of the bitonic network's one per stage.
+      uint64_t mine = 0;
+      int rank = 0;
+      if (tid < n) {
+        mine = s.keys[tid];
+        for (int j = 0; j < n; ++j) rank += s.keys[j] < mine ? 1 : 0;
+      }
+      __syncthreads();
+      if (tid < n) s.keys[rank] = mine;
+      __syncthreads();
+      return;
+    }
     int p = 1;
     while (p < n) p <<= 1;
     for (int i = n + tid; i < p; i += kSampThreads) s.keys[i] = ~uint64_t{0};
@@ -359,17 +500,69 @@ struct RowSampler {
   }
 
   // Gathers bucket b of the shared histogram into s.keys in rank order.
+  // The first 16-bit key (pk_key order, between the -inf and +inf keys)
+  // whose logit's bucket is at most b: bucket0 never increases along the
+  // keys, so bisection finds it. No NaN reaches the histogram path.
+  __device__ __forceinline__ uint32_t first_key_at_most(int b, float scale) const {
+    uint32_t lo = Inf16<T>::kNegKey, hi = Inf16<T>::kPosKey + 1;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) >> 1;
+      if (bucket0(lo_f<T>(key_bits(mid)), kmax, scale) <= b) hi = mid;
+      else lo = mid + 1;
+    }
+    return lo;
+  }
+  // Every element whose 16-bit key lies in [klo, khi] into s.keys (as a rank
+  // key), for a chunked 16-bit row: per 8-logit chunk, packed 16-bit keys,
+  // their offsets from klo and the offsets' minimum tell in a few
+  // instructions whether any key of the chunk is in the range; only such
+  // chunks are looked into.
+  __device__ __forceinline__ void gather_key_range(uint32_t klo, uint32_t khi) {
+    const uint32_t span = khi - klo, lo2 = klo | (klo << 16);
+    each_chunk(reinterpret_cast<const u32x4*>(row), tid, static_cast<int>(a.V >> 3), kSampThreads,
+               [&](const u32x4 w, int ch) {
+                 uint32_t k[4], m = 0xFFFFFFFFu;
+#pragma unroll
+                 for (int e = 0; e < 4; ++e) {
+                   k[e] = pk_key(w[e]);
+                   // key - klo in each half, mod 2^16: a key below klo wraps above span
+                   m = pk_min(m, __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, k[e]) -
+                                                                  __builtin_bit_cast(u16x2, lo2)));
+                 }
+                 if (min(m & 0xFFFFu, m >> 16) > span) return;  // no key of the chunk in range
+#pragma unroll
+                 for (int e = 0; e < 8; ++e) {
+                   const uint32_t key = (k[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+                   if (key - klo <= span) {
+                     const uint32_t at = atomicAdd(&s.n_gather, 1u);
+                     if (at < kCap)
+                       s.keys[at] = rank_key((e & 1) ? hi_f<T>(w[e >> 1]) : lo_f<T>(w[e >> 1]), 8 * ch + e);
+                   }
+                 }
+               });
+  }
+
   __device__ __forceinline__ bool gather_sorted(int b, float scale, int& cached) {
     if (cached == b) return true;
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
-    // (a single bucket is a narrow range most chunks straddle: no skipping)
-    each_key([&](int i, float kv) {
-      if (bucket0(kv, kmax, scale) == b) {
-        const uint32_t at = atomicAdd(&s.n_gather, 1u);
-        if (at < kCap) s.keys[at] = rank_key(kv, i);
+    bool keyed = false;
+    if constexpr (UNIT && sizeof(T) == 2) {
+      if (chunked()) {  // the bucket: keys [first_key_at_most(b), first_key_at_most(b - 1))
+        const uint32_t klo = first_key_at_most(b, scale);
+        const uint32_t khi = (b > 0 ? first_key_at_most(b - 1, scale) : Inf16<T>::kPosKey + 1) - 1;
+        gather_key_range(klo, khi);
+        keyed = true;
       }
-    });
+    }
+    // (a single bucket is a narrow range most chunks straddle: no skipping)
+    if (!keyed)
+      each_key([&](int i, float kv) {
+        if (bucket0(kv, kmax, scale) == b) {
+          const uint32_t at = atomicAdd(&s.n_gather, 1u);
+          if (at < kCap) s.keys[at] = rank_key(kv, i);
+        }
+      });
     __syncthreads();
     if (s.n_gather != s.cnt[b]) return false;  // (the histogram's own count: never expected to differ)
     sort_keys(static_cast<int>(s.cnt[b]));
@@ -382,14 +575,23 @@ struct RowSampler {
   __device__ __forceinline__ bool gather_prefix(int nb, float scale) {
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
-    float lo, hi;
-    bucket_range(0, nb, scale, lo, hi);
-    each_key_in(lo, hi, [&](int i, float kv) {
-      if (bucket0(kv, kmax, scale) <= nb) {
-        const uint32_t at = atomicAdd(&s.n_gather, 1u);
-        if (at < kCap) s.keys[at] = rank_key(kv, i);
+    bool keyed = false;
+    if constexpr (UNIT && sizeof(T) == 2) {
+      if (chunked()) {  // buckets 0 .. nb: the keys from first_key_at_most(nb) up
+        gather_key_range(first_key_at_most(nb, scale), Inf16<T>::kPosKey);
+        keyed = true;
       }
-    });
+    }
+    if (!keyed) {
+      float lo, hi;
+      bucket_range(0, nb, scale, lo, hi);
+      each_key_in(lo, hi, [&](int i, float kv) {
+        if (bucket0(kv, kmax, scale) <= nb) {
+          const uint32_t at = atomicAdd(&s.n_gather, 1u);
+          if (at < kCap) s.keys[at] = rank_key(kv, i);
+        }
+      });
+    }
     __syncthreads();
     if (s.n_gather != s.pcnt[nb] + s.cnt[nb]) return false;  // (never expected)
     sort_keys(static_cast<int>(s.pcnt[nb] + s.cnt[nb]));
@@ -911,16 +1113,35 @@ struct RowSampler {
   __device__ __forceinline__ bool fast(float lo, int64_t k, bool cut_k, double p, double u, int64_t& token) {
     // lo: the smallest finite key
     const float scale = kmax > lo ? static_cast<float>(kBuckets - 1) / (kmax - lo) : 0.f;
-    for (int b = tid; b < kBuckets; b += kSampThreads) {
-      s.cnt[b] = 0;
-      s.wsum[b] = 0;
+    if (srow >= 0) {  // the sum of the row's split partials (sample_split_hist, same buckets and masses)
+      const size_t base = static_cast<size_t>(srow) * a.S * kBuckets;
+      for (int b = tid; b < kBuckets; b += kSampThreads) {
+        uint32_t c = 0;
+        uint64_t m = 0;
+        // (every load issued, at a clamped segment, before any is summed)
+#pragma unroll
+        for (int w = 0; w < kMaxSegments; ++w) {
+          const size_t at = base + static_cast<size_t>(min(w, a.S - 1)) * kBuckets + b;
+          const uint32_t cw = a.pcnt[at];
+          const uint64_t mw = a.pmass[at];
+          c += w < a.S ? cw : 0u;
+          m += w < a.S ? mw : uint64_t{0};
+        }
+        s.cnt[b] = c;
+        s.wsum[b] = m;
+      }
+    } else {
+      for (int b = tid; b < kBuckets; b += kSampThreads) {
+        s.cnt[b] = 0;
+        s.wsum[b] = 0;
+      }
+      __syncthreads();
+      each_key([&](int, float kv) {
+        const int b = bucket0(kv, kmax, scale);
+        atomicAdd(&s.cnt[b], 1u);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&s.wsum[b]), static_cast<unsigned long long>(mass_key(kv)));
+      });
     }
-    __syncthreads();
-    each_key([&](int, float kv) {
-      const int b = bucket0(kv, kmax, scale);
-      atomicAdd(&s.cnt[b], 1u);
-      atomicAdd(reinterpret_cast<unsigned long long*>(&s.wsum[b]), static_cast<unsigned long long>(mass_key(kv)));
-    });
     __syncthreads();
     scan2(s.cnt, s.pcnt);
     scan2(s.wsum, s.pmass);
@@ -1181,6 +1402,89 @@ struct RowSampler {
   }
 };
 
+// The chunks of segment seg of a split row: [seg * per, min((seg + 1) *
+// per, V / 8)), per = ceil(V / 8 / S).
+__device__ __forceinline__ void split_range(const SampleArgs& a, int seg, int& c0, int& c1) {
+  const int n8 = static_cast<int>(a.V >> 3), per = (n8 + a.S - 1) / a.S;
+  c0 = min(n8, seg * per);
+  c1 = min(n8, c0 + per);
+}
+
+// The statistics record of segment blockIdx.x of split row blockIdx.y.
+template <typename T>
+__global__ __launch_bounds__(kSplitThreads) void sample_split_stats(SampleArgs a) {
+  const int64_t r = blockIdx.y;
+  const int seg = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (!split_row(a, a.temp[r * a.temp_s], load_int(a.topk, a.topk_dt, r * a.topk_s))) return;
+  int c0, c1;
+  split_range(a, seg, c0, c1);
+  const u32x4* r4 = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.logits) + r * a.ls0);
+  const int V = static_cast<int>(a.V);
+  ChunkStats st;
+  st.init(V);
+  each_chunk(r4, c0 + tid, c1, kSplitThreads, [&](const u32x4 w, int ch) { st.add<T>(w, ch, V); });
+  st.wave_reduce();
+  __shared__ SplitStat red[kSplitThreads / 64];
+  if (lane == 0) red[wave] = SplitStat{st.mx, st.mn, st.fmn, st.imx, st.imn, st.inan, {0, 0}};
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kSplitThreads / 64; ++w) st.merge(red[w]);
+    a.stat[r * a.S + seg] = SplitStat{st.mx, st.mn, st.fmn, st.imx, st.imn, st.inan, {0, 0}};
+  }
+}
+
+// The merged statistics of split row r (its S records).
+__device__ __forceinline__ ChunkStats split_stats(const SampleArgs& a, int64_t r) {
+  ChunkStats st;
+  st.init(static_cast<int>(a.V));
+#pragma unroll
+  for (int w = 0; w < kMaxSegments; ++w)
+    if (w < a.S) st.merge(a.stat[r * a.S + w]);
+  return st;
+}
+
+// The partial histogram (count and mass per bucket, the buckets and masses
+// of RowSampler::fast) of segment blockIdx.x of split row blockIdx.y, for a
+// row that reaches the histogram path: no NaN, a finite maximum of x.
+template <typename T>
+__global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a) {
+  __shared__ uint32_t cnt[kBuckets];
+  __shared__ uint64_t msum[kBuckets];
+  const int64_t r = blockIdx.y;
+  const int seg = blockIdx.x, tid = threadIdx.x;
+  const float temp = a.temp[r * a.temp_s];
+  if (!split_row(a, temp, load_int(a.topk, a.topk_dt, r * a.topk_s))) return;
+  const ChunkStats st = split_stats(a, r);
+  const float t = fmaxf(temp, 1e-5f);
+  if (st.inan < static_cast<int>(a.V) || !(fabsf(__fdiv_rn(st.mx, t)) < INFINITY)) return;  // (uniform)
+  const float kmax = st.mx, kc = 1.4426950408889634f / t, lo = fminf(st.fmn, st.mx);
+  const float scale = kmax > lo ? static_cast<float>(kBuckets - 1) / (kmax - lo) : 0.f;
+  for (int b = tid; b < kBuckets; b += kSplitThreads) {
+    cnt[b] = 0;
+    msum[b] = 0;
+  }
+  __syncthreads();
+  int c0, c1;
+  split_range(a, seg, c0, c1);
+  const u32x4* r4 = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.logits) + r * a.ls0);
+  each_chunk(r4, c0 + tid, c1, kSplitThreads, [&](const u32x4 w, int) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float kv = (e & 1) ? hi_f<T>(w[e >> 1]) : lo_f<T>(w[e >> 1]);
+      const int b = RowSampler<T, true>::bucket0(kv, kmax, scale);
+      atomicAdd(&cnt[b], 1u);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&msum[b]),
+                static_cast<unsigned long long>(mass_of(kv, kmax, kc)));
+    }
+  });
+  __syncthreads();
+  const size_t base = (static_cast<size_t>(r) * a.S + seg) * kBuckets;
+  for (int b = tid; b < kBuckets; b += kSplitThreads) {
+    a.pcnt[base + b] = cnt[b];
+    a.pmass[base + b] = msum[b];
+  }
+}
+
 template <typename T, bool UNIT>
 __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -1191,10 +1495,14 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   const float temp = a.temp[r * a.temp_s];
   RowSampler<T, UNIT> rs{a, s, static_cast<const T*>(a.logits) + r * a.ls0, fmaxf(temp, 1e-5f), 0.f, tid, lane, wave, 0.f, 0.f};
 
+  // Split rows: their statistics and histogram were made by
+  // sample_split_stats and sample_split_hist.
+  const bool split = split_row(a, temp, load_int(a.topk, a.topk_dt, r * a.topk_s));
+
   // Top-k and greedy rows of a 16-bit row that fits the registers: the
   // candidate pass decides from one read of the row, or sends it on.
   if constexpr (UNIT && sizeof(T) == 2) {
-    if (a.cand && rs.chunked() && a.V <= kRegMaxV) {
+    if (!split && a.cand && rs.chunked() && a.V <= kRegMaxV) {
       // The row's parameters are loaded first: loads complete in order, so
       // the test below waits for them alone while the row is in flight.
       const int64_t k = load_int(a.topk, a.topk_dt, r * a.topk_s);
@@ -1217,91 +1525,67 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   // keeps the first index of its maximum and <= the last of its minimum.
   float mx = -INFINITY, mn = INFINITY, fmn = INFINITY;
   int imx = static_cast<int>(a.V), imn = -1, inan = static_cast<int>(a.V);
-  if constexpr (UNIT && sizeof(T) == 2) {
-    if (rs.chunked()) {  // per 8-logit chunk: its max and min first, indices only when they win
-      const u32x4* r4 = reinterpret_cast<const u32x4*>(rs.row);
-      const int n8 = static_cast<int>(a.V >> 3);
-#pragma unroll 8
-      for (int ch = tid; ch < n8; ch += kSampThreads) {
-        const u32x4 w = r4[ch];
-        float l[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          l[2 * e] = lo_f<T>(w[e]);
-          l[2 * e + 1] = hi_f<T>(w[e]);
-        }
-        // cmax propagates NaN (v_maximum3_f32): a chunk holding a NaN never
-        // passes cmax > mx, and records its first NaN instead.
-        float cmax = l[0], cmin = l[0], cfin = l[0] != -INFINITY ? l[0] : INFINITY;
-#pragma unroll
-        for (int e = 1; e < 8; ++e) {
-          cmax = __builtin_elementwise_maximum(cmax, l[e]);
-          cmin = fminf(cmin, l[e]);
-          cfin = fminf(cfin, l[e] != -INFINITY ? l[e] : INFINITY);
-        }
-        fmn = fminf(fmn, cfin);
-        if (cmax != cmax && inan == static_cast<int>(a.V)) {
-          int first = 7;
-#pragma unroll
-          for (int e = 7; e >= 0; --e)
-            if (l[e] != l[e]) first = e;
-          inan = 8 * ch + first;
-        }
-        if (cmax > mx) {
-          int first = 0;
-#pragma unroll
-          for (int e = 7; e >= 0; --e)
-            if (l[e] == cmax) first = e;
-          mx = cmax;
-          imx = 8 * ch + first;
-        }
-        if (cmin <= mn) {
-          int last = 7;
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (l[e] == cmin) last = e;
-          mn = cmin;
-          imn = 8 * ch + last;
-        }
+  if (split) {
+    const ChunkStats st = split_stats(a, r);
+    mx = st.mx;
+    mn = st.mn;
+    fmn = st.fmn;
+    imx = st.imx;
+    imn = st.imn;
+    inan = st.inan;
+  } else {
+    if constexpr (UNIT && sizeof(T) == 2) {
+      if (rs.chunked()) {  // per 8-logit chunk: its max and min first, indices only when they win
+        const u32x4* r4 = reinterpret_cast<const u32x4*>(rs.row);
+        const int V = static_cast<int>(a.V);
+        ChunkStats cs;
+        cs.init(V);
+        each_chunk(r4, tid, V >> 3, kSampThreads, [&](const u32x4 w, int ch) { cs.add<T>(w, ch, V); });
+        mx = cs.mx;
+        mn = cs.mn;
+        fmn = cs.fmn;
+        imx = cs.imx;
+        imn = cs.imn;
+        inan = cs.inan;
+      } else {
+        rs.each_key([&](int i, float x) {
+          if (x > mx) { mx = x; imx = i; }
+          if (x <= mn) { mn = x; imn = i; }
+          if (x != -INFINITY) fmn = fminf(fmn, x);
+          if (x != x) inan = min(inan, i);
+        });
       }
     } else {
-      rs.each_key([&](int i, float x) {
+      rs.each_key([&](int i, float x) {  // x, or for 16-bit logits the logit (same order, same ties)
         if (x > mx) { mx = x; imx = i; }
         if (x <= mn) { mn = x; imn = i; }
         if (x != -INFINITY) fmn = fminf(fmn, x);
         if (x != x) inan = min(inan, i);
       });
     }
-  } else {
-    rs.each_key([&](int i, float x) {  // x, or for 16-bit logits the logit (same order, same ties)
-      if (x > mx) { mx = x; imx = i; }
-      if (x <= mn) { mn = x; imn = i; }
-      if (x != -INFINITY) fmn = fminf(fmn, x);
-      if (x != x) inan = min(inan, i);
-    });
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    const float omx = __shfl_xor(mx, o, 64), omn = __shfl_xor(mn, o, 64), ofm = __shfl_xor(fmn, o, 64);
-    const int oimx = __shfl_xor(imx, o, 64), oimn = __shfl_xor(imn, o, 64);
-    if (omx > mx || (omx == mx && oimx < imx)) { mx = omx; imx = oimx; }
-    if (omn < mn || (omn == mn && oimn > imn)) { mn = omn; imn = oimn; }
-    fmn = fminf(fmn, ofm);
-    inan = min(inan, __shfl_xor(inan, o, 64));
-  }
-  __shared__ float red_mx[kSampWaves], red_mn[kSampWaves], red_fm[kSampWaves];
-  __shared__ int red_imx[kSampWaves], red_imn[kSampWaves], red_nan[kSampWaves];
-  if (lane == 0) {
-    red_mx[wave] = mx; red_imx[wave] = imx;
-    red_mn[wave] = mn; red_imn[wave] = imn;
-    red_fm[wave] = fmn;
-    red_nan[wave] = inan;
-  }
-  __syncthreads();
-  for (int w = 0; w < kSampWaves; ++w) {
-    if (red_mx[w] > mx || (red_mx[w] == mx && red_imx[w] < imx)) { mx = red_mx[w]; imx = red_imx[w]; }
-    if (red_mn[w] < mn || (red_mn[w] == mn && red_imn[w] > imn)) { mn = red_mn[w]; imn = red_imn[w]; }
-    fmn = fminf(fmn, red_fm[w]);
-    inan = min(inan, red_nan[w]);
+    for (int o = 32; o > 0; o >>= 1) {
+      const float omx = __shfl_xor(mx, o, 64), omn = __shfl_xor(mn, o, 64), ofm = __shfl_xor(fmn, o, 64);
+      const int oimx = __shfl_xor(imx, o, 64), oimn = __shfl_xor(imn, o, 64);
+      if (omx > mx || (omx == mx && oimx < imx)) { mx = omx; imx = oimx; }
+      if (omn < mn || (omn == mn && oimn > imn)) { mn = omn; imn = oimn; }
+      fmn = fminf(fmn, ofm);
+      inan = min(inan, __shfl_xor(inan, o, 64));
+    }
+    __shared__ float red_mx[kSampWaves], red_mn[kSampWaves], red_fm[kSampWaves];
+    __shared__ int red_imx[kSampWaves], red_imn[kSampWaves], red_nan[kSampWaves];
+    if (lane == 0) {
+      red_mx[wave] = mx; red_imx[wave] = imx;
+      red_mn[wave] = mn; red_imn[wave] = imn;
+      red_fm[wave] = fmn;
+      red_nan[wave] = inan;
+    }
+    __syncthreads();
+    for (int w = 0; w < kSampWaves; ++w) {
+      if (red_mx[w] > mx || (red_mx[w] == mx && red_imx[w] < imx)) { mx = red_mx[w]; imx = red_imx[w]; }
+      if (red_mn[w] < mn || (red_mn[w] == mn && red_imn[w] > imn)) { mn = red_mn[w]; imn = red_imn[w]; }
+      fmn = fminf(fmn, red_fm[w]);
+      inan = min(inan, red_nan[w]);
+    }
   }
   int64_t* out = a.out + r * a.out_s;
   // A row whose softmax is NaN: a NaN logit, a +inf maximum, or every logit
@@ -1333,6 +1617,7 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   const double p = a.topp[r * a.topp_s];
   const double u = a.unif[r * a.unif_s];
   int64_t token;
+  if (split) rs.srow = r;
   if (rs.fast(klo, k, cut_k, p, u, token)) {
     if (tid == 0) *out = token;
     return;
@@ -1390,9 +1675,29 @@ bool candidates_enabled() {
 }
 }  // namespace
 
-extern "C" int tsa_sample_tokens(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature,
-                                 const tsa_view* top_k, const tsa_view* top_p, const tsa_view* uniforms,
-                                 void* stream) {
+namespace {
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Segments per split row: for a batch too small to fill the device with one
+// workgroup per row, about 512 workgroups per pass (0: no split).
+int split_segments(int64_t B, int64_t V) {
+  if (B <= 0 || B > 256 || V < 16384) return 0;
+  const int64_t S = 512 / B;
+  return S < 2 ? 0 : static_cast<int>(S > kMaxSegments ? kMaxSegments : S);
+}
+
+// Workspace of a split launch: the statistics records, then the partial
+// counts and masses, each region 256-byte aligned.
+size_t split_bytes(int64_t B, int S) {
+  if (S <= 1) return 0;
+  const size_t segs = static_cast<size_t>(B) * S;
+  return align256(segs * sizeof(SplitStat)) + align256(segs * kBuckets * sizeof(uint32_t)) +
+         segs * kBuckets * sizeof(uint64_t);
+}
+
+int sample_impl(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature, const tsa_view* top_k,
+                const tsa_view* top_p, const tsa_view* uniforms, void* workspace, size_t workspace_bytes,
+                void* stream) {
   TSA_REQUIRE(view_ok(logits, 2), "Expected logits shape [B, vocab_size]");
   const int64_t B = logits->size[0], V = logits->size[1];
   TSA_REQUIRE(is_float_dtype(logits->dtype), "logits must be bf16, f16 or f32");
@@ -1417,6 +1722,32 @@ extern "C" int tsa_sample_tokens(const tsa_view* out, const tsa_view* logits, co
   a.out = static_cast<int64_t*>(out->data); a.out_s = out->stride[0];
   hipStream_t st = static_cast<hipStream_t>(stream);
   a.cand = candidates_enabled() ? 1 : 0;
+  // Split rows: 16-bit logits, rows of 16-byte aligned 8-logit chunks, a
+  // workspace, and a batch small enough (split_segments).
+  const bool rows16 = (logits->dtype == TSA_BF16 || logits->dtype == TSA_F16) && a.ls1 == 1 && (V & 7) == 0 &&
+                      (reinterpret_cast<uintptr_t>(logits->data) & 15) == 0 && ((a.ls0 * 2) & 15) == 0;
+  const int S = workspace != nullptr && rows16 ? split_segments(B, V) : 0;
+  if (S > 1) {
+    const size_t need = split_bytes(B, S);
+    TSA_REQUIRE(workspace_bytes >= need, "workspace too small: %zu bytes, need %zu (tsa_sample_tokens_workspace_bytes)",
+                workspace_bytes, need);
+    TSA_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "workspace must be 256-byte aligned");
+    const size_t segs = static_cast<size_t>(B) * S;
+    char* w = static_cast<char*>(workspace);
+    a.stat = reinterpret_cast<SplitStat*>(w);
+    a.pcnt = reinterpret_cast<uint32_t*>(w + align256(segs * sizeof(SplitStat)));
+    a.pmass = reinterpret_cast<uint64_t*>(w + align256(segs * sizeof(SplitStat)) +
+                                          align256(segs * kBuckets * sizeof(uint32_t)));
+    a.S = S;
+    const dim3 sgrid(S, B);
+    if (logits->dtype == TSA_BF16) {
+      sample_split_stats<bf16_t><<<sgrid, dim3(kSplitThreads), 0, st>>>(a);
+      sample_split_hist<bf16_t><<<sgrid, dim3(kSplitThreads), 0, st>>>(a);
+    } else {
+      sample_split_stats<f16_t><<<sgrid, dim3(kSplitThreads), 0, st>>>(a);
+      sample_split_hist<f16_t><<<sgrid, dim3(kSplitThreads), 0, st>>>(a);
+    }
+  }
   const size_t lds = sizeof(SampleLds);
   switch (logits->dtype) {
     case TSA_BF16:
@@ -1433,4 +1764,21 @@ extern "C" int tsa_sample_tokens(const tsa_view* out, const tsa_view* logits, co
       break;
   }
   return check_launch("tsa_sample_tokens");
+}
+}  // namespace
+
+extern "C" int tsa_sample_tokens(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature,
+                                 const tsa_view* top_k, const tsa_view* top_p, const tsa_view* uniforms,
+                                 void* stream) {
+  return sample_impl(out, logits, temperature, top_k, top_p, uniforms, nullptr, 0, stream);
+}
+
+extern "C" size_t tsa_sample_tokens_workspace_bytes(int64_t batch, int64_t vocab) {
+  return split_bytes(batch, split_segments(batch, vocab));
+}
+
+extern "C" int tsa_sample_tokens_ws(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature,
+                                    const tsa_view* top_k, const tsa_view* top_p, const tsa_view* uniforms,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  return sample_impl(out, logits, temperature, top_k, top_p, uniforms, workspace, workspace_bytes, stream);
 }

@@ -2,8 +2,10 @@
 (server/model/sampling.py:119-194), on the gfx950 HIP library.
 
 Same signature, argument meaning and ValueError messages. One launch samples
-every row; nothing synchronises with the host (the caller's ``.tolist()`` is
-the step's one sync, as in the reference). The kernel finds the top-k cut, the
+every row (three for a small batch of long 16-bit rows, whose statistics and
+histogram passes are spread over several workgroups per row, through a
+workspace allocated here); nothing synchronises with the host (the caller's
+``.tolist()`` is the step's one sync, as in the reference). The kernel finds the top-k cut, the
 top-p cut and the inverse-CDF pick without sorting the row; its decisions
 match the reference's sort/softmax/cumsum/searchsorted except where a target
 lies within fp32 rounding of a cumulative sum.
@@ -52,6 +54,21 @@ def sample_tokens(
         out = torch.empty(batch_size, dtype=torch.int64, device=dev)
     lib = _lib.load()
     views = [_lib.view(t) for t in (out, logits, temperature, top_k, top_p, uniforms)]
-    rc = lib.tsa_sample_tokens(*map(_lib.ref, views), _lib.stream_of(dev))
+    nbytes = _workspace_bytes(lib, *logits.shape)
+    if nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        rc = lib.tsa_sample_tokens_ws(*map(_lib.ref, views), ws.data_ptr(), nbytes, _lib.stream_of(dev))
+    else:
+        rc = lib.tsa_sample_tokens(*map(_lib.ref, views), _lib.stream_of(dev))
     _lib.check(rc, "sample_tokens")
     return out
+
+
+_WS_BYTES: dict = {}
+
+
+def _workspace_bytes(lib, batch: int, vocab: int) -> int:
+    key = (batch, vocab)
+    if key not in _WS_BYTES:
+        _WS_BYTES[key] = int(lib.tsa_sample_tokens_workspace_bytes(batch, vocab))
+    return _WS_BYTES[key]
