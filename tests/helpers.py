@@ -30,3 +30,19 @@ def assert_bitexact(out, ref, what=""):
     )
     bad = int((~same).sum())
     assert bad == 0, f"{what}: {bad} of {same.numel()} elements differ"
+
+
+def assert_within_ulps(out, ref, ulps=1, what=""):
+    """16-bit float outputs at most `ulps` units in the last place apart
+    (as ordered integers), for results of the same arithmetic summed in a
+    different order."""
+    o, r = out.detach().cpu(), ref.detach().cpu()
+    assert o.shape == r.shape and o.dtype == r.dtype and o.element_size() == 2, what
+
+    def ordered(t):
+        i = t.view(torch.int16).to(torch.int32)
+        return torch.where(i < 0, -(i & 0x7FFF), i)  # sign-magnitude -> ordered (+0 and -0 meet at 0)
+
+    d = (ordered(o) - ordered(r)).abs()
+    print(f"{what}: {int((d > 0).sum())} of {d.numel()} elements differ, at most {int(d.max())} ulp", flush=True)
+    assert int(d.max()) <= ulps, f"{what}: {int(d.max())} ulp apart (<= {ulps})"

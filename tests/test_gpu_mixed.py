@@ -22,8 +22,10 @@ Checked, for every sequence and every head:
 The same step as an engine batching both would issue it -- one norm/RoPE/
 store over the tokens of both batches, then both attentions in one launch
 (``mixed_attention``) -- gives every output, the rotated q/k and both caches
-bit-identical to the scheduler-order step above, and so passes the oracle
-checks too; small cases cover the two-launch fallback (2 q-heads per kv
+bit-identical to the scheduler-order step above (the prefill output within
+one bf16 ulp where the scheduler-order step's prefill takes
+varlen_prefill_w64, which sums in another order than the one launch's
+varlen_prefill_gqa body), and passes the oracle checks too; small cases cover the two-launch fallback (2 q-heads per kv
 head) and prefill workgroup counts below and above what is resident.
 """
 
@@ -34,7 +36,7 @@ from oracle import kv_store as ok
 from oracle import norm_rope as onr
 from oracle import paged as op
 from oracle import varlen as ov
-from tests.helpers import assert_bitexact, assert_close
+from tests.helpers import assert_bitexact, assert_close, assert_within_ulps
 from tinyserver_amd import workloads as W
 from tinyserver_amd.kernels import flash_attn_varlen_func, mixed_attention, paged_attention_forward, qk_norm_rope_store
 
@@ -159,7 +161,13 @@ def _packed(gp, gd):
 def _two_vs_one(cpu, **kw):
     """The step in scheduler order (two stores, two attention launches) and
     as one store + one attention launch; every output, the rotated q/k and
-    both caches must match bit for bit. Returns the one-launch outputs."""
+    both caches must match bit for bit -- except the prefill output of a
+    group of 4 q-heads per kv head at head_dim 128, which the scheduler-order
+    step computes with varlen_prefill_w64 and the one launch with
+    varlen_prefill_gqa's body: the same arithmetic summed in another order,
+    within one bf16 ulp. Returns the one-launch outputs."""
+    gp0 = cpu.prefill
+    w64 = (gp0.q.shape[1] // gp0.k.shape[1]) % 4 == 0 and gp0.q.shape[2] == 128
     runs = {}
     for mode in ("two", "one"):
         g = cpu.to(DEV)
@@ -189,7 +197,11 @@ def _two_vs_one(cpu, **kw):
         torch.cuda.empty_cache()
     names = ("prefill output", "decode output", "rotated q", "rotated k", "k_cache", "v_cache")
     for name, a, b in zip(names, runs["two"], runs["one"]):
-        assert_bitexact(b, a, f"one store + one attention launch vs scheduler order: {name}")
+        what = f"one store + one attention launch vs scheduler order: {name}"
+        if name == "prefill output" and w64:
+            assert_within_ulps(b, a, 1, what)
+        else:
+            assert_bitexact(b, a, what)
     return runs["one"]
 
 
