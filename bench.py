@@ -395,7 +395,7 @@ def bench_prefill(name, steps, warmup):
         "us_per_call_p90": spread["p90"], "tflops": flops / (us * 1e-6) / 1e12,
         "pct_peak_mfma": 100.0 * flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
         "tokens_per_s": T / (us * 1e-6),
-        "roofline": {**_roof_mfma(flops, us), "kernel": "varlen_prefill_gqa"},
+        "roofline": {**_roof_mfma(flops, us), "kernel": _prefill_kernel(w.q.shape[1] // w.k.shape[1], w.q.shape[2])},
         "norm_rope_store_us": ns_us, "norm_rope_store_us_median": ns_spread["median"],
         "norm_rope_store_us_p10": ns_spread["p10"], "norm_rope_store_us_p90": ns_spread["p90"],
         "norm_rope_store_gbs": ns_bytes / (ns_us * 1e-6) / 1e9,
@@ -588,6 +588,14 @@ def bench_sampling(steps, warmup, batch=64, vocab=151936, copies=16):
     del pool
     return {"workload": f"sample_tokens bs{batch} vocab{vocab} bf16", "batch": batch, "vocab": vocab,
             "logits_copies": copies, **cases}, (logits, temperature, top_k, top_p, uniforms)
+
+
+def _prefill_kernel(group, head_dim):
+    """The kernel tsa_varlen_prefill runs for bf16 rows of this GQA group and
+    head_dim (varlen_prefill.hip: takes_w64, then takes_gqa)."""
+    if head_dim == 128 and group % 4 == 0 and os.environ.get("TSA_PREFILL_W64", "1")[:1] != "0":
+        return "varlen_prefill_w64"
+    return "varlen_prefill_gqa" if group in (2, 4, 8) else "varlen_prefill_mfma"
 
 
 def _graph_us_per_call(fn, steps, warmup, calls=20):
