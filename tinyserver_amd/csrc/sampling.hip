@@ -102,6 +102,7 @@ __device__ __forceinline__ void each_chunk(const u32x4* r4, int first, int end, 
       const int ch = base + j * step;
       w[j] = ch < end ? r4[ch] : u32x4{0, 0, 0, 0};
     }
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first use
 #pragma unroll
     for (int j = 0; j < kLoadBatch; ++j) {
       const int ch = base + j * step;
@@ -1119,13 +1120,19 @@ struct RowSampler {
         uint32_t c = 0;
         uint64_t m = 0;
         // (every load issued, at a clamped segment, before any is summed)
+        uint32_t cw[kMaxSegments];
+        uint64_t mw[kMaxSegments];
 #pragma unroll
         for (int w = 0; w < kMaxSegments; ++w) {
           const size_t at = base + static_cast<size_t>(min(w, a.S - 1)) * kBuckets + b;
-          const uint32_t cw = a.pcnt[at];
-          const uint64_t mw = a.pmass[at];
-          c += w < a.S ? cw : 0u;
-          m += w < a.S ? mw : uint64_t{0};
+          cw[w] = a.pcnt[at];
+          mw[w] = a.pmass[at];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int w = 0; w < kMaxSegments; ++w) {
+          c += w < a.S ? cw[w] : 0u;
+          m += w < a.S ? mw[w] : uint64_t{0};
         }
         s.cnt[b] = c;
         s.wsum[b] = m;
@@ -1435,11 +1442,16 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_stats(SampleArgs a
 
 // The merged statistics of split row r (its S records).
 __device__ __forceinline__ ChunkStats split_stats(const SampleArgs& a, int64_t r) {
+  // Every record loaded (at a clamped segment: merging a record twice
+  // changes nothing) before the first merge.
+  SplitStat rec[kMaxSegments];
+#pragma unroll
+  for (int w = 0; w < kMaxSegments; ++w) rec[w] = a.stat[r * a.S + min(w, a.S - 1)];
+  __builtin_amdgcn_sched_barrier(0);
   ChunkStats st;
   st.init(static_cast<int>(a.V));
 #pragma unroll
-  for (int w = 0; w < kMaxSegments; ++w)
-    if (w < a.S) st.merge(a.stat[r * a.S + w]);
+  for (int w = 0; w < kMaxSegments; ++w) st.merge(rec[w]);
   return st;
 }
 
