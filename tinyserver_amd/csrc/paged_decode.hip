@@ -714,15 +714,16 @@ __global__ __launch_bounds__(kPrefixThreads) void decode_tile_prefix(DecodeArgs 
 // the wave workers v whose tiles cover unit (s, kvh); an empty sequence gives
 // 0/0 = NaN, as the reference's does. One workgroup per unit, one thread per
 // (head, dim) output (head_dim * G <= 2048 outputs over 256 threads). The
-// contributors are combined with an online log-sum-exp in batches of 4 whose
-// loads are all issued before any is used, so a unit costs a few memory
-// round trips however many waves covered it. A batch past the last
-// contributor repeats its loads, so batches are sized for the usual 2 to 5
-// contributors (batches of 8 measured 0.8 us slower per Qwen3-8B batch-64
-// call; the combine order, and so the result, is the same).
+// contributors are combined in order with an online log-sum-exp, in batches
+// whose loads are all issued before any is used, so a unit costs a few
+// memory round trips however many waves covered it. A batch past the last
+// contributor repeats its loads and weighs them by exactly 0 (scale 2^0 on
+// the sum, 2^-inf on the repeat), so the batch size leaves the result
+// unchanged. Batches of 4 suit the usual 2 to 5 contributors (batches of 8
+// measured 0.8 us slower per Qwen3-8B batch-64 call); a unit of more
+// contributors takes batches of 16.
 template <typename T, int kOut>  // kOut: outputs per thread, G * head_dim / 256 rounded up
 __global__ __launch_bounds__(256) void paged_decode_stream_merge(DecodeArgs a) {
-  constexpr int kBatch = 4;  // contributors per batch
   const int u = blockIdx.x, tid = threadIdx.x;
   const int Hkv = a.Hkv, G = a.G, D = a.D;
   const int s = u / Hkv, kvh = u - s * Hkv;
@@ -750,30 +751,41 @@ __global__ __launch_bounds__(256) void paged_decode_stream_merge(DecodeArgs a) {
     den[i] = 0.f;
     o[i] = 0.f;
   }
-  for (int v = v0; v <= v1; v += kBatch) {
-    float mb[kBatch][kOut], lb[kBatch][kOut], ab[kBatch][kOut];
+  auto combine = [&](auto batch) {
+    constexpr int kBatch = decltype(batch)::value;  // contributors per batch
+    for (int v = v0; v <= v1; v += kBatch) {
+      float mb[kBatch][kOut], lb[kBatch][kOut], ab[kBatch][kOut];
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const float* sl = base + static_cast<int64_t>(min(v + k, v1)) * slot_floats;
+      for (int k = 0; k < kBatch; ++k) {
+        const float* sl = base + static_cast<int64_t>(min(v + k, v1)) * slot_floats;
 #pragma unroll
-      for (int i = 0; i < kOut; ++i) {
-        const int idx = min(tid + 256 * i, nout - 1);
-        mb[k][i] = v + k <= v1 ? sl[G * D + hd[i]] : kNegInf;
-        lb[k][i] = sl[G * D + G + hd[i]];
-        ab[k][i] = sl[idx];
+        for (int i = 0; i < kOut; ++i) {
+          const int idx = min(tid + 256 * i, nout - 1);
+          mb[k][i] = v + k <= v1 ? sl[G * D + hd[i]] : kNegInf;
+          lb[k][i] = sl[G * D + G + hd[i]];
+          ab[k][i] = sl[idx];
+        }
       }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k)
+#pragma unroll
+        for (int i = 0; i < kOut; ++i) {
+          const float mn = fmaxf(M[i], mb[k][i]);
+          if (mn == kNegInf) continue;
+          const float c_old = fast_exp2(M[i] - mn), c_new = fast_exp2(mb[k][i] - mn);
+          o[i] = o[i] * c_old + ab[k][i] * c_new;
+          den[i] = den[i] * c_old + lb[k][i] * c_new;
+          M[i] = mn;
+        }
     }
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k)
-#pragma unroll
-      for (int i = 0; i < kOut; ++i) {
-        const float mn = fmaxf(M[i], mb[k][i]);
-        if (mn == kNegInf) continue;
-        const float c_old = fast_exp2(M[i] - mn), c_new = fast_exp2(mb[k][i] - mn);
-        o[i] = o[i] * c_old + ab[k][i] * c_new;
-        den[i] = den[i] * c_old + lb[k][i] * c_new;
-        M[i] = mn;
-      }
+  };
+  // Many contributors (small batches: a wave per tile or two) in batches of
+  // 16, so a unit of up to 16 one-tile partials costs one round trip.
+  if constexpr (kOut <= 2) {
+    if (v1 - v0 >= 4) combine(std::integral_constant<int, 16>{});
+    else combine(std::integral_constant<int, 4>{});
+  } else {
+    combine(std::integral_constant<int, 4>{});
   }
 #pragma unroll
   for (int i = 0; i < kOut; ++i) {
