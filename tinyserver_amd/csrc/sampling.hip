@@ -419,21 +419,48 @@ struct RowSampler {
     __syncthreads();
   }
 
-  // Bitonic sort of s.keys[0, n) ascending, padded to a power of two.
+  // s.keys[0, n) sorted ascending: up to one key per thread as below, more
+  // by a bitonic network in LDS padded to a power of two.
   __device__ __forceinline__ void sort_keys(int n) {
-    if (n <= 512) {
-      // Few keys (a bucket of tied or close logits): each of the first n
-      // threads counts the keys below its own -- the keys are distinct (they
-      // hold the index) -- and writes it to that rank: two barriers instead
-      // of the bitonic network's one per stage.
-      uint64_t mine = 0;
-      int rank = 0;
-      if (tid < n) {
-        mine = s.keys[tid];
-        for (int j = 0; j < n; ++j) rank += s.keys[j] < mine ? 1 : 0;
+    if (n <= kSampThreads) {
+      // At most one key per thread: each wave sorts its 64 (a bitonic
+      // network on lane shuffles; ~0, above every rank key, pads the last
+      // run), the sorted runs go to LDS, and a key's place is its lane plus
+      // the keys below it in every other run (a binary search of each run,
+      // the runs' searches interleaved). The keys are distinct (they hold
+      // the index).
+      const int runs = (n + 63) >> 6;
+      uint64_t x = tid < n ? s.keys[tid] : ~uint64_t{0};
+      if (wave < runs) {
+#pragma unroll
+        for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+          for (int j = k >> 1; j > 0; j >>= 1) {
+            const uint64_t y = __shfl_xor(x, j, 64);
+            const bool keep_min = ((lane & j) == 0) == ((lane & k) == 0);
+            x = keep_min == (x < y) ? x : y;
+          }
       }
       __syncthreads();
-      if (tid < n) s.keys[rank] = mine;
+      if (wave < runs) s.keys[tid] = x;
+      __syncthreads();
+      int rank = lane;
+      if (wave < runs) {
+        for (int g = 0; g < runs; g += 4) {  // four runs' searches at a time
+          int below[4] = {0, 0, 0, 0};
+#pragma unroll
+          for (int step = 32; step > 0; step >>= 1)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (g + i < runs && g + i != wave && s.keys[64 * (g + i) + below[i] + step - 1] < x) below[i] += step;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)  // (the steps reach 63 keys: the 64th decides alone)
+            if (g + i < runs && g + i != wave && s.keys[64 * (g + i) + below[i]] < x) ++below[i];
+          rank += below[0] + below[1] + below[2] + below[3];
+        }
+      }
+      __syncthreads();
+      if (wave < runs && x != ~uint64_t{0}) s.keys[rank] = x;
       __syncthreads();
       return;
     }
