@@ -203,6 +203,27 @@ def test_workspace_plan():
     assert lib.tsa_paged_decode_workspace_bytes(0, 8, 2, 128, 64, 16, 10) == 0
 
 
+def test_workspace_plan_small_tables():
+    """With no grid asked for, block tables of few tiles (Hkv * B *
+    ceil(max_blocks * block_size / 16), at most 8 per default workgroup)
+    take a grid of one workgroup per 8 such tiles, at least 64: the
+    workspace holds units + 4 * workgroups partial slots."""
+    lib = _lib.load()
+
+    def plan(b, blocks, bs=16, nwg=0):
+        return lib.tsa_paged_decode_workspace_bytes(b, 16, 8, 128, blocks, bs, nwg)
+
+    def size(b, wg):  # G = 2, head_dim 128
+        align = lambda n: (n + 255) // 256 * 256
+        return align((b * 8 + 4 * wg) * 2 * (128 + 2) * 4) + align((b + 1) * 4)
+
+    assert plan(4, 32) == size(4, 128)  # 1024 tiles: the Qwen3-0.6B batch of 4 at contexts up to 512
+    assert plan(4, 16, bs=32) == size(4, 128)  # the same tokens in 32-token pages
+    assert plan(4, 1) == size(4, 64)  # 32 tiles: the floor of 64 workgroups
+    assert plan(4, 32, nwg=200) == size(4, 200)  # a grid asked for is kept
+    assert plan(64, 256) > size(64, 128)  # the Qwen3-8B batch: the default grid (one per CU)
+
+
 def test_sampling_workspace_plan():
     lib = _lib.load()
     # Split rows: 512 / B segments per row (2 .. 16), each a 32-byte

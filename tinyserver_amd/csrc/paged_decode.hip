@@ -880,9 +880,23 @@ struct DecodePlan {
 
 // Workspace: one partial slot per (unit, wave worker) pair that can occur --
 // units * 1 + workers, since slot = unit + worker -- and the tile prefix.
-static DecodePlan make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int32_t num_workgroups) {
+// With no grid asked for, a batch whose block tables hold few tiles (at
+// most 8 per workgroup of the default grid, Hkv * B * ceil(max_blocks *
+// block_size / 16) -- a bound the host knows without reading seq_lens)
+// takes a grid of about two tiles per wave worker, but at least kMinAutoWG
+// workgroups: fewer workers leave fewer partials per unit for the merge
+// (Qwen3-0.6B batch of 4, 1024-tile tables: 11.5 us replayed at 128
+// workgroups against 12.6 at 256; a 56-tile batch 10.7 us at any grid).
+constexpr int kMinAutoWG = 64;
+static DecodePlan make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_blocks, int64_t BS,
+                            int32_t num_workgroups) {
   DecodePlan p{};
   p.W = num_workgroups > 0 ? num_workgroups : default_workgroups();
+  if (num_workgroups == 0) {
+    const int64_t cap_tiles = Hkv * B * ((max_blocks * BS + 15) / 16);
+    const int64_t want = (cap_tiles + 2 * kWaves - 1) / (2 * kWaves);
+    if (want < p.W) p.W = static_cast<int>(want < kMinAutoWG ? kMinAutoWG : want);
+  }
   const int64_t G = Hq / Hkv;
   const int64_t slots = B * Hkv + static_cast<int64_t>(kWaves) * p.W;
   p.part_bytes = align256(static_cast<size_t>(slots) * G * (D + 2) * sizeof(float));
@@ -968,10 +982,8 @@ using namespace tsa;
 extern "C" size_t tsa_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads,
                                                    int64_t head_dim, int64_t max_blocks_per_seq, int64_t block_size,
                                                    int32_t num_workgroups) {
-  (void)max_blocks_per_seq;
-  (void)block_size;
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || num_heads % num_kv_heads) return 0;
-  return make_plan(num_seqs, num_heads, num_kv_heads, head_dim, num_workgroups).total;
+  return make_plan(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size, num_workgroups).total;
 }
 
 namespace tsa {
@@ -1028,7 +1040,7 @@ static int check_decode(const tsa_view* out, const tsa_view* query, const tsa_vi
          rows_vec16(k_cache) && rows_vec16(v_cache) && out->stride[2] == 1;
   plan = DecodePlan{};
   if (mfma) {
-    plan = make_plan(B, Hq, Hkv, D, num_workgroups);
+    plan = make_plan(B, Hq, Hkv, D, block_tables->size[1], BS, num_workgroups);
     a.W = plan.W;
     a.NW = kWaves * plan.W;
   }
