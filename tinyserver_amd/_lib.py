@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import struct
-from ctypes import POINTER, c_double, c_int, c_int32, c_int64, c_size_t, c_void_p
+from ctypes import c_double, c_int, c_int32, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 import torch
@@ -37,7 +37,10 @@ class TsaView(ctypes.Structure):
     ]
 
 
-_V = POINTER(TsaView)
+# A view argument: the address of a tsa_view. view() hands over the packed
+# bytes themselves (ctypes passes a bytes object's buffer as the pointer,
+# valid for the call); a TsaView passed by ctypes.byref works too.
+_V = c_void_p
 
 # name -> (restype, argtypes); mirrors include/tsa_api.h.
 SIGNATURES = {
@@ -101,8 +104,9 @@ _PACK = [struct.Struct("<Q" + "q" * nd + "x" * (8 * (4 - nd)) + "q" * nd + "x" *
          for nd in range(5)]
 
 
-def view(t: torch.Tensor | None) -> TsaView | None:
-    """Describe a tensor for the C ABI (None stays None -> NULL)."""
+def view(t: torch.Tensor | None) -> bytes | None:
+    """Describe a tensor for the C ABI: the tsa_view struct's bytes (None
+    stays None -> NULL)."""
     if t is None:
         return None
     nd = t.dim()
@@ -111,11 +115,12 @@ def view(t: torch.Tensor | None) -> TsaView | None:
     dt = _DTYPES.get(t.dtype)
     if dt is None:
         raise ValueError(f"unsupported dtype {t.dtype}")
-    return TsaView.from_buffer_copy(_PACK[nd].pack(t.data_ptr() if t.numel() else 0, *t.shape, *t.stride(), nd, dt))
+    return _PACK[nd].pack(t.data_ptr() if t.numel() else 0, *t.shape, *t.stride(), nd, dt)
 
 
-def ref(v: TsaView | None):
-    return ctypes.byref(v) if v is not None else None
+def ref(v: bytes | None):
+    """The argument for a view (its bytes; ctypes passes their address)."""
+    return v
 
 
 def check(rc: int, what: str) -> None:

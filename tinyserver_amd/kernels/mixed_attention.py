@@ -18,7 +18,7 @@ import math
 import torch
 
 from .. import _lib
-from .paged_attention import _workspace
+from .paged_attention import _workspace, _ws_bytes
 
 
 def mixed_attention(
@@ -84,8 +84,8 @@ def mixed_attention(
     num_seqs, num_heads, head_dim = query.shape
     lib = _lib.load()
     stream = _lib.stream_of(dev)
-    nbytes = int(lib.tsa_paged_decode_workspace_bytes(num_seqs, num_heads, k_cache.shape[1], head_dim,
-                                                      block_tables.shape[1], k_cache.shape[2], num_workgroups))
+    nbytes = _ws_bytes(dev, num_seqs, num_heads, k_cache.shape[1], head_dim, block_tables.shape[1], k_cache.shape[2],
+                       int(num_workgroups))
     ws = _workspace(dev, stream, nbytes)
     vp = [_lib.view(t) for t in (prefill_out, prefill_q, prefill_k, prefill_v, cu_seqlens)]
     vd = [_lib.view(t) for t in (out, query, k_cache, v_cache, block_tables, seq_lens)]

@@ -37,6 +37,19 @@ def decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim, max_bloc
                                                     block_size, num_workgroups))
 
 
+_WS_BYTES: dict[tuple, int] = {}
+
+
+def _ws_bytes(device: torch.device, *shape) -> int:
+    """tsa_paged_decode_workspace_bytes for a call shape, cached per device
+    (the default grid depends on the device's CU count)."""
+    key = (device.index, *shape)
+    n = _WS_BYTES.get(key)
+    if n is None:
+        n = _WS_BYTES[key] = int(_lib.load().tsa_paged_decode_workspace_bytes(*shape))
+    return n
+
+
 def paged_attention_forward(
     query: torch.Tensor,
     k_cache: torch.Tensor,
@@ -77,8 +90,8 @@ def paged_attention_forward(
     softmax_scale = 1.0 / math.sqrt(head_dim)
     lib = _lib.load()
     stream = _lib.stream_of(dev)
-    nbytes = int(lib.tsa_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim,
-                                                      block_tables.shape[1], k_cache.shape[2], num_workgroups))
+    nbytes = _ws_bytes(dev, num_seqs, num_heads, num_kv_heads, head_dim, block_tables.shape[1], k_cache.shape[2],
+                       int(num_workgroups))
     ws = _workspace(dev, stream, nbytes)
     views = [_lib.view(t) for t in (out, query, k_cache, v_cache, block_tables, seq_lens)]
     rc = lib.tsa_paged_decode(
@@ -131,8 +144,8 @@ def paged_decode_step(
         out = torch.empty_like(q)
     lib = _lib.load()
     stream = _lib.stream_of(dev)
-    nbytes = int(lib.tsa_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim,
-                                                      block_tables.shape[1], k_cache.shape[2], num_workgroups))
+    nbytes = _ws_bytes(dev, num_seqs, num_heads, num_kv_heads, head_dim, block_tables.shape[1], k_cache.shape[2],
+                       int(num_workgroups))
     ws = _workspace(dev, stream, nbytes)
     v8 = [_lib.view(t) for t in (out, q, k, v, q_weight, k_weight, cos, sin)]
     v4 = [_lib.view(t) for t in (k_cache, v_cache, block_tables, seq_lens)]
