@@ -894,7 +894,7 @@ static DecodePlan make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64
   p.W = num_workgroups > 0 ? num_workgroups : default_workgroups();
   constexpr int64_t k31 = int64_t(1) << 31;
   if (num_workgroups == 0 && max_blocks > 0 && BS > 0 && max_blocks < k31 && BS < k31 && max_blocks * BS < k31 &&
-      B * Hkv < k31) {
+      B < k31 && Hkv < k31 && B * Hkv < k31) {
     const int64_t cap_tiles = Hkv * B * ((max_blocks * BS + 15) / 16);
     const int64_t want = (cap_tiles + 2 * kWaves - 1) / (2 * kWaves);
     if (want < p.W) p.W = static_cast<int>(want < kMinAutoWG ? kMinAutoWG : want);
