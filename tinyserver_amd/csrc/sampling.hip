@@ -283,7 +283,7 @@ struct SampleLds {
   float wave_f[kSampWaves];
   int64_t wave_i[kSampWaves];
   uint32_t n_gather;
-  int found_bucket;
+  int found_bucket, found_bucket2;
   uint64_t found_cum;
   int64_t found_index;
   float found_x;
@@ -540,28 +540,37 @@ struct RowSampler {
     }
     return lo;
   }
-  // Every element whose 16-bit key lies in [klo, khi] into s.keys (as a rank
-  // key), for a chunked 16-bit row: per 8-logit chunk, packed 16-bit keys,
-  // their offsets from klo and the offsets' minimum tell in a few
-  // instructions whether any key of the chunk is in the range; only such
-  // chunks are looked into.
-  __device__ __forceinline__ void gather_key_range(uint32_t klo, uint32_t khi) {
+  // Every element whose 16-bit key lies in [klo, khi] (or in [klo2, khi2]
+  // too: TWO) into s.keys (as a rank key), for a chunked 16-bit row: per
+  // 8-logit chunk, packed 16-bit keys, their offsets from klo and the
+  // offsets' minimum tell in a few instructions whether any key of the
+  // chunk is in range; only such chunks are looked into. (Reserving a
+  // wave's matches with one atomic after a wave prefix of the lanes' counts
+  // measured slower: the gather is bound by its instructions, not the
+  // atomics' latency.)
+  template <bool TWO = false>
+  __device__ __forceinline__ void gather_key_range(uint32_t klo, uint32_t khi, uint32_t klo2 = 0, uint32_t khi2 = 0) {
     const uint32_t span = khi - klo, lo2 = klo | (klo << 16);
+    const uint32_t span2 = khi2 - klo2, lo22 = klo2 | (klo2 << 16);
     each_chunk(reinterpret_cast<const u32x4*>(row), tid, static_cast<int>(a.V >> 3), kSampThreads,
                [&](const u32x4 w, int ch) {
-                 uint32_t k[4], m = 0xFFFFFFFFu;
+                 uint32_t k[4], m = 0xFFFFFFFFu, m2 = 0xFFFFFFFFu;
 #pragma unroll
                  for (int e = 0; e < 4; ++e) {
                    k[e] = pk_key(w[e]);
                    // key - klo in each half, mod 2^16: a key below klo wraps above span
                    m = pk_min(m, __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, k[e]) -
                                                                   __builtin_bit_cast(u16x2, lo2)));
+                   if constexpr (TWO)
+                     m2 = pk_min(m2, __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, k[e]) -
+                                                                      __builtin_bit_cast(u16x2, lo22)));
                  }
-                 if (min(m & 0xFFFFu, m >> 16) > span) return;  // no key of the chunk in range
+                 const bool none = min(m & 0xFFFFu, m >> 16) > span;
+                 if (TWO ? none && min(m2 & 0xFFFFu, m2 >> 16) > span2 : none) return;  // no key of the chunk in range
 #pragma unroll
                  for (int e = 0; e < 8; ++e) {
                    const uint32_t key = (k[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-                   if (key - klo <= span) {
+                   if (key - klo <= span || (TWO && key - klo2 <= span2)) {
                      const uint32_t at = atomicAdd(&s.n_gather, 1u);
                      if (at < kCap)
                        s.keys[at] = rank_key((e & 1) ? hi_f<T>(w[e >> 1]) : lo_f<T>(w[e >> 1]), 8 * ch + e);
@@ -654,9 +663,11 @@ struct RowSampler {
   // Over the first `limit` sorted elements, with `base` before them: the
   // position of the one element that reaches the target (see select), its
   // running mass through it, and the mass of all `limit` elements.
-  __device__ __forceinline__ int scan_sorted(int limit, uint64_t base, bool ge, double target, uint64_t& cum_at, uint64_t& total) {
+  __device__ __forceinline__ int scan_sorted(int limit, uint64_t base, bool ge, double target, uint64_t& cum_at,
+                                             uint64_t& total, int off = 0) {
+    // (elements keys[off, off + limit); the position returned is relative to off)
     const int per = (limit + kSampThreads - 1) / kSampThreads;
-    const int e0 = min(limit, tid * per), e1 = min(limit, e0 + per);
+    const int e0 = off + min(limit, tid * per), e1 = off + min(limit, tid * per + per);
     uint64_t mine = 0;
     for (int e = e0; e < e1; ++e) mine += mass_key(key_of_rank(s.keys[e]));  // no reload of the row
     uint64_t incl = mine;
@@ -677,8 +688,8 @@ struct RowSampler {
       cum += mass_key(key_of_rank(s.keys[e]));
       const bool r = ge ? static_cast<double>(cum) >= target : static_cast<double>(cum) > target;
       const bool rx = ge ? static_cast<double>(excl) >= target : static_cast<double>(excl) > target;
-      if (r && (e == 0 || !rx)) {
-        s.found_index = e;
+      if (r && (e == off || !rx)) {
+        s.found_index = e - off;
         s.found_cum = cum;
         break;
       }
@@ -1138,6 +1149,70 @@ struct RowSampler {
   // then a known prefix of one sorted bucket -- so only the buckets where a
   // cut or the pick falls are gathered. False if such a bucket is larger
   // than LDS holds (the caller then runs the per-decision path).
+  // A top-p cut in bucket bp (no top-k cut) and the pick from one gather of
+  // the row. The kept mass lies in [pmass[bp], pmass[bp] + wsum[bp]]:
+  // whole buckets before bp, then a prefix of bp. The pick bucket is the
+  // first non-empty bucket whose running mass reaches u * (kept mass), bp's
+  // own running mass being the kept mass (which u < 1 reaches), so it lies
+  // between the buckets that u times either end reaches (blo and bhi; a
+  // larger target never reaches an earlier bucket), or is bp. The buckets
+  // blo .. min(bhi, bp - 1) and bp are gathered in one pass (two key
+  // ranges) and sorted together (rank order: the earlier buckets first),
+  // and the cut and the pick are the scans the two-gather path makes, on the
+  // same sorted elements. False (nothing decided) when they exceed one key
+  // per thread, or the gathered count is not the histogram's.
+  __device__ __forceinline__ bool cut_and_pick(int bp, uint64_t z, double p, double u, float scale, int64_t& token) {
+    const double tlo = u * static_cast<double>(s.pmass[bp]);
+    const double thi = u * static_cast<double>(s.pmass[bp] + s.wsum[bp]);
+    if (tid == 0) {
+      s.found_bucket = bp;
+      s.found_bucket2 = bp;
+    }
+    __syncthreads();
+    for (int b = tid; b < bp; b += kSampThreads) {
+      if (s.cnt[b] == 0) continue;
+      const double incl = static_cast<double>(s.pmass[b] + s.wsum[b]);
+      if (incl >= tlo) atomicMin(&s.found_bucket, b);
+      if (incl >= thi) atomicMin(&s.found_bucket2, b);
+    }
+    __syncthreads();
+    const int blo = s.found_bucket, last = min(s.found_bucket2, bp - 1);
+    __syncthreads();
+    const uint32_t n_u = blo <= last ? s.pcnt[last] + s.cnt[last] - s.pcnt[blo] : 0u;  // elements of blo .. last
+    const uint32_t n = n_u + s.cnt[bp];
+    if (n > static_cast<uint32_t>(kSampThreads)) return false;
+    // bucket b holds the keys [first_key_at_most(b), first_key_at_most(b - 1)), bucket 0 up to +inf
+    auto key_end = [&](int b) { return b > 0 ? first_key_at_most(b - 1, scale) - 1 : Inf16<T>::kPosKey; };
+    const uint32_t kb_lo = first_key_at_most(bp, scale), kb_hi = key_end(bp);
+    if (tid == 0) s.n_gather = 0;
+    __syncthreads();
+    if (blo > last) gather_key_range(kb_lo, kb_hi);
+    else if (last + 1 == bp) gather_key_range(kb_lo, key_end(blo));  // adjacent: one range
+    else gather_key_range<true>(kb_lo, kb_hi, first_key_at_most(last, scale), key_end(blo));
+    __syncthreads();
+    if (s.n_gather != n) return false;  // (the histogram's own counts: never expected to differ)
+    sort_keys(static_cast<int>(n));
+    uint64_t cum, tot;
+    const int pos = scan_sorted(static_cast<int>(s.cnt[bp]), s.pmass[bp], false, p * static_cast<double>(z), cum,
+                                tot, static_cast<int>(n_u));
+    if (pos < 0) return false;
+    const uint64_t kept = cum;
+    const double tu = u * static_cast<double>(kept);
+    int bu = bp;
+    for (int b = blo; b <= last; ++b)
+      if (s.cnt[b] > 0 && static_cast<double>(s.pmass[b] + s.wsum[b]) >= tu) {
+        bu = b;
+        break;
+      }
+    const int lim = bu == bp ? pos + 1 : static_cast<int>(s.cnt[bu]);
+    const int off = bu == bp ? static_cast<int>(n_u) : static_cast<int>(s.pcnt[bu] - s.pcnt[blo]);
+    const int pos2 = scan_sorted(lim, s.pmass[bu], true, tu, cum, tot, off);
+    if (pos2 < 0) return false;
+    token = static_cast<uint32_t>(s.keys[off + pos2]);
+    __syncthreads();
+    return true;
+  }
+
   __device__ __forceinline__ bool fast(float lo, int64_t k, bool cut_k, double p, double u, int64_t& token) {
     // lo: the smallest finite key
     const float scale = kmax > lo ? static_cast<float>(kBuckets - 1) / (kmax - lo) : 0.f;
@@ -1211,6 +1286,9 @@ struct RowSampler {
       if (!gather_prefix(bp, scale)) return false;
       token = decide_on_prefix(static_cast<int>(s.pcnt[bp] + s.cnt[bp]), -1, true, z, p, u);
       return token >= 0;
+    }
+    if constexpr (UNIT && sizeof(T) == 2) {
+      if (!cut_k && bp < kBuckets && chunked() && cut_and_pick(bp, z, p, u, scale, token)) return true;
     }
     if (bp < kBuckets) {
       if (s.cnt[bp] > kCap) return false;
