@@ -511,6 +511,42 @@ struct RowSampler {
     __syncthreads();
   }
 
+  // Both exclusive prefixes of the shared histogram, cnt into pcnt and wsum
+  // into pmass, with one set of barriers (the sums of scan2, together).
+  __device__ __forceinline__ void scan2_hist() {
+    const uint32_t c0 = s.cnt[2 * tid], c1 = s.cnt[2 * tid + 1];
+    const uint64_t m0 = s.wsum[2 * tid], m1 = s.wsum[2 * tid + 1];
+    int64_t ic = static_cast<int64_t>(c0) + c1;
+    uint64_t im = m0 + m1;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t upc = __shfl_up(ic, o, 64);
+      const uint64_t upm = __shfl_up(im, o, 64);
+      if (lane >= o) {
+        ic += upc;
+        im += upm;
+      }
+    }
+    __syncthreads();
+    if (lane == 63) {
+      s.wave_i[wave] = ic;
+      s.wave_u64[wave] = im;
+    }
+    __syncthreads();
+    int64_t bc = 0;
+    uint64_t bm = 0;
+    for (int w = 0; w < wave; ++w) {
+      bc += s.wave_i[w];
+      bm += s.wave_u64[w];
+    }
+    const int64_t ec = bc + ic - (static_cast<int64_t>(c0) + c1);
+    const uint64_t em = bm + im - (m0 + m1);
+    s.pcnt[2 * tid] = static_cast<uint32_t>(ec);
+    s.pcnt[2 * tid + 1] = static_cast<uint32_t>(ec + c0);
+    s.pmass[2 * tid] = em;
+    s.pmass[2 * tid + 1] = em + m0;
+    __syncthreads();
+  }
+
   // The smallest non-empty bucket b <= last whose running mass through b
   // (the full bucket, or last_incl for bucket `last`) reaches the target.
   __device__ __forceinline__ int first_bucket(int last, uint64_t last_incl, bool ge, double target) {
@@ -1221,20 +1257,23 @@ struct RowSampler {
       for (int b = tid; b < kBuckets; b += kSampThreads) {
         uint32_t c = 0;
         uint64_t m = 0;
-        // (every load issued, at a clamped segment, before any is summed)
-        uint32_t cw[kMaxSegments];
-        uint64_t mw[kMaxSegments];
+        // Eight segments per step, every load (at a clamped segment) issued
+        // before any is summed: one step for the usual 8 segments.
+        for (int w0 = 0; w0 < a.S; w0 += 8) {
+          uint32_t cw[8];
+          uint64_t mw[8];
 #pragma unroll
-        for (int w = 0; w < kMaxSegments; ++w) {
-          const size_t at = base + static_cast<size_t>(min(w, a.S - 1)) * kBuckets + b;
-          cw[w] = a.pcnt[at];
-          mw[w] = a.pmass[at];
-        }
-        __builtin_amdgcn_sched_barrier(0);
+          for (int w = 0; w < 8; ++w) {
+            const size_t at = base + static_cast<size_t>(min(w0 + w, a.S - 1)) * kBuckets + b;
+            cw[w] = a.pcnt[at];
+            mw[w] = a.pmass[at];
+          }
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int w = 0; w < kMaxSegments; ++w) {
-          c += w < a.S ? cw[w] : 0u;
-          m += w < a.S ? mw[w] : uint64_t{0};
+          for (int w = 0; w < 8; ++w) {
+            c += w0 + w < a.S ? cw[w] : 0u;
+            m += w0 + w < a.S ? mw[w] : uint64_t{0};
+          }
         }
         s.cnt[b] = c;
         s.wsum[b] = m;
@@ -1252,8 +1291,7 @@ struct RowSampler {
       });
     }
     __syncthreads();
-    scan2(s.cnt, s.pcnt);
-    scan2(s.wsum, s.pmass);
+    scan2_hist();
     int cached = -1;
     uint64_t cum, tot;
     // top-k: bucket bk holds rank k - 1; its first need_k sorted elements stay.
@@ -1547,16 +1585,18 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_stats(SampleArgs a
 
 // The merged statistics of split row r (its S records).
 __device__ __forceinline__ ChunkStats split_stats(const SampleArgs& a, int64_t r) {
-  // Every record loaded (at a clamped segment: merging a record twice
-  // changes nothing) before the first merge.
-  SplitStat rec[kMaxSegments];
-#pragma unroll
-  for (int w = 0; w < kMaxSegments; ++w) rec[w] = a.stat[r * a.S + min(w, a.S - 1)];
-  __builtin_amdgcn_sched_barrier(0);
+  // Eight records per step, every one loaded (at a clamped segment: merging
+  // a record twice changes nothing) before the first merge.
   ChunkStats st;
   st.init(static_cast<int>(a.V));
+  for (int w0 = 0; w0 < a.S; w0 += 8) {
+    SplitStat rec[8];
 #pragma unroll
-  for (int w = 0; w < kMaxSegments; ++w) st.merge(rec[w]);
+    for (int w = 0; w < 8; ++w) rec[w] = a.stat[r * a.S + min(w0 + w, a.S - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) st.merge(rec[w]);
+  }
   return st;
 }
 
