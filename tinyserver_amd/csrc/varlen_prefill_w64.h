@@ -3,7 +3,10 @@
 // Reference: server/model/kernels/varlen_attention.py:8-142 (per query
 // block, an fp32 online softmax over 32-key blocks, top-left causal mask
 // :116-119, P cast to the V dtype before P.V :126, l summing the fp32 P
-// :128-129).
+// :128-129). Here l sums the 16-bit P that P.V takes (in fp32, on the
+// matrix cores), so numerator and denominator weigh the same P: the
+// output moves by a relative ~2^-9 / sqrt(keys) at most against summing
+// the fp32 P, well inside the attention tolerance.
 //
 // head_dim 128, bf16/f16, GQA groups of a multiple of 4 q-heads. A work item
 // is (sequence, kv head, group of 4 q-heads, 64 queries); the workgroup's 4
@@ -100,6 +103,25 @@ __device__ __forceinline__ void scale_agpr16(f32x16& x, float alpha) {
   }
 #pragma unroll
   for (int i = 0; i < 16; ++i) x[i] = e[i];
+  in_agpr(x);
+}
+
+// Elements 0 and 1 of x (4 fp32 in AGPRs) *= a0 and a1, in place, as
+// scale_agpr16 does. Elements 2 and 3 are left alone, but pass through the
+// assembly as AGPR operands too: otherwise the compiler keeps copies of
+// them in VGPRs across the branch that holds this.
+__device__ __forceinline__ void scale_agpr2(f32x4& x, float a0, float a1) {
+  float e[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) e[i] = x[i];
+  float tmp;
+  asm volatile(
+      "v_accvgpr_read_b32 %4, %0\n\tv_mul_f32 %4, %4, %5\n\tv_accvgpr_write_b32 %0, %4\n\t"
+      "v_accvgpr_read_b32 %4, %1\n\tv_mul_f32 %4, %4, %6\n\tv_accvgpr_write_b32 %1, %4"
+      : "+a"(e[0]), "+a"(e[1]), "+a"(e[2]), "+a"(e[3]), "=&v"(tmp)
+      : "v"(a0), "v"(a1));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = e[i];
   in_agpr(x);
 }
 
@@ -414,15 +436,31 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
 
   // ---- Per-tile softmax state, scores and output accumulators. m: the
   // running max (log2 units); mt: the max of the tile's scores in sc, found
-  // in the half that computed them; l: the lane's share of the denominator,
-  // as two partial sums.
-  float m[2], mt[2], lp[2][2];
+  // in the half that computed them; lacc: the denominators, summed on the
+  // matrix cores from the P operands the P.V MFMAs take: a 16x16x32 MFMA
+  // with A = ones where row m meets the k-groups g with g % 2 == m (lane l
+  // supplies A[l % 16][8(l / 16)..+8]) and B = the P operand (lane (h, c)
+  // supplies query c's 8 keys of the step, read as B[8(2h + c / 16)..+8][c %
+  // 16]) gives D[0][n] = query n's 16 keys and D[1][n] = query 16 + n's, so
+  // lane n < 16 holds l of query n in element 0 and of query 16 + n in
+  // element 1 (the other elements stay zero). l sums the bf16 P the product
+  // takes, in fp32.
+  float m[2], mt[2];
+  f32x4 lacc[2];
+  uint32_t one2 = 0;  // the A operand: ones (two 16-bit 1.0) where lane % 16 == (lane / 16) % 2
+  if ((lane & 15) == ((lane >> 4) & 1)) one2 = std::is_same<T, bf16_t>::value ? 0x3F803F80u : 0x3C003C00u;
+  u32x4 lone = u32x4{one2, one2, one2, one2};
+  in_agpr(lone);
   f32x16 sc[2];
   f32x16 acc[2][NU];
   u32x4 pop[2][2];
   auto qk1 = [&](int t, int jj) __attribute__((always_inline)) { mfma_qk_v<T>(sc[t], kop[jj], qop[t][jj], jj == 0); };
   auto pv1 = [&](int t, int s2, int u) __attribute__((always_inline)) {
     acc[t][u] = mfma_k16x32<T>(vop[s2][u], pop[t][s2], acc[t][u]);
+  };
+  auto lsum1 = [&](int t, int s2) __attribute__((always_inline)) {
+    lacc[t] = mfma_k32<T>(lone, pop[t][s2], lacc[t]);
+    in_agpr(lacc[t]);
   };
   // Scores e0 .. e1-1 of tile t in block blk set to -inf past k_len and,
   // causal, past the query (the key of accumulator e is 8(e/4) + 4h + e%4).
@@ -468,11 +506,11 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
       const float m_new = fmaxf(m[t], mt[t]);
       if (!__all(m[t] == kNegInfP)) {
         const float alpha = m_new == kNegInfP ? 1.f : fast_exp2(m[t] - m_new);
-        lp[t][0] *= alpha;
-        lp[t][1] *= alpha;
+        const float alpha16 = __shfl_down(alpha, 16, 64);  // query lane + 16's (lacc element 1)
         xdl_to_valu_nops();
 #pragma unroll
         for (int u = 0; u < NU; ++u) scale_agpr16(acc[t][u], alpha);
+        scale_agpr2(lacc[t], alpha, alpha16);
         xdl_to_valu_nops();
       }
       m[t] = m_new;
@@ -507,10 +545,10 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
       } else {
         pv1(o, (g - 8) / NU, (g - 8) % NU);
         in_agpr(acc[o][(g - 8) % NU]);  // keeps the MFMA in its slot
+        if ((g - 8) % NU == NU - 1) lsum1(o, (g - 8) / NU);  // l of the step's P, after its last P.V
       }
       x[g] = fmaf(sc[t][g], cs, -mm);
       if (g >= 1) p[g - 1] = fast_exp2(x[g - 1]);
-      if (g >= 2) lp[t][g & 1] += p[g - 2];
       if (g >= 3 && (g & 1)) {
         uint32_t pk = pack2<T>(p[g - 3], p[g - 2]);
         asm volatile("" : "+v"(pk));
@@ -525,20 +563,18 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
       if (g >= 12 && do_qk) max_part(o, g - 12);
       // The slot's results, pinned here: nothing of it can sink into a later
       // slot or past the mask branch.
-      asm volatile("" : "+v"(lp[t][0]), "+v"(lp[t][1]), "+v"(x[g]));
+      asm volatile("" : "+v"(x[g]));
       if (g >= 1) asm volatile("" : "+v"(p[g - 1]));
       if (g >= 12 && do_qk) asm volatile("" : "+v"(mxa), "+v"(mxb));
       __builtin_amdgcn_sched_barrier(0);
     }
     p[15] = fast_exp2(x[15]);
-    lp[t][0] += p[14];
-    lp[t][1] += p[15];
     pop[t][1][3] = pack2<T>(p[14], p[15]);
     if (do_qk) max_end(o);
     // Everything of this half is computed here, under its MFMAs: without
     // this the compiler sinks it to the first use in the next half.
     float& mto = mt[o];
-    asm volatile("" : "+v"(pop[t][0]), "+v"(pop[t][1]), "+v"(lp[t][0]), "+v"(lp[t][1]), "+v"(mto));
+    asm volatile("" : "+v"(pop[t][0]), "+v"(pop[t][1]), "+v"(mto));
   };
 
   // ---- One iteration j: on entry S0(j) is in sc[0] with its max in mt[0],
@@ -596,8 +632,8 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
     };
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const float lt = lp[t][0] + lp[t][1];
-      const float rl = 1.f / (lt + __shfl_xor(lt, 32, 64));  // 1 / query c's denominator
+      const float l0 = __shfl(lacc[t][0], c & 15, 64), l1 = __shfl(lacc[t][1], c & 15, 64);
+      const float rl = 1.f / (c < 16 ? l0 : l1);  // 1 / query c's denominator
       const int rbase = it.q0 + 32 * t;
       const bool full = rbase + 32 <= it.q_len;
       char* rowp[4];
@@ -655,7 +691,8 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       m[t] = kNegInfP;
-      lp[t][0] = lp[t][1] = 0.f;
+      lacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      in_agpr(lacc[t]);
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
 #pragma unroll
@@ -714,9 +751,11 @@ __device__ __forceinline__ void prefill_w64_body(PrefillArgs a, const int32_t* _
     // its output. (An item without keys: 0/0, as the reference's.)
     if (n > 0) {
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
+      for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
         for (int u = 0; u < NU; ++u) pv1(1, s2, u);
+        lsum1(1, s2);
+      }
     }
     store_out(X);
     X = Y;
