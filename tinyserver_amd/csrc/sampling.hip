@@ -63,11 +63,16 @@ struct SampleArgs {
   int64_t* out; int64_t out_s;
   int cand;  // 1: top-k and greedy rows may take the register-resident candidate pass
   // Rows split over S workgroups (split_row; S = 0: none): per (row,
-  // segment) the statistics record and the partial histogram.
+  // segment) the statistics record and the partial histogram, as the
+  // exclusive prefix of its counts (plp) and its masses (pmass); with
+  // bucket lists (pidx non-null) also its elements' indices, relative to
+  // the segment's first element, in bucket order (segcap each).
   struct SplitStat* stat;
-  uint32_t* pcnt;
+  uint32_t* plp;
   uint64_t* pmass;
   int S;
+  uint16_t* pidx;
+  int segcap;
 };
 
 // ---- Rows split over several workgroups. A histogram row (temperature >
@@ -82,6 +87,9 @@ struct SampleArgs {
 // workgroup path's.
 constexpr int kSplitThreads = 256;
 constexpr int kMaxSegments = 16;  // workgroups per split row, at most
+// Elements of a segment whose bucket list sample_split_hist builds in LDS:
+// 55 KB beside the 24 KB histogram, so two workgroups fit a CU's 160 KB.
+constexpr int kSegListMax = 28160;
 struct SplitStat {
   float mx, mn, fmn;
   int imx, imn, inan;
@@ -236,6 +244,14 @@ __device__ __forceinline__ bool candidate_row(const SampleArgs& a, float temp, i
 // sample_split_hist make (a.S > 1: the launch split rows).
 __device__ __forceinline__ bool split_row(const SampleArgs& a, float temp, int64_t k) {
   return a.S > 1 && temp > 0.f && !(a.cand && a.V <= kRegMaxV && candidate_row(a, temp, k));
+}
+
+// The chunks of segment seg of a split row: [seg * per, min((seg + 1) *
+// per, V / 8)), per = ceil(V / 8 / S).
+__device__ __forceinline__ void split_range(const SampleArgs& a, int seg, int& c0, int& c1) {
+  const int n8 = static_cast<int>(a.V >> 3), per = (n8 + a.S - 1) / a.S;
+  c0 = min(n8, seg * per);
+  c1 = min(n8, c0 + per);
 }
 
 // Two 16-bit floats (one word) -> two order-preserving 16-bit keys, larger
@@ -615,13 +631,55 @@ struct RowSampler {
                });
   }
 
+  // A split row whose segments' bucket lists sample_split_hist wrote
+  // (lists()): every element of buckets b0 .. b1 appended to s.keys (as a
+  // rank key) from the lists, without a pass over the row. Segment g holds
+  // [plp[g][b0], plp[g][b1 + 1]) of them (its element count past the last
+  // bucket); an element's list entry is its index relative to the segment.
+  __device__ __forceinline__ bool lists() const { return srow >= 0 && a.pidx != nullptr; }
+  __device__ __forceinline__ void gather_lists(int b0, int b1) {
+    const int S = a.S;
+    const size_t rs0 = static_cast<size_t>(srow) * S;
+    if (tid < S) {  // (S <= kMaxSegments <= kSampWaves)
+      int c0, c1;
+      split_range(a, tid, c0, c1);
+      const uint32_t len = static_cast<uint32_t>(8 * (c1 - c0));  // the segment's elements
+      // (prefixes never exceed len: the clamps only bound every read below
+      // to the segment's list, whatever the workspace held)
+      const uint32_t lo = min(a.plp[(rs0 + tid) * kBuckets + b0], len);
+      const uint32_t hi = min(b1 + 1 < kBuckets ? a.plp[(rs0 + tid) * kBuckets + b1 + 1] : len, len);
+      s.wave_u64[tid] = lo;
+      s.wave_i[tid] = hi > lo ? hi - lo : 0;
+    }
+    __syncthreads();
+    const uint32_t at0 = s.n_gather;
+    int n = 0;
+    for (int g = 0; g < S; ++g) n += static_cast<int>(s.wave_i[g]);
+    for (int e = tid; e < n; e += kSampThreads) {
+      int g = 0, first = 0;
+      while (g + 1 < S && e >= first + static_cast<int>(s.wave_i[g])) first += static_cast<int>(s.wave_i[g++]);
+      int c0, c1;
+      split_range(a, g, c0, c1);
+      const uint32_t li = a.pidx[(rs0 + g) * a.segcap + s.wave_u64[g] + (e - first)];
+      const int i = min(8 * c0 + static_cast<int>(li), 8 * c1 - 1);
+      if (at0 + e < static_cast<uint32_t>(kCap)) s.keys[at0 + e] = rank_key(logit(i), i);
+    }
+    __syncthreads();
+    if (tid == 0) s.n_gather = at0 + static_cast<uint32_t>(n);
+    __syncthreads();
+  }
+
   __device__ __forceinline__ bool gather_sorted(int b, float scale, int& cached) {
     if (cached == b) return true;
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
     bool keyed = false;
+    if (lists()) {
+      gather_lists(b, b);
+      keyed = true;
+    }
     if constexpr (UNIT && sizeof(T) == 2) {
-      if (chunked()) {  // the bucket: keys [first_key_at_most(b), first_key_at_most(b - 1))
+      if (!keyed && chunked()) {  // the bucket: keys [first_key_at_most(b), first_key_at_most(b - 1))
         const uint32_t klo = first_key_at_most(b, scale);
         const uint32_t khi = (b > 0 ? first_key_at_most(b - 1, scale) : Inf16<T>::kPosKey + 1) - 1;
         gather_key_range(klo, khi);
@@ -649,8 +707,12 @@ struct RowSampler {
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
     bool keyed = false;
+    if (lists()) {
+      gather_lists(0, nb);
+      keyed = true;
+    }
     if constexpr (UNIT && sizeof(T) == 2) {
-      if (chunked()) {  // buckets 0 .. nb: the keys from first_key_at_most(nb) up
+      if (!keyed && chunked()) {  // buckets 0 .. nb: the keys from first_key_at_most(nb) up
         gather_key_range(first_key_at_most(nb, scale), Inf16<T>::kPosKey);
         keyed = true;
       }
@@ -1219,12 +1281,21 @@ struct RowSampler {
     if (n > static_cast<uint32_t>(kSampThreads)) return false;
     // bucket b holds the keys [first_key_at_most(b), first_key_at_most(b - 1)), bucket 0 up to +inf
     auto key_end = [&](int b) { return b > 0 ? first_key_at_most(b - 1, scale) - 1 : Inf16<T>::kPosKey; };
-    const uint32_t kb_lo = first_key_at_most(bp, scale), kb_hi = key_end(bp);
     if (tid == 0) s.n_gather = 0;
     __syncthreads();
-    if (blo > last) gather_key_range(kb_lo, kb_hi);
-    else if (last + 1 == bp) gather_key_range(kb_lo, key_end(blo));  // adjacent: one range
-    else gather_key_range<true>(kb_lo, kb_hi, first_key_at_most(last, scale), key_end(blo));
+    if (lists()) {
+      if (blo > last) gather_lists(bp, bp);
+      else if (last + 1 == bp) gather_lists(blo, bp);
+      else {
+        gather_lists(blo, last);
+        gather_lists(bp, bp);
+      }
+    } else {
+      const uint32_t kb_lo = first_key_at_most(bp, scale), kb_hi = key_end(bp);
+      if (blo > last) gather_key_range(kb_lo, kb_hi);
+      else if (last + 1 == bp) gather_key_range(kb_lo, key_end(blo));  // adjacent: one range
+      else gather_key_range<true>(kb_lo, kb_hi, first_key_at_most(last, scale), key_end(blo));
+    }
     __syncthreads();
     if (s.n_gather != n) return false;  // (the histogram's own counts: never expected to differ)
     sort_keys(static_cast<int>(n));
@@ -1253,6 +1324,9 @@ struct RowSampler {
     // lo: the smallest finite key
     const float scale = kmax > lo ? static_cast<float>(kBuckets - 1) / (kmax - lo) : 0.f;
     if (srow >= 0) {  // the sum of the row's split partials (sample_split_hist, same buckets and masses)
+      // The segments' count prefixes add up to the row's (pcnt), and a
+      // bucket's count is the step to the next bucket's prefix (the last
+      // bucket's to V: every element is in one bucket).
       const size_t base = static_cast<size_t>(srow) * a.S * kBuckets;
       for (int b = tid; b < kBuckets; b += kSampThreads) {
         uint32_t c = 0;
@@ -1265,7 +1339,7 @@ struct RowSampler {
 #pragma unroll
           for (int w = 0; w < 8; ++w) {
             const size_t at = base + static_cast<size_t>(min(w0 + w, a.S - 1)) * kBuckets + b;
-            cw[w] = a.pcnt[at];
+            cw[w] = a.plp[at];
             mw[w] = a.pmass[at];
           }
           __builtin_amdgcn_sched_barrier(0);
@@ -1275,9 +1349,12 @@ struct RowSampler {
             m += w0 + w < a.S ? mw[w] : uint64_t{0};
           }
         }
-        s.cnt[b] = c;
+        s.pcnt[b] = c;
         s.wsum[b] = m;
       }
+      __syncthreads();
+      for (int b = tid; b < kBuckets; b += kSampThreads)
+        s.cnt[b] = (b + 1 < kBuckets ? s.pcnt[b + 1] : static_cast<uint32_t>(a.V)) - s.pcnt[b];
     } else {
       for (int b = tid; b < kBuckets; b += kSampThreads) {
         s.cnt[b] = 0;
@@ -1291,7 +1368,8 @@ struct RowSampler {
       });
     }
     __syncthreads();
-    scan2_hist();
+    if (srow >= 0) scan2(s.wsum, s.pmass);  // (pcnt came with the partials)
+    else scan2_hist();
     int cached = -1;
     uint64_t cum, tot;
     // top-k: bucket bk holds rank k - 1; its first need_k sorted elements stay.
@@ -1552,14 +1630,6 @@ struct RowSampler {
   }
 };
 
-// The chunks of segment seg of a split row: [seg * per, min((seg + 1) *
-// per, V / 8)), per = ceil(V / 8 / S).
-__device__ __forceinline__ void split_range(const SampleArgs& a, int seg, int& c0, int& c1) {
-  const int n8 = static_cast<int>(a.V >> 3), per = (n8 + a.S - 1) / a.S;
-  c0 = min(n8, seg * per);
-  c1 = min(n8, c0 + per);
-}
-
 // The statistics record of segment blockIdx.x of split row blockIdx.y.
 template <typename T>
 __global__ __launch_bounds__(kSplitThreads) void sample_split_stats(SampleArgs a) {
@@ -1602,13 +1672,20 @@ __device__ __forceinline__ ChunkStats split_stats(const SampleArgs& a, int64_t r
 
 // The partial histogram (count and mass per bucket, the buckets and masses
 // of RowSampler::fast) of segment blockIdx.x of split row blockIdx.y, for a
-// row that reaches the histogram path: no NaN, a finite maximum of x.
+// row that reaches the histogram path: no NaN, a finite maximum of x; the
+// counts as their exclusive prefix (a.plp). With bucket lists (a.pidx),
+// also the segment's elements in bucket order: each element's index
+// relative to the segment at its bucket's next place (a counting sort in
+// LDS, order within a bucket free), written out whole. sample_tokens_kernel then
+// gathers a bucket range from the lists instead of reading the row.
 template <typename T>
 __global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a) {
   __shared__ uint32_t cnt[kBuckets];
   __shared__ uint64_t msum[kBuckets];
+  __shared__ __align__(16) uint16_t list[kSegListMax];
+  __shared__ uint32_t wtot[kSplitThreads / 64];
   const int64_t r = blockIdx.y;
-  const int seg = blockIdx.x, tid = threadIdx.x;
+  const int seg = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float temp = a.temp[r * a.temp_s];
   if (!split_row(a, temp, load_int(a.topk, a.topk_dt, r * a.topk_s))) return;
   const ChunkStats st = split_stats(a, r);
@@ -1624,7 +1701,7 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a)
   int c0, c1;
   split_range(a, seg, c0, c1);
   const u32x4* r4 = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.logits) + r * a.ls0);
-  each_chunk(r4, c0 + tid, c1, kSplitThreads, [&](const u32x4 w, int) {
+  auto add = [&](const u32x4 w) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float kv = (e & 1) ? hi_f<T>(w[e >> 1]) : lo_f<T>(w[e >> 1]);
@@ -1633,13 +1710,76 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a)
       atomicAdd(reinterpret_cast<unsigned long long*>(&msum[b]),
                 static_cast<unsigned long long>(mass_of(kv, kmax, kc)));
     }
-  });
+  };
+  // With bucket lists the segment (at most kSegListMax elements) stays in
+  // registers for both passes: KEEP chunks per thread, all loaded at once.
+  constexpr int KEEP = (kSegListMax / 8 + kSplitThreads - 1) / kSplitThreads;
+  const bool lists = a.pidx != nullptr;
+  u32x4 seg_w[KEEP];
+  if (lists) {
+#pragma unroll
+    for (int j = 0; j < KEEP; ++j) {
+      const int ch = c0 + tid + j * kSplitThreads;
+      seg_w[j] = ch < c1 ? r4[ch] : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < KEEP; ++j)
+      if (c0 + tid + j * kSplitThreads < c1) add(seg_w[j]);
+  } else {
+    each_chunk(r4, c0 + tid, c1, kSplitThreads, [&](const u32x4 w, int) { add(w); });
+  }
   __syncthreads();
   const size_t base = (static_cast<size_t>(r) * a.S + seg) * kBuckets;
-  for (int b = tid; b < kBuckets; b += kSplitThreads) {
-    a.pcnt[base + b] = cnt[b];
-    a.pmass[base + b] = msum[b];
+  for (int b = tid; b < kBuckets; b += kSplitThreads) a.pmass[base + b] = msum[b];
+  // The counts go out as their exclusive prefix (cnt -> prefix in place: 8
+  // buckets per thread, a wave scan of the threads' sums, then the waves'
+  // totals): the bucket lists' offsets, and the merge's row prefix without
+  // a scan of the counts.
+  constexpr int BPT = kBuckets / kSplitThreads;
+  uint32_t v[BPT], run = 0;
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    v[i] = cnt[BPT * tid + i];
+    run += v[i];
   }
+  uint32_t incl = run;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t up = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += up;
+  }
+  if (lane == 63) wtot[wave] = incl;
+  __syncthreads();
+  uint32_t before = incl - run;
+  for (int w = 0; w < wave; ++w) before += wtot[w];
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    cnt[BPT * tid + i] = before;
+    a.plp[base + BPT * tid + i] = before;
+    before += v[i];
+  }
+  if (!lists) return;
+  __syncthreads();
+  // Each element's index at its bucket's next place. A chunk's 8 places
+  // are claimed before any is written, so the writes wait for the claims
+  // once per chunk, not once per element.
+#pragma unroll
+  for (int j = 0; j < KEEP; ++j) {
+    const int ch = c0 + tid + j * kSplitThreads;
+    if (ch >= c1) continue;
+    const u32x4 w = seg_w[j];
+    uint32_t at[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float kv = (e & 1) ? hi_f<T>(w[e >> 1]) : lo_f<T>(w[e >> 1]);
+      at[e] = atomicAdd(&cnt[RowSampler<T, true>::bucket0(kv, kmax, scale)], 1u);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) list[at[e]] = static_cast<uint16_t>(8 * (ch - c0) + e);
+  }
+  __syncthreads();
+  u32x4* const dst = reinterpret_cast<u32x4*>(a.pidx + (static_cast<size_t>(r) * a.S + seg) * a.segcap);
+  const u32x4* const src = reinterpret_cast<const u32x4*>(list);
+  for (int i = tid; i < c1 - c0; i += kSplitThreads) dst[i] = src[i];  // 8 indices per 16 bytes
 }
 
 template <typename T, bool UNIT>
@@ -1843,14 +1983,31 @@ int split_segments(int64_t B, int64_t V) {
   return S < 2 ? 0 : static_cast<int>(S > kMaxSegments ? kMaxSegments : S);
 }
 
-// Workspace of a split launch: the statistics records, then the partial
-// counts and masses, each region 256-byte aligned.
-size_t split_bytes(int64_t B, int S) {
-  if (S <= 1) return 0;
+// Elements per segment of a split row (S segments of whole 8-logit chunks),
+// and whether sample_split_hist builds the segments' bucket lists: when a
+// segment's list fits its LDS (kSegListMax).
+int64_t seg_elems(int64_t V, int S) { return 8 * (((V >> 3) + S - 1) / S); }
+bool split_lists(int64_t V, int S) { return S > 1 && seg_elems(V, S) <= kSegListMax; }
+
+// Workspace of a split launch, each region 256-byte aligned: the statistics
+// records, the partial count prefixes and masses, and the bucket lists.
+struct SplitLayout {
+  size_t plp, pmass, pidx, total;
+};
+SplitLayout split_layout(int64_t B, int64_t V, int S) {
   const size_t segs = static_cast<size_t>(B) * S;
-  return align256(segs * sizeof(SplitStat)) + align256(segs * kBuckets * sizeof(uint32_t)) +
-         segs * kBuckets * sizeof(uint64_t);
+  SplitLayout l{};
+  l.plp = align256(segs * sizeof(SplitStat));
+  l.pmass = l.plp + align256(segs * kBuckets * sizeof(uint32_t));
+  l.pidx = l.pmass + segs * kBuckets * sizeof(uint64_t);
+  l.total = l.pidx;
+  if (split_lists(V, S)) {
+    l.pidx = align256(l.pidx);
+    l.total = l.pidx + segs * static_cast<size_t>(seg_elems(V, S)) * sizeof(uint16_t);
+  }
+  return l;
 }
+size_t split_bytes(int64_t B, int64_t V, int S) { return S <= 1 ? 0 : split_layout(B, V, S).total; }
 
 int sample_impl(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature, const tsa_view* top_k,
                 const tsa_view* top_p, const tsa_view* uniforms, void* workspace, size_t workspace_bytes,
@@ -1885,16 +2042,19 @@ int sample_impl(const tsa_view* out, const tsa_view* logits, const tsa_view* tem
                       (reinterpret_cast<uintptr_t>(logits->data) & 15) == 0 && ((a.ls0 * 2) & 15) == 0;
   const int S = workspace != nullptr && rows16 ? split_segments(B, V) : 0;
   if (S > 1) {
-    const size_t need = split_bytes(B, S);
+    const size_t need = split_bytes(B, V, S);
     TSA_REQUIRE(workspace_bytes >= need, "workspace too small: %zu bytes, need %zu (tsa_sample_tokens_workspace_bytes)",
                 workspace_bytes, need);
     TSA_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "workspace must be 256-byte aligned");
-    const size_t segs = static_cast<size_t>(B) * S;
+    const SplitLayout l = split_layout(B, V, S);
     char* w = static_cast<char*>(workspace);
     a.stat = reinterpret_cast<SplitStat*>(w);
-    a.pcnt = reinterpret_cast<uint32_t*>(w + align256(segs * sizeof(SplitStat)));
-    a.pmass = reinterpret_cast<uint64_t*>(w + align256(segs * sizeof(SplitStat)) +
-                                          align256(segs * kBuckets * sizeof(uint32_t)));
+    a.plp = reinterpret_cast<uint32_t*>(w + l.plp);
+    a.pmass = reinterpret_cast<uint64_t*>(w + l.pmass);
+    if (split_lists(V, S)) {
+      a.pidx = reinterpret_cast<uint16_t*>(w + l.pidx);
+      a.segcap = static_cast<int>(seg_elems(V, S));
+    }
     a.S = S;
     const dim3 sgrid(S, B);
     if (logits->dtype == TSA_BF16) {
@@ -1931,7 +2091,7 @@ extern "C" int tsa_sample_tokens(const tsa_view* out, const tsa_view* logits, co
 }
 
 extern "C" size_t tsa_sample_tokens_workspace_bytes(int64_t batch, int64_t vocab) {
-  return split_bytes(batch, split_segments(batch, vocab));
+  return split_bytes(batch, vocab, split_segments(batch, vocab));
 }
 
 extern "C" int tsa_sample_tokens_ws(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature,
