@@ -563,15 +563,27 @@ struct RowSampler {
     __syncthreads();
   }
 
+  // atomicMin(at, b) for the wave's lowest lane with hit, where the wave's
+  // lanes hold consecutive b (b = tid + j kSampThreads, the same j in every
+  // lane): one LDS atomic per wave, not one per qualifying lane (on one
+  // address those serialise).
+  __device__ __forceinline__ void min_first_hit(int* at, bool hit, int b) {
+    const uint64_t m = __ballot(hit);
+    if (m != 0 && lane == __builtin_ctzll(m)) atomicMin(at, b);
+  }
+
   // The smallest non-empty bucket b <= last whose running mass through b
   // (the full bucket, or last_incl for bucket `last`) reaches the target.
   __device__ __forceinline__ int first_bucket(int last, uint64_t last_incl, bool ge, double target) {
     if (tid == 0) s.found_bucket = kBuckets;
     __syncthreads();
     for (int b = tid; b < kBuckets; b += kSampThreads) {
-      if (b > last || s.cnt[b] == 0) continue;
-      const double incl = static_cast<double>(b == last ? last_incl : s.pmass[b] + s.wsum[b]);
-      if (ge ? incl >= target : incl > target) atomicMin(&s.found_bucket, b);
+      bool hit = false;
+      if (b <= last && s.cnt[b] != 0) {
+        const double incl = static_cast<double>(b == last ? last_incl : s.pmass[b] + s.wsum[b]);
+        hit = ge ? incl >= target : incl > target;
+      }
+      min_first_hit(&s.found_bucket, hit, b);
     }
     __syncthreads();
     const int fb = s.found_bucket;
@@ -1267,11 +1279,15 @@ struct RowSampler {
       s.found_bucket2 = bp;
     }
     __syncthreads();
-    for (int b = tid; b < bp; b += kSampThreads) {
-      if (s.cnt[b] == 0) continue;
-      const double incl = static_cast<double>(s.pmass[b] + s.wsum[b]);
-      if (incl >= tlo) atomicMin(&s.found_bucket, b);
-      if (incl >= thi) atomicMin(&s.found_bucket2, b);
+    for (int b = tid; b < kBuckets; b += kSampThreads) {
+      bool hlo = false, hhi = false;
+      if (b < bp && s.cnt[b] != 0) {
+        const double incl = static_cast<double>(s.pmass[b] + s.wsum[b]);
+        hlo = incl >= tlo;
+        hhi = incl >= thi;
+      }
+      min_first_hit(&s.found_bucket, hlo, b);
+      min_first_hit(&s.found_bucket2, hhi, b);
     }
     __syncthreads();
     const int blo = s.found_bucket, last = min(s.found_bucket2, bp - 1);
@@ -1379,7 +1395,7 @@ struct RowSampler {
       if (tid == 0) s.found_bucket = kBuckets;
       __syncthreads();
       for (int b = tid; b < kBuckets; b += kSampThreads)
-        if (s.cnt[b] > 0 && static_cast<int64_t>(s.pcnt[b]) + s.cnt[b] >= k) atomicMin(&s.found_bucket, b);
+        min_first_hit(&s.found_bucket, s.cnt[b] > 0 && static_cast<int64_t>(s.pcnt[b]) + s.cnt[b] >= k, b);
       __syncthreads();
       bk = s.found_bucket;
       __syncthreads();
@@ -1490,7 +1506,7 @@ struct RowSampler {
       __syncthreads();
       for (int b = tid; b < kBuckets; b += kSampThreads) {
         const uint64_t incl = b + 1 < kBuckets ? s.wsum[b + 1] : s.wsum[b] + w_last;
-        if (s.cnt[b] > 0 && reached(base + incl)) atomicMin(&s.found_bucket, b);
+        min_first_hit(&s.found_bucket, s.cnt[b] > 0 && reached(base + incl), b);
       }
       __syncthreads();
       const int fb = s.found_bucket;
