@@ -298,6 +298,8 @@ struct SampleLds {
   uint64_t wave_u64[kSampWaves];
   float wave_f[kSampWaves];
   int64_t wave_i[kSampWaves];
+  uint32_t list_lo[2 * kMaxSegments];  // gather_lists: per (range, segment) its first list entry
+  int list_n[2 * kMaxSegments];        // and its entries
   uint32_t n_gather;
   int found_bucket, found_bucket2;
   uint64_t found_cum;
@@ -644,35 +646,44 @@ struct RowSampler {
   }
 
   // A split row whose segments' bucket lists sample_split_hist wrote
-  // (lists()): every element of buckets b0 .. b1 appended to s.keys (as a
-  // rank key) from the lists, without a pass over the row. Segment g holds
-  // [plp[g][b0], plp[g][b1 + 1]) of them (its element count past the last
-  // bucket); an element's list entry is its index relative to the segment.
+  // (lists()): every element of buckets b0 .. b1 and, when b2 <= b3, of
+  // buckets b2 .. b3, appended to s.keys (as a rank key) from the lists,
+  // without a pass over the row: three dependent reads (the prefixes, the
+  // list entries, the logits) for both ranges together. Segment g holds
+  // [plp[g][b], plp[g][b' + 1]) of a range b .. b' (its element count past
+  // the last bucket); an element's list entry is its index relative to
+  // the segment.
   __device__ __forceinline__ bool lists() const { return srow >= 0 && a.pidx != nullptr; }
-  __device__ __forceinline__ void gather_lists(int b0, int b1) {
+  __device__ __forceinline__ void gather_lists(int b0, int b1, int b2 = 1, int b3 = 0) {
     const int S = a.S;
     const size_t rs0 = static_cast<size_t>(srow) * S;
-    if (tid < S) {  // (S <= kMaxSegments <= kSampWaves)
+    if (tid < 2 * S) {  // thread g + S r: segment g, range r
+      const int g = tid % S, rg = tid / S;
+      const int lo_b = rg ? b2 : b0, hi_b = rg ? b3 : b1;
       int c0, c1;
-      split_range(a, tid, c0, c1);
+      split_range(a, g, c0, c1);
       const uint32_t len = static_cast<uint32_t>(8 * (c1 - c0));  // the segment's elements
-      // (prefixes never exceed len: the clamps only bound every read below
-      // to the segment's list, whatever the workspace held)
-      const uint32_t lo = min(a.plp[(rs0 + tid) * kBuckets + b0], len);
-      const uint32_t hi = min(b1 + 1 < kBuckets ? a.plp[(rs0 + tid) * kBuckets + b1 + 1] : len, len);
-      s.wave_u64[tid] = lo;
-      s.wave_i[tid] = hi > lo ? hi - lo : 0;
+      uint32_t lo = 0, hi = 0;
+      if (lo_b <= hi_b) {
+        // (prefixes never exceed len: the clamps only bound every read below
+        // to the segment's list, whatever the workspace held)
+        lo = min(a.plp[(rs0 + g) * kBuckets + lo_b], len);
+        hi = min(hi_b + 1 < kBuckets ? a.plp[(rs0 + g) * kBuckets + hi_b + 1] : len, len);
+      }
+      s.list_lo[tid] = lo;
+      s.list_n[tid] = static_cast<int>(hi > lo ? hi - lo : 0);
     }
     __syncthreads();
     const uint32_t at0 = s.n_gather;
     int n = 0;
-    for (int g = 0; g < S; ++g) n += static_cast<int>(s.wave_i[g]);
+    for (int q = 0; q < 2 * S; ++q) n += s.list_n[q];
     for (int e = tid; e < n; e += kSampThreads) {
-      int g = 0, first = 0;
-      while (g + 1 < S && e >= first + static_cast<int>(s.wave_i[g])) first += static_cast<int>(s.wave_i[g++]);
+      int q = 0, first = 0;  // q: the (range, segment) pair holding element e
+      while (q + 1 < 2 * S && e >= first + s.list_n[q]) first += s.list_n[q++];
+      const int g = q % S;
       int c0, c1;
       split_range(a, g, c0, c1);
-      const uint32_t li = a.pidx[(rs0 + g) * a.segcap + s.wave_u64[g] + (e - first)];
+      const uint32_t li = a.pidx[(rs0 + g) * a.segcap + s.list_lo[q] + (e - first)];
       const int i = min(8 * c0 + static_cast<int>(li), 8 * c1 - 1);
       if (at0 + e < static_cast<uint32_t>(kCap)) s.keys[at0 + e] = rank_key(logit(i), i);
     }
@@ -1302,10 +1313,7 @@ struct RowSampler {
     if (lists()) {
       if (blo > last) gather_lists(bp, bp);
       else if (last + 1 == bp) gather_lists(blo, bp);
-      else {
-        gather_lists(blo, last);
-        gather_lists(bp, bp);
-      }
+      else gather_lists(blo, last, bp, bp);
     } else {
       const uint32_t kb_lo = first_key_at_most(bp, scale), kb_hi = key_end(bp);
       if (blo > last) gather_key_range(kb_lo, kb_hi);
