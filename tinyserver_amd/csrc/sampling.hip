@@ -756,25 +756,61 @@ struct RowSampler {
     return true;
   }
 
+  // Running masses of the sorted keys s.keys[0, n) (n <= kSampThreads),
+  // into s.keys[kCumOff + e]: base0 plus the masses of [0, e] for e < n0,
+  // base1 plus those of [n0, e] for e >= n0 (two runs of the rank order,
+  // each starting from the mass of every bucket before it). One key per
+  // thread, one scan; the decisions then read them (first_reaching).
+  static constexpr int kCumOff = kCap - kSampThreads;
+  __device__ __forceinline__ void running_mass(int n, int n0, uint64_t base0, uint64_t base1) {
+    const uint64_t m = tid < n ? mass_key(key_of_rank(s.keys[tid])) : 0;
+    uint64_t incl = m;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t up = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += up;
+    }
+    if (lane == 63) s.wave_u64[wave] = incl;
+    __syncthreads();
+    for (int w = 0; w < wave; ++w) incl += s.wave_u64[w];  // the masses of [0, tid]
+    if (tid == n0 - 1) s.found_cum = incl;                  // the first run's
+    __syncthreads();
+    if (tid < n) s.keys[kCumOff + tid] = tid < n0 ? base0 + incl : base1 + incl - (n0 > 0 ? s.found_cum : 0);
+    __syncthreads();
+  }
+  // The first position e in [lo, hi) (hi - lo <= kSampThreads) whose
+  // running mass reaches the target (>= with ge, else >), or -1; the
+  // running masses never decrease along [lo, hi).
+  __device__ __forceinline__ int first_reaching(int lo, int hi, bool ge, double target) {
+    if (tid == 0) s.found_index = -1;
+    __syncthreads();
+    auto reached = [&](int e) {
+      const double c = static_cast<double>(s.keys[kCumOff + e]);
+      return ge ? c >= target : c > target;
+    };
+    const int e = lo + tid;
+    if (e < hi && reached(e) && (e == lo || !reached(e - 1))) s.found_index = e;
+    __syncthreads();
+    const int pos = static_cast<int>(s.found_index);
+    __syncthreads();
+    return pos;
+  }
+
   // The decisions on the sorted top ranks [0, n): top-k keeps the first
   // lim_k, top-p the ranks through the first whose running mass exceeds
   // p * Z (z: the kept mass when known from the histogram, else summed
   // here), the pick is the first kept rank reaching u * (kept mass).
   __device__ __forceinline__ int64_t decide_on_prefix(int n, int lim_k, bool z_known, uint64_t z, double p, double u) {
-    uint64_t cum, tot;
     const int lk = lim_k >= 0 ? lim_k : n;
-    if (!z_known) {
-      scan_sorted(lk, 0, true, -1.0, cum, tot);
-      z = tot;
-    }
+    running_mass(n, n, 0, 0);
+    if (!z_known) z = lk > 0 ? s.keys[kCumOff + lk - 1] : 0;
     int lim = lk;
     uint64_t kept = z;
-    const int pos_p = scan_sorted(lk, 0, false, p * static_cast<double>(z), cum, tot);
+    const int pos_p = first_reaching(0, lk, false, p * static_cast<double>(z));
     if (pos_p >= 0) {
       lim = pos_p + 1;
-      kept = cum;
+      kept = s.keys[kCumOff + pos_p];
     }
-    const int pos = scan_sorted(lim, 0, true, u * static_cast<double>(kept), cum, tot);
+    const int pos = first_reaching(0, lim, true, u * static_cast<double>(kept));
     if (pos < 0) return -1;
     const int64_t token = static_cast<uint32_t>(s.keys[pos]);
     __syncthreads();
@@ -1323,23 +1359,18 @@ struct RowSampler {
     __syncthreads();
     if (s.n_gather != n) return false;  // (the histogram's own counts: never expected to differ)
     sort_keys(static_cast<int>(n));
-    uint64_t cum, tot;
-    const int pos = scan_sorted(static_cast<int>(s.cnt[bp]), s.pmass[bp], false, p * static_cast<double>(z), cum,
-                                tot, static_cast<int>(n_u));
+    // Rank order: buckets blo .. last, then bp; the running mass of each
+    // run starts from the mass of the buckets before it, and never
+    // decreases along the list (the buckets between last and bp, if any,
+    // come after the pick). The cut: the first of bp's keys past p * Z; the
+    // pick: the first key through the cut reaching u * (the kept mass).
+    running_mass(static_cast<int>(n), static_cast<int>(n_u), n_u > 0 ? s.pmass[blo] : 0, s.pmass[bp]);
+    const int pos = first_reaching(static_cast<int>(n_u), static_cast<int>(n), false, p * static_cast<double>(z));
     if (pos < 0) return false;
-    const uint64_t kept = cum;
-    const double tu = u * static_cast<double>(kept);
-    int bu = bp;
-    for (int b = blo; b <= last; ++b)
-      if (s.cnt[b] > 0 && static_cast<double>(s.pmass[b] + s.wsum[b]) >= tu) {
-        bu = b;
-        break;
-      }
-    const int lim = bu == bp ? pos + 1 : static_cast<int>(s.cnt[bu]);
-    const int off = bu == bp ? static_cast<int>(n_u) : static_cast<int>(s.pcnt[bu] - s.pcnt[blo]);
-    const int pos2 = scan_sorted(lim, s.pmass[bu], true, tu, cum, tot, off);
+    const uint64_t kept = s.keys[kCumOff + pos];
+    const int pos2 = first_reaching(0, pos + 1, true, u * static_cast<double>(kept));
     if (pos2 < 0) return false;
-    token = static_cast<uint32_t>(s.keys[off + pos2]);
+    token = static_cast<uint32_t>(s.keys[pos2]);
     __syncthreads();
     return true;
   }
@@ -1392,8 +1423,10 @@ struct RowSampler {
       });
     }
     __syncthreads();
-    if (srow >= 0) scan2(s.wsum, s.pmass);  // (pcnt came with the partials)
-    else scan2_hist();
+    // (for a split row this recomputes the count prefix the merge summed,
+    // with the mass prefix: one scan, and the kernel stays in 124 VGPRs
+    // where a mass-only scan here made it spill)
+    scan2_hist();
     int cached = -1;
     uint64_t cum, tot;
     // top-k: bucket bk holds rank k - 1; its first need_k sorted elements stay.
