@@ -1768,20 +1768,34 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a)
                 static_cast<unsigned long long>(mass_of(kv, kmax, kc)));
     }
   };
-  // With bucket lists the segment (at most kSegListMax elements) stays in
-  // registers for both passes: KEEP chunks per thread, all loaded at once.
+  // With bucket lists the segment (at most kSegListMax elements) is
+  // loaded at once, KEEP chunks per thread, and each element's count atomic
+  // returns its place among its bucket's elements in the segment: the
+  // thread keeps (bucket << 16 | place) for each of its elements, so the
+  // list pass needs neither the logits nor another atomic.
   constexpr int KEEP = (kSegListMax / 8 + kSplitThreads - 1) / kSplitThreads;
+  static_assert(kSegListMax <= 65536 && kBuckets <= 65536, "a bucket and a place share 32 bits");
   const bool lists = a.pidx != nullptr;
-  u32x4 seg_w[KEEP];
+  uint32_t bp_el[KEEP][8];
   if (lists) {
+    u32x4 seg_w[KEEP];
 #pragma unroll
     for (int j = 0; j < KEEP; ++j) {
       const int ch = c0 + tid + j * kSplitThreads;
       seg_w[j] = ch < c1 ? r4[ch] : u32x4{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int j = 0; j < KEEP; ++j)
-      if (c0 + tid + j * kSplitThreads < c1) add(seg_w[j]);
+    for (int j = 0; j < KEEP; ++j) {
+      if (c0 + tid + j * kSplitThreads >= c1) continue;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float kv = (e & 1) ? hi_f<T>(seg_w[j][e >> 1]) : lo_f<T>(seg_w[j][e >> 1]);
+        const int b = RowSampler<T, true>::bucket0(kv, kmax, scale);
+        bp_el[j][e] = (static_cast<uint32_t>(b) << 16) | atomicAdd(&cnt[b], 1u);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&msum[b]),
+                  static_cast<unsigned long long>(mass_of(kv, kmax, kc)));
+      }
+    }
   } else {
     each_chunk(r4, c0 + tid, c1, kSplitThreads, [&](const u32x4 w, int) { add(w); });
   }
@@ -1816,22 +1830,14 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a)
   }
   if (!lists) return;
   __syncthreads();
-  // Each element's index at its bucket's next place. A chunk's 8 places
-  // are claimed before any is written, so the writes wait for the claims
-  // once per chunk, not once per element.
+  // Each element's index at its bucket's first place plus its own.
 #pragma unroll
   for (int j = 0; j < KEEP; ++j) {
     const int ch = c0 + tid + j * kSplitThreads;
     if (ch >= c1) continue;
-    const u32x4 w = seg_w[j];
-    uint32_t at[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float kv = (e & 1) ? hi_f<T>(w[e >> 1]) : lo_f<T>(w[e >> 1]);
-      at[e] = atomicAdd(&cnt[RowSampler<T, true>::bucket0(kv, kmax, scale)], 1u);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) list[at[e]] = static_cast<uint16_t>(8 * (ch - c0) + e);
+    for (int e = 0; e < 8; ++e)
+      list[cnt[bp_el[j][e] >> 16] + (bp_el[j][e] & 0xFFFFu)] = static_cast<uint16_t>(8 * (ch - c0) + e);
   }
   __syncthreads();
   u32x4* const dst = reinterpret_cast<u32x4*>(a.pidx + (static_cast<size_t>(r) * a.S + seg) * a.segcap);
