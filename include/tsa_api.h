@@ -253,8 +253,11 @@ size_t tsa_sample_tokens_workspace_bytes(int64_t batch, int64_t vocab);
  * path (temperature > 0 and not top-k/greedy candidate rows: the server's
  * default top-p request among them) have their statistics and histogram
  * passes spread over several workgroups per row (two more launches on
- * `stream`); the tokens are those of tsa_sample_tokens. Calls that share a
- * workspace must be ordered on one stream. */
+ * `stream`); for batches of up to about 85 such rows the histogram pass
+ * also leaves each segment's elements sorted by bucket in the workspace,
+ * and the decision gathers from those lists (about 32 MB of workspace at
+ * 64 x 151936). The tokens are those of tsa_sample_tokens. Calls that
+ * share a workspace must be ordered on one stream. */
 int tsa_sample_tokens_ws(const tsa_view* out, const tsa_view* logits, const tsa_view* temperature,
                          const tsa_view* top_k, const tsa_view* top_p, const tsa_view* uniforms,
                          void* workspace, size_t workspace_bytes, void* stream);
