@@ -354,14 +354,17 @@ def _one_workgroup(logits, temperature, top_k, top_p, uniforms):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("b", [1, 3, 64, 256])
+@pytest.mark.parametrize("b", [1, 3, 64, 85, 86, 256])
 def test_split_rows_match_one_workgroup(dtype, b):
     """A batch of at most 256 rows of >= 16384 16-bit logits spreads its
     histogram rows' statistics and histogram passes over several workgroups
-    per row (16 segments at b = 1 and 3, 8 at 64, 2 at 256): token for token
-    the one-workgroup path's, for rows of every kind (the server's default
-    request, top-p only, full, top_k > 512 with top-p, top-k and greedy rows
-    that take the candidate pass)."""
+    per row (16 segments at b = 1 and 3, 8 at 64, 6 at 85, 5 at 86, 2 at
+    256), and up to b = 85 (segments of at most 28,160 logits) the
+    histogram pass also writes each segment's bucket lists, which the
+    decision gathers from: token for token the one-workgroup path's, for
+    rows of every kind (the server's default request, top-p only, full,
+    top_k > 512 with top-p, top-k and greedy rows that take the candidate
+    pass)."""
     g = torch.Generator().manual_seed(31 + b)
     v = 151936
     logits = torch.randn(b, v, generator=g) * 2.5
