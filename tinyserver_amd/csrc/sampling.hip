@@ -1745,6 +1745,22 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a)
   const int seg = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float temp = a.temp[r * a.temp_s];
   if (!split_row(a, temp, load_int(a.topk, a.topk_dt, r * a.topk_s))) return;
+  int c0, c1;
+  split_range(a, seg, c0, c1);
+  const u32x4* r4 = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.logits) + r * a.ls0);
+  // With bucket lists the segment (at most kSegListMax elements) is
+  // loaded at once, KEEP chunks per thread, before the row's statistics
+  // records (which the loads do not need): both arrive in one round trip.
+  constexpr int KEEP = (kSegListMax / 8 + kSplitThreads - 1) / kSplitThreads;
+  const bool lists = a.pidx != nullptr;
+  u32x4 seg_w[KEEP];
+  if (lists) {
+#pragma unroll
+    for (int j = 0; j < KEEP; ++j) {
+      const int ch = c0 + tid + j * kSplitThreads;
+      seg_w[j] = ch < c1 ? r4[ch] : u32x4{0, 0, 0, 0};
+    }
+  }
   const ChunkStats st = split_stats(a, r);
   const float t = fmaxf(temp, 1e-5f);
   if (st.inan < static_cast<int>(a.V) || !(fabsf(__fdiv_rn(st.mx, t)) < INFINITY)) return;  // (uniform)
@@ -1755,9 +1771,6 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a)
     msum[b] = 0;
   }
   __syncthreads();
-  int c0, c1;
-  split_range(a, seg, c0, c1);
-  const u32x4* r4 = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.logits) + r * a.ls0);
   auto add = [&](const u32x4 w) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -1768,22 +1781,13 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a)
                 static_cast<unsigned long long>(mass_of(kv, kmax, kc)));
     }
   };
-  // With bucket lists the segment (at most kSegListMax elements) is
-  // loaded at once, KEEP chunks per thread, and each element's count atomic
-  // returns its place among its bucket's elements in the segment: the
-  // thread keeps (bucket << 16 | place) for each of its elements, so the
-  // list pass needs neither the logits nor another atomic.
-  constexpr int KEEP = (kSegListMax / 8 + kSplitThreads - 1) / kSplitThreads;
+  // With bucket lists each element's count atomic returns its place among
+  // its bucket's elements in the segment: the thread keeps (bucket << 16 |
+  // place) for each of its elements, so the list pass needs neither the
+  // logits nor another atomic.
   static_assert(kSegListMax <= 65536 && kBuckets <= 65536, "a bucket and a place share 32 bits");
-  const bool lists = a.pidx != nullptr;
   uint32_t bp_el[KEEP][8];
   if (lists) {
-    u32x4 seg_w[KEEP];
-#pragma unroll
-    for (int j = 0; j < KEEP; ++j) {
-      const int ch = c0 + tid + j * kSplitThreads;
-      seg_w[j] = ch < c1 ? r4[ch] : u32x4{0, 0, 0, 0};
-    }
 #pragma unroll
     for (int j = 0; j < KEEP; ++j) {
       if (c0 + tid + j * kSplitThreads >= c1) continue;
