@@ -68,6 +68,7 @@ struct SampleArgs {
   // bucket lists (pidx non-null) also its elements' indices, relative to
   // the segment's first element, in bucket order (segcap each).
   struct SplitStat* stat;
+  struct SplitStat* mstat;  // per row: the merge of its S records (sample_split_hist, segment 0)
   uint32_t* plp;
   uint64_t* pmass;
   int S;
@@ -1375,42 +1376,49 @@ struct RowSampler {
     return true;
   }
 
+  // The shared histogram of split row srow: the sum of its S partials
+  // (sample_split_hist: the same buckets and masses), into s.pcnt (the
+  // count prefix) and s.wsum, then s.cnt. Made before the row's statistics
+  // are used (it needs none of them), so its loads share a round trip with
+  // the statistics record's.
+  __device__ __forceinline__ void merge_partials() {
+    // The segments' count prefixes add up to the row's (pcnt), and a
+    // bucket's count is the step to the next bucket's prefix (the last
+    // bucket's to V: every element is in one bucket).
+    const size_t base = static_cast<size_t>(srow) * a.S * kBuckets;
+    for (int b = tid; b < kBuckets; b += kSampThreads) {
+      uint32_t c = 0;
+      uint64_t m = 0;
+      // Eight segments per step, every load (at a clamped segment) issued
+      // before any is summed: one step for the usual 8 segments.
+      for (int w0 = 0; w0 < a.S; w0 += 8) {
+        uint32_t cw[8];
+        uint64_t mw[8];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          const size_t at = base + static_cast<size_t>(min(w0 + w, a.S - 1)) * kBuckets + b;
+          cw[w] = a.plp[at];
+          mw[w] = a.pmass[at];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          c += w0 + w < a.S ? cw[w] : 0u;
+          m += w0 + w < a.S ? mw[w] : uint64_t{0};
+        }
+      }
+      s.pcnt[b] = c;
+      s.wsum[b] = m;
+    }
+    __syncthreads();
+    for (int b = tid; b < kBuckets; b += kSampThreads)
+      s.cnt[b] = (b + 1 < kBuckets ? s.pcnt[b + 1] : static_cast<uint32_t>(a.V)) - s.pcnt[b];
+  }
+
   __device__ __forceinline__ bool fast(float lo, int64_t k, bool cut_k, double p, double u, int64_t& token) {
     // lo: the smallest finite key
     const float scale = kmax > lo ? static_cast<float>(kBuckets - 1) / (kmax - lo) : 0.f;
-    if (srow >= 0) {  // the sum of the row's split partials (sample_split_hist, same buckets and masses)
-      // The segments' count prefixes add up to the row's (pcnt), and a
-      // bucket's count is the step to the next bucket's prefix (the last
-      // bucket's to V: every element is in one bucket).
-      const size_t base = static_cast<size_t>(srow) * a.S * kBuckets;
-      for (int b = tid; b < kBuckets; b += kSampThreads) {
-        uint32_t c = 0;
-        uint64_t m = 0;
-        // Eight segments per step, every load (at a clamped segment) issued
-        // before any is summed: one step for the usual 8 segments.
-        for (int w0 = 0; w0 < a.S; w0 += 8) {
-          uint32_t cw[8];
-          uint64_t mw[8];
-#pragma unroll
-          for (int w = 0; w < 8; ++w) {
-            const size_t at = base + static_cast<size_t>(min(w0 + w, a.S - 1)) * kBuckets + b;
-            cw[w] = a.plp[at];
-            mw[w] = a.pmass[at];
-          }
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int w = 0; w < 8; ++w) {
-            c += w0 + w < a.S ? cw[w] : 0u;
-            m += w0 + w < a.S ? mw[w] : uint64_t{0};
-          }
-        }
-        s.pcnt[b] = c;
-        s.wsum[b] = m;
-      }
-      __syncthreads();
-      for (int b = tid; b < kBuckets; b += kSampThreads)
-        s.cnt[b] = (b + 1 < kBuckets ? s.pcnt[b + 1] : static_cast<uint32_t>(a.V)) - s.pcnt[b];
-    } else {
+    if (srow < 0) {  // (a split row's partials were merged by merge_partials)
       for (int b = tid; b < kBuckets; b += kSampThreads) {
         s.cnt[b] = 0;
         s.wsum[b] = 0;
@@ -1762,6 +1770,7 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a)
     }
   }
   const ChunkStats st = split_stats(a, r);
+  if (seg == 0 && tid == 0) a.mstat[r] = SplitStat{st.mx, st.mn, st.fmn, st.imx, st.imn, st.inan, {0, 0}};
   const float t = fmaxf(temp, 1e-5f);
   if (st.inan < static_cast<int>(a.V) || !(fabsf(__fdiv_rn(st.mx, t)) < INFINITY)) return;  // (uniform)
   const float kmax = st.mx, kc = 1.4426950408889634f / t, lo = fminf(st.fmn, st.mx);
@@ -1890,7 +1899,12 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   float mx = -INFINITY, mn = INFINITY, fmn = INFINITY;
   int imx = static_cast<int>(a.V), imn = -1, inan = static_cast<int>(a.V);
   if (split) {
-    const ChunkStats st = split_stats(a, r);
+    // The row's merged statistics record (sample_split_hist's segment 0
+    // wrote it), then the partials' merge, which needs none of it: the
+    // record's load and the partials' share one round trip.
+    const SplitStat st = a.mstat[r];
+    rs.srow = r;
+    rs.merge_partials();
     mx = st.mx;
     mn = st.mn;
     fmn = st.fmn;
@@ -1981,7 +1995,6 @@ __global__ __launch_bounds__(kSampThreads) void sample_tokens_kernel(SampleArgs 
   const double p = a.topp[r * a.topp_s];
   const double u = a.unif[r * a.unif_s];
   int64_t token;
-  if (split) rs.srow = r;
   if (rs.fast(klo, k, cut_k, p, u, token)) {
     if (tid == 0) *out = token;
     return;
@@ -2057,14 +2070,16 @@ int64_t seg_elems(int64_t V, int S) { return 8 * (((V >> 3) + S - 1) / S); }
 bool split_lists(int64_t V, int S) { return S > 1 && seg_elems(V, S) <= kSegListMax; }
 
 // Workspace of a split launch, each region 256-byte aligned: the statistics
-// records, the partial count prefixes and masses, and the bucket lists.
+// records and each row's merged one, the partial count prefixes and masses,
+// and the bucket lists.
 struct SplitLayout {
-  size_t plp, pmass, pidx, total;
+  size_t mstat, plp, pmass, pidx, total;
 };
 SplitLayout split_layout(int64_t B, int64_t V, int S) {
   const size_t segs = static_cast<size_t>(B) * S;
   SplitLayout l{};
-  l.plp = align256(segs * sizeof(SplitStat));
+  l.mstat = align256(segs * sizeof(SplitStat));
+  l.plp = l.mstat + align256(static_cast<size_t>(B) * sizeof(SplitStat));
   l.pmass = l.plp + align256(segs * kBuckets * sizeof(uint32_t));
   l.pidx = l.pmass + segs * kBuckets * sizeof(uint64_t);
   l.total = l.pidx;
@@ -2116,6 +2131,7 @@ int sample_impl(const tsa_view* out, const tsa_view* logits, const tsa_view* tem
     const SplitLayout l = split_layout(B, V, S);
     char* w = static_cast<char*>(workspace);
     a.stat = reinterpret_cast<SplitStat*>(w);
+    a.mstat = reinterpret_cast<SplitStat*>(w + l.mstat);
     a.plp = reinterpret_cast<uint32_t*>(w + l.plp);
     a.pmass = reinterpret_cast<uint64_t*>(w + l.pmass);
     if (split_lists(V, S)) {
