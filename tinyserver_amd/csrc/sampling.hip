@@ -198,6 +198,41 @@ struct ChunkStats {
   }
 };
 
+// Inclusive scan over a wave's 64 lanes on DPP moves (no LDS round trip):
+// sums within rows of 16 lanes (row shifts by 1, 2, 4, 8; a lane whose
+// source lies before its row's start reads 0), then lane 15's sum added to
+// row 1 and lane 47's to row 3 (row_bcast:15), then lane 31's to rows 2
+// and 3 (row_bcast:31). These lane mappings were checked on the GPU. Every
+// lane of the wave must take part.
+template <int CTRL, int ROWS, bool BC>
+__device__ __forceinline__ uint32_t dpp32(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, ROWS, 0xf, BC));
+}
+template <int CTRL, int ROWS, bool BC>
+__device__ __forceinline__ uint64_t dpp64(uint64_t x) {
+  const uint32_t lo = dpp32<CTRL, ROWS, BC>(static_cast<uint32_t>(x));
+  const uint32_t hi = dpp32<CTRL, ROWS, BC>(static_cast<uint32_t>(x >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x) {
+  x += dpp32<0x111, 0xf, true>(x);
+  x += dpp32<0x112, 0xf, true>(x);
+  x += dpp32<0x114, 0xf, true>(x);
+  x += dpp32<0x118, 0xf, true>(x);
+  x += dpp32<0x142, 0xa, false>(x);
+  x += dpp32<0x143, 0xc, false>(x);
+  return x;
+}
+__device__ __forceinline__ uint64_t wave_scan_u64(uint64_t x) {
+  x += dpp64<0x111, 0xf, true>(x);
+  x += dpp64<0x112, 0xf, true>(x);
+  x += dpp64<0x114, 0xf, true>(x);
+  x += dpp64<0x118, 0xf, true>(x);
+  x += dpp64<0x142, 0xa, false>(x);
+  x += dpp64<0x143, 0xc, false>(x);
+  return x;
+}
+
 __device__ __forceinline__ int64_t load_int(const void* p, int dt, int64_t i) {
   return dt == TSA_I64 ? static_cast<const int64_t*>(p)[i] : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
 }
@@ -423,10 +458,7 @@ struct RowSampler {
   __device__ __forceinline__ void scan_buckets() {
     const uint64_t w0 = s.wsum[2 * tid], w1 = s.wsum[2 * tid + 1];
     uint64_t incl = w0 + w1;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t up = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += up;
-    }
+    incl = wave_scan_u64(incl);
     __syncthreads();
     if (lane == 63) s.wave_u64[wave] = incl;
     __syncthreads();
@@ -515,10 +547,7 @@ struct RowSampler {
   __device__ __forceinline__ void scan2(const U* in, U* out) {
     const U w0 = in[2 * tid], w1 = in[2 * tid + 1];
     uint64_t incl = static_cast<uint64_t>(w0) + w1;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t up = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += up;
-    }
+    incl = wave_scan_u64(incl);
     __syncthreads();
     if (lane == 63) s.wave_u64[wave] = incl;
     __syncthreads();
@@ -537,14 +566,8 @@ struct RowSampler {
     const uint64_t m0 = s.wsum[2 * tid], m1 = s.wsum[2 * tid + 1];
     int64_t ic = static_cast<int64_t>(c0) + c1;
     uint64_t im = m0 + m1;
-    for (int o = 1; o < 64; o <<= 1) {
-      const int64_t upc = __shfl_up(ic, o, 64);
-      const uint64_t upm = __shfl_up(im, o, 64);
-      if (lane >= o) {
-        ic += upc;
-        im += upm;
-      }
-    }
+    ic = static_cast<int64_t>(wave_scan_u64(static_cast<uint64_t>(ic)));
+    im = wave_scan_u64(im);
     __syncthreads();
     if (lane == 63) {
       s.wave_i[wave] = ic;
@@ -766,10 +789,7 @@ struct RowSampler {
   __device__ __forceinline__ void running_mass(int n, int n0, uint64_t base0, uint64_t base1) {
     const uint64_t m = tid < n ? mass_key(key_of_rank(s.keys[tid])) : 0;
     uint64_t incl = m;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t up = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += up;
-    }
+    incl = wave_scan_u64(incl);
     if (lane == 63) s.wave_u64[wave] = incl;
     __syncthreads();
     for (int w = 0; w < wave; ++w) incl += s.wave_u64[w];  // the masses of [0, tid]
@@ -829,10 +849,7 @@ struct RowSampler {
     uint64_t mine = 0;
     for (int e = e0; e < e1; ++e) mine += mass_key(key_of_rank(s.keys[e]));  // no reload of the row
     uint64_t incl = mine;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t up = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += up;
-    }
+    incl = wave_scan_u64(incl);
     __syncthreads();
     if (lane == 63) s.wave_u64[wave] = incl;
     if (tid == 0) s.found_index = -1;
@@ -1016,10 +1033,7 @@ struct RowSampler {
     const uint32_t h0 = hist[b0], h1 = hist[b0 - 1], h2 = hist[b0 - 2], h3 = hist[b0 - 3];
     const uint32_t mine = h0 + h1 + h2 + h3;
     uint32_t incl = mine;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t up = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += up;
-    }
+    incl = wave_scan_u32(incl);
     if (lane == 63) red[32 + wave] = incl;
     __syncthreads();
     uint32_t excl = incl - mine;
@@ -1220,10 +1234,7 @@ struct RowSampler {
                                                   double u) const {
     const uint64_t m = lane < lk ? mass_of(cand_value(sorted), km, kcv) : 0;
     uint64_t incl = m;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t up = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += up;
-    }
+    incl = wave_scan_u64(incl);
     const uint64_t excl = incl - m;
     const uint64_t z = __shfl(incl, 63, 64);
     const double tp = p * static_cast<double>(z);
@@ -1256,10 +1267,7 @@ struct RowSampler {
       mine += m[i];
     }
     uint64_t incl = mine;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t up = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += up;
-    }
+    incl = wave_scan_u64(incl);
     const uint64_t z = __shfl(incl, 63, 64);
     // top-p: the first rank whose running mass exceeds p * z (exactly one lane holds it)
     const double tp = p * static_cast<double>(z);
@@ -1581,10 +1589,7 @@ struct RowSampler {
         uint64_t mine = 0;
         for (int e = e0; e < e1; ++e) mine += by_mass ? mass(x_at(static_cast<uint32_t>(s.keys[e]))) : 1;
         uint64_t incl = mine;
-        for (int o = 1; o < 64; o <<= 1) {
-          const uint64_t up = __shfl_up(incl, o, 64);
-          if (lane >= o) incl += up;
-        }
+        incl = wave_scan_u64(incl);
         __syncthreads();
         if (lane == 63) s.wave_u64[wave] = incl;
         if (tid == 0) s.found_index = -1;
@@ -1649,10 +1654,7 @@ struct RowSampler {
         uint64_t mine = 0;  // members in this thread's run
         for (int64_t i = i0; i < i1; ++i) mine += member(i, x_at(i)) ? 1 : 0;
         uint64_t incl = mine;
-        for (int o = 1; o < 64; o <<= 1) {
-          const uint64_t up = __shfl_up(incl, o, 64);
-          if (lane >= o) incl += up;
-        }
+        incl = wave_scan_u64(incl);
         __syncthreads();
         if (lane == 63) s.wave_u64[wave] = incl;
         if (tid == 0) s.found_index = -1;
@@ -1827,10 +1829,7 @@ __global__ __launch_bounds__(kSplitThreads) void sample_split_hist(SampleArgs a)
     run += v[i];
   }
   uint32_t incl = run;
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t up = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += up;
-  }
+  incl = wave_scan_u32(incl);
   if (lane == 63) wtot[wave] = incl;
   __syncthreads();
   uint32_t before = incl - run;
