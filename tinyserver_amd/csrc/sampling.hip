@@ -233,6 +233,68 @@ __device__ __forceinline__ uint64_t wave_scan_u64(uint64_t x) {
   return x;
 }
 
+// The value held by lane (lane ^ J), for J a power of two below 64, without
+// an LDS round trip: quad permutes [1,0,3,2] and [2,3,0,1] for 1 and 2, a
+// row rotation by 8 for 8, rotations by 4 and 12 with a per-lane choice for
+// 4, and the half-row and half-wave swaps (v_permlane16_swap,
+// v_permlane32_swap, whose second result is the partner's value in the
+// lower half and whose first is it in the upper half) for 16 and 32. These
+// lane mappings were checked on the GPU. Every lane of the wave must take
+// part.
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane32(uint32_t v, int lane) {
+  if constexpr (J == 1) {
+    return dpp32<0xB1, 0xf, false>(v);
+  } else if constexpr (J == 2) {
+    return dpp32<0x4E, 0xf, false>(v);
+  } else if constexpr (J == 4) {
+    // (row_ror:n: lane l reads lane (l - n) mod 16 of its row.)
+    const uint32_t up = dpp32<0x12C, 0xf, false>(v), down = dpp32<0x124, 0xf, false>(v);
+    return (lane & 4) ? down : up;
+  } else if constexpr (J == 8) {
+    return dpp32<0x128, 0xf, false>(v);
+  } else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    static_assert(J == 32, "xor_lane32: J in {1, 2, 4, 8, 16, 32}");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+template <int J>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v, int lane) {
+  const uint32_t lo = xor_lane32<J>(static_cast<uint32_t>(v), lane);
+  const uint32_t hi = xor_lane32<J>(static_cast<uint32_t>(v >> 32), lane);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// One compare-exchange stage (K, J) of a bitonic sort of 64 keys held one
+// per lane, ascending over the lanes when the network is done.
+template <int K, int J>
+__device__ __forceinline__ uint64_t bitonic_stage(uint64_t x, int lane) {
+  const uint64_t y = xor_lane64<J>(x, lane);
+  const bool keep_min = ((lane & J) == 0) == ((lane & K) == 0);
+  return keep_min == (x < y) ? x : y;
+}
+template <int K>
+__device__ __forceinline__ uint64_t bitonic_merge(uint64_t x, int lane) {
+  if constexpr (K >= 64) x = bitonic_stage<K, 32>(x, lane);
+  if constexpr (K >= 32) x = bitonic_stage<K, 16>(x, lane);
+  if constexpr (K >= 16) x = bitonic_stage<K, 8>(x, lane);
+  if constexpr (K >= 8) x = bitonic_stage<K, 4>(x, lane);
+  if constexpr (K >= 4) x = bitonic_stage<K, 2>(x, lane);
+  return bitonic_stage<K, 1>(x, lane);
+}
+__device__ __forceinline__ uint64_t wave_sort_u64(uint64_t x, int lane) {
+  x = bitonic_merge<2>(x, lane);
+  x = bitonic_merge<4>(x, lane);
+  x = bitonic_merge<8>(x, lane);
+  x = bitonic_merge<16>(x, lane);
+  x = bitonic_merge<32>(x, lane);
+  return bitonic_merge<64>(x, lane);
+}
+
 __device__ __forceinline__ int64_t load_int(const void* p, int dt, int64_t i) {
   return dt == TSA_I64 ? static_cast<const int64_t*>(p)[i] : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
 }
@@ -267,6 +329,8 @@ constexpr int64_t kRegMaxV = int64_t{kSampThreads} * kRegChunks * 8;  // 155,648
 constexpr int64_t kFastK = 512;                                        // the largest top_k it takes
 constexpr int kWaveStage = 64;    // chunks holding a candidate one wave may stage
 constexpr int kCandOff = 4608;    // the candidates: keys[kCandOff, kCap)
+constexpr int kRunStride = 68;    // a sorted run of 64 keys with a slot after each 16 (sort_keys)
+static_assert(kRunStride * (kSampWaves - 1) + kRunStride <= kCandOff, "sorted runs stay below the candidates");
 constexpr int kGatherCap = kCap - kCandOff;
 constexpr int kSelBins = 4096;        // 12-bit key prefixes
 
@@ -475,38 +539,48 @@ struct RowSampler {
   __device__ __forceinline__ void sort_keys(int n) {
     if (n <= kSampThreads) {
       // At most one key per thread: each wave sorts its 64 (a bitonic
-      // network on lane shuffles; ~0, above every rank key, pads the last
-      // run), the sorted runs go to LDS, and a key's place is its lane plus
-      // the keys below it in every other run (a binary search of each run,
-      // the runs' searches interleaved). The keys are distinct (they hold
-      // the index).
+      // network on cross-lane register moves; ~0, above every rank key,
+      // pads the last run), the sorted runs go to LDS, and a key's place is
+      // its lane plus the keys below it in every other run. The keys are
+      // distinct (they hold the index).
+      //
+      // The count below x in a run is found by a 4-ary search in three
+      // dependent rounds, four runs' searches side by side: keys 15, 31,
+      // 47, 63 fix the block of 16, three keys in it the block of 4, three
+      // keys in that the count. A run is stored with one empty slot after
+      // each 16 keys (key e at kRunStride * run + e + e / 16), which puts
+      // the addresses of each round's reads on distinct LDS banks.
       const int runs = (n + 63) >> 6;
       uint64_t x = tid < n ? s.keys[tid] : ~uint64_t{0};
-      if (wave < runs) {
-#pragma unroll
-        for (int k = 2; k <= 64; k <<= 1)
-#pragma unroll
-          for (int j = k >> 1; j > 0; j >>= 1) {
-            const uint64_t y = __shfl_xor(x, j, 64);
-            const bool keep_min = ((lane & j) == 0) == ((lane & k) == 0);
-            x = keep_min == (x < y) ? x : y;
-          }
-      }
+      if (wave < runs) x = wave_sort_u64(x, lane);
       __syncthreads();
-      if (wave < runs) s.keys[tid] = x;
+      if (wave < runs) s.keys[kRunStride * wave + lane + (lane >> 4)] = x;
       __syncthreads();
       int rank = lane;
       if (wave < runs) {
-        for (int g = 0; g < runs; g += 4) {  // four runs' searches at a time
-          int below[4] = {0, 0, 0, 0};
+#pragma unroll 1
+        for (int g = 0; g < runs; g += 4) {
+          int below[4];
 #pragma unroll
-          for (int step = 32; step > 0; step >>= 1)
+          for (int i = 0; i < 4; ++i) {
+            below[i] = 0;
+            if (g + i < runs && g + i != wave) {
+              const uint64_t* r = &s.keys[kRunStride * (g + i)];
+              below[i] = 16 * ((r[15] < x) + (r[32] < x) + (r[49] < x) + (r[66] < x));
+            }
+          }
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (g + i < runs && g + i != wave && s.keys[64 * (g + i) + below[i] + step - 1] < x) below[i] += step;
+          for (int i = 0; i < 4; ++i)
+            if (g + i < runs && g + i != wave && below[i] < 64) {
+              const uint64_t* r = &s.keys[kRunStride * (g + i) + below[i] + (below[i] >> 4)];
+              below[i] += 4 * ((r[3] < x) + (r[7] < x) + (r[11] < x));
+            }
 #pragma unroll
-          for (int i = 0; i < 4; ++i)  // (the steps reach 63 keys: the 64th decides alone)
-            if (g + i < runs && g + i != wave && s.keys[64 * (g + i) + below[i]] < x) ++below[i];
+          for (int i = 0; i < 4; ++i)
+            if (g + i < runs && g + i != wave && below[i] < 64) {
+              const uint64_t* r = &s.keys[kRunStride * (g + i) + below[i] + (below[i] >> 4)];
+              below[i] += (r[0] < x) + (r[1] < x) + (r[2] < x);
+            }
           rank += below[0] + below[1] + below[2] + below[3];
         }
       }
