@@ -149,10 +149,13 @@ size_t tsa_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int
  * seq_lens[s] tokens gathered through block_tables[s], kv head h / (Hq/Hkv).
  * query/out: (B, Hq, D); caches (NB, Hkv, BS, D); block_tables (B, max_blocks)
  * int32; seq_lens (B,) int32. The 16-token tiles of all sequences are split
- * evenly over the 4 waves of num_workgroups workgroups (0 = one per CU); a
- * second launch merges each sequence's per-wave partial results, which the
- * workspace holds (no initialisation needed; calls that share one must be
- * ordered on one stream). */
+ * evenly over the 4 waves of num_workgroups workgroups (0 = the library's
+ * choice: one per CU, fewer for small tables); a second launch merges each
+ * sequence's per-wave partial results, which the workspace holds (no
+ * initialisation needed; calls that share one must be ordered on one
+ * stream). With num_workgroups 0, a batch of at most 64 (sequence, kv head)
+ * units whose tables hold at most 512 tokens takes one launch instead: one
+ * workgroup per unit, whose waves merge in LDS and write out. */
 int tsa_paged_decode(const tsa_view* out, const tsa_view* query, const tsa_view* k_cache,
                      const tsa_view* v_cache, const tsa_view* block_tables,
                      const tsa_view* seq_lens, double softmax_scale, void* workspace,

@@ -204,10 +204,13 @@ def test_workspace_plan():
 
 
 def test_workspace_plan_small_tables():
-    """With no grid asked for, block tables of few tiles (Hkv * B *
-    ceil(max_blocks * block_size / 16), at most 8 per default workgroup)
-    take a grid of one workgroup per 8 such tiles, at least 64: the
-    workspace holds units + 4 * workgroups partial slots."""
+    """With no grid asked for: at most 64 (sequence, kv head) units whose
+    tables hold at most 512 tokens run one workgroup per unit, whose partials
+    stay in LDS, so the workspace is the tile prefix alone. Otherwise block
+    tables of few tiles (Hkv * B * ceil(max_blocks * block_size / 16), at
+    most 8 per default workgroup) take a grid of one workgroup per 8 such
+    tiles, at least 64: the workspace holds units + 4 * workgroups partial
+    slots."""
     lib = _lib.load()
 
     def plan(b, blocks, bs=16, nwg=0):
@@ -217,9 +220,12 @@ def test_workspace_plan_small_tables():
         align = lambda n: (n + 255) // 256 * 256
         return align((b * 8 + 4 * wg) * 2 * (128 + 2) * 4) + align((b + 1) * 4)
 
-    assert plan(4, 32) == size(4, 128)  # 1024 tiles: the Qwen3-0.6B batch of 4 at contexts up to 512
-    assert plan(4, 16, bs=32) == size(4, 128)  # the same tokens in 32-token pages
-    assert plan(4, 1) == size(4, 64)  # 32 tiles: the floor of 64 workgroups
+    prefix_only = 256  # (B + 1) int32, 256-byte aligned
+    assert plan(4, 32) == prefix_only  # the Qwen3-0.6B batch of 4 at contexts up to 512: 32 units
+    assert plan(4, 16, bs=32) == prefix_only  # the same tokens in 32-token pages
+    assert plan(8, 1) == prefix_only  # 64 units
+    assert plan(4, 33) == size(4, 132)  # 528-token tables: the stream, 1056 tiles over 132 workgroups
+    assert plan(9, 1) == size(9, 64)  # 72 units: the stream, the floor of 64 workgroups
     assert plan(4, 32, nwg=200) == size(4, 200)  # a grid asked for is kept
     assert plan(64, 256) > size(64, 128)  # the Qwen3-8B batch: the default grid (one per CU)
 

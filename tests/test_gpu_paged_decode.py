@@ -4,7 +4,8 @@ The oracle restates the reference kernel (paged_attention.py:8-121) in fp32.
 Cases: the reference's own three configurations, query not mutated, shape and
 dtype, the poisoned partial last block (tests/model/test_paged_attention_kernel.py:
 109-222); the Qwen3-0.6B-shaped decode step end to end (norm+RoPE+store then
-attend); GQA groups 1..16, head_dim 64/128, page sizes 4..64; split-K with
+attend); GQA groups 1..16, head_dim 64/128, page sizes 4..64; small batches in
+one workgroup per (sequence, kv head) unit (no merge launch); split-K with
 forced small splits, called twice to show the merge counters reset; seq_len 1
 (output = the V row); the full Qwen3-8B bs64 and Qwen3-32B bs32 batches, every sequence and
 head. Tolerance for bf16/fp16: max-abs 2e-2, mean-abs 2e-3;
@@ -137,6 +138,41 @@ def test_stream_partition(num_workgroups):
         assert torch.isnan(out[5]).all(), "empty sequence must give NaN (0/0) like the reference"
         keep = [0, 1, 2, 3, 4, 6]
         assert_close(out[keep], ref[keep], what=f"W={num_workgroups} call {call}")
+
+
+UNIT_CASES = [
+    # (num_heads, num_kv_heads, head_dim, block_size, dtype, seq_lens)
+    (16, 8, 128, 16, torch.bfloat16, [0, 1, 5, 63, 300, 512]),
+    (32, 8, 128, 16, torch.float16, [17, 512, 2, 33]),
+    (8, 8, 64, 16, torch.bfloat16, [3, 64, 511, 100, 1, 16, 250]),
+    (64, 4, 128, 32, torch.bfloat16, [500, 31, 1, 96]),
+    (16, 4, 128, 8, torch.bfloat16, [7, 512, 130]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(UNIT_CASES)))
+def test_unit_form(case):
+    """With no grid asked for, a batch of at most 64 (sequence, kv head) units
+    whose block tables hold at most 512 tokens runs one workgroup per unit:
+    its four waves split the unit's tiles (some waves get none when a unit
+    has fewer than four tiles) and merge in LDS, with no merge launch. Every
+    such case here -- an empty sequence (NaN), seq_len 1, a full 512-token
+    table, head_dim 64, groups of 1 to 16 heads, 8-, 16- and 32-token pages,
+    bf16 and f16 -- against the oracle, and against the stream form that an
+    explicit grid takes."""
+    hq, hkv, d, bs, dtype, lens = UNIT_CASES[case]
+    q, kc, vc, bt, sl = _random_paged_inputs(lens, hq, hkv, d, bs, dtype, seed=60 + case)
+    assert len(lens) * hkv <= 64 and bt.shape[1] * bs <= 512
+    print(f"unit form: heads {hq}/{hkv}, head_dim {d}, page {bs}, {dtype}, lens {lens}", flush=True)
+    ref = op.paged_attention_forward(q, kc, vc, bt, bs, sl)
+    out = _run(q, kc, vc, bt, bs, sl).cpu()
+    stream = _run(q, kc, vc, bt, bs, sl, num_workgroups=16).cpu()
+    keep = [i for i, n in enumerate(lens) if n > 0]
+    for i, n in enumerate(lens):
+        if n == 0:
+            assert torch.isnan(out[i]).all(), "empty sequence must give NaN (0/0) like the reference"
+    assert_close(out[keep], ref[keep], what=f"unit form case {case}")
+    assert_close(out[keep], stream[keep], what=f"unit form vs stream form, case {case}")
 
 
 def test_workspace_reuse_across_shapes():

@@ -84,6 +84,7 @@ struct DecodeArgs {
   int32_t B, Hq, Hkv, G, BS, max_blocks, D;
   int32_t W;        // workgroups of the stream kernel
   int32_t NW;       // wave workers sharing the tile list (kWaves * W)
+  int32_t unit;     // 1: one workgroup per (sequence, kv head) unit, W = B * Hkv, no merge launch
   float scale_log2;
   float* part;      // [B * Hkv + NW][G * (D + 2)]: per (unit, worker) acc[G][D], m[G], l[G]
   int32_t* pref_out;  // [B + 1] tile prefix over the sequences, for the merge
@@ -218,7 +219,7 @@ __device__ __forceinline__ int tiles_of(const DecodeArgs& a, int s) {
 
 // Exclusive prefix of tiles per sequence into pref[0..B] (pref[B] = total),
 // computed by one wave alone into its own LDS copy: lane i sums sequences
-// [i * per, (i + 1) * per), a shuffle scan combines the lanes, and no
+// [i * per, (i + 1) * per), a DPP scan combines the lanes, and no
 // workgroup barrier is needed. Only this wave reads pref afterwards.
 __device__ void tile_prefix_wave(const DecodeArgs& a, int* pref) {
   const int lane = threadIdx.x & 63;
@@ -228,12 +229,7 @@ __device__ void tile_prefix_wave(const DecodeArgs& a, int* pref) {
     const int s = lane * per + i;
     if (s < a.B) local += tiles_of(a, s);
   }
-  int incl = local;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int up = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += up;
-  }
+  const int incl = static_cast<int>(wave_scan_u32(static_cast<uint32_t>(local)));
   int run = incl - local;  // exclusive prefix of this lane's first sequence
   for (int i = 0; i < per; ++i) {
     const int s = lane * per + i;
@@ -250,6 +246,59 @@ __device__ void tile_prefix_wave(const DecodeArgs& a, int* pref) {
 
 // Position of one wave in the global tile list (unit-major): unit (s, kvh),
 // tile t of the unit's n tiles. Wave-uniform; empty sequences are skipped.
+// One workgroup per unit: the four waves' partials (acc[G][D], m[G], l[G],
+// padded to 16 bytes) in LDS after the tile prefixes -- or, in the fused
+// step, at the start of each wave's own area, which its stream no longer
+// reads once the partial is written (no LDS DMA is in flight by then: the
+// only one, the unit's, lands before the wave's first tile is computed).
+__host__ __device__ inline int unit_slot_floats(int G, int D) { return (G * (D + 2) + 3) & ~3; }
+__host__ __device__ inline int prefix_lds_bytes16(int B) { return (kWaves * (B + 1) * 4 + 15) & ~15; }
+static_assert(kFusedWaveBytes >= 8 * (128 + 2) * 4, "a fused wave's area holds its partial (G <= 8, head_dim 128)");
+template <bool FUSED>
+__device__ __forceinline__ float* unit_slot(const DecodeArgs& a, int* lds_i, int w) {
+  char* const base = reinterpret_cast<char*>(lds_i) + prefix_lds_bytes16(a.B);
+  if constexpr (FUSED) return reinterpret_cast<float*>(base + w * kFusedWaveBytes);
+  else return reinterpret_cast<float*>(base) + w * unit_slot_floats(a.G, a.D);
+}
+
+// Workgroup barrier over the LDS partials only. The fences order LDS and not
+// global memory, so the barrier does not wait for the ring's last loads
+// (repeats of the wave's last tile, whose registers nothing reads).
+__device__ __forceinline__ void unit_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The merge of one unit's wave partials (after the workgroup barrier):
+// output (head h, dim d) combines the waves that had tiles in wave order,
+// with the running-max rescale of paged_decode_stream_merge. A unit with no
+// tiles (seq_len 0) gives 0/0 = NaN, as the reference's does.
+template <typename T, bool FUSED>
+__device__ __forceinline__ void unit_merge(const DecodeArgs& a, int* lds_i) {
+  const int Hkv = a.Hkv, G = a.G, D = a.D;
+  const int s = blockIdx.x / Hkv, kvh = blockIdx.x - s * Hkv;
+  const int n = lds_i[s + 1] - lds_i[s];  // wave 0's prefix copy
+  const int q = (n + kWaves - 1) / kWaves;
+  const int nw = n == 0 ? 0 : (n + q - 1) / q;
+  T* orow = static_cast<T*>(a.out) + s * a.o_ss + (kvh * G) * a.o_sh;
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int hd = idx / D;
+    float M = kNegInf, den = 0.f, o = 0.f;
+    for (int w = 0; w < nw; ++w) {
+      const float* sl = unit_slot<FUSED>(a, lds_i, w);
+      const float mb = sl[G * D + hd], lb = sl[G * D + G + hd], ab = sl[idx];
+      const float mn = fmaxf(M, mb);
+      if (mn == kNegInf) continue;
+      const float c_old = fast_exp2(M - mn), c_new = fast_exp2(mb - mn);
+      o = o * c_old + ab * c_new;
+      den = den * c_old + lb * c_new;
+      M = mn;
+    }
+    orow[hd * a.o_sh + (idx - hd * D) * a.o_sd] = from_float<T>(o / den);
+  }
+}
+
 struct TileCursor {
   int s, kvh, n, t;
   // Values read from the LDS prefix go through readfirstlane, so the compiler
@@ -288,11 +337,12 @@ struct TileCursor {
 // (batches whose prefixes would not fit in LDS) the waves read the tile
 // prefix that decode_tile_prefix wrote to the workspace instead, and the
 // workgroup takes no LDS.
-template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED, bool GPREF = false>
+template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED, bool GPREF = false, bool UNIT = false>
 __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* __restrict__ bt,
                                                    const int32_t* __restrict__ sl, float* __restrict__ part,
                                                    int* lds_i) {
   static_assert(!(GPREF && FUSED), "the fused step keeps its tile prefixes in LDS");
+  static_assert(!(GPREF && UNIT), "one workgroup per unit keeps its tile prefixes in LDS");
   constexpr int KJ = D / 32;  // k-steps of the score MFMA
   a.bt = bt;
   a.seq_lens = sl;
@@ -302,6 +352,16 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
   // Wave-uniform (scalar) so tile indices, block-table reads and page bases
   // stay in SGPRs and the table lookups are scalar loads.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // One workgroup per unit, 16-token pages: lane i holds the unit's block-table
+  // entry i, loaded beside the sequence lengths, and each tile's page id is a
+  // lane read rather than a dependent scalar load. (The plan takes this form
+  // only for tables of at most 64 tiles per unit, so 16-token or larger pages
+  // give at most 64 entries.)
+  int btv = 0;
+  if constexpr (UNIT && PAGE16) {
+    const int us = blockIdx.x / Hkv;
+    if (lane < a.max_blocks) btv = bt[us * a.bt_s0 + lane * a.bt_s1];
+  }
   const int* pref;
   if constexpr (GPREF) {
     pref = a.pref_out;  // [B + 1], written by decode_tile_prefix before this launch
@@ -326,12 +386,26 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
     dma16(src, __builtin_amdgcn_readfirstlane(lds_byte));
   };
 
-  const int64_t total = static_cast<int64_t>(Hkv) * pref[a.B];
-  const int64_t share = (total + a.NW - 1) / a.NW;
   const int v = blockIdx.x * kWaves + wave;
-  const int64_t lo = static_cast<int64_t>(v) * share;
-  const int64_t hi = min(total, lo + share);
-  if (lo >= hi) return;  // no barrier follows: waves leave independently
+  int64_t lo, hi;
+  if constexpr (UNIT) {
+    // Workgroup u takes unit (u / Hkv, u % Hkv); wave w its w-th quarter
+    // of the unit's n tiles (ceil(n / kWaves) each, the last waves fewer or
+    // none). The wave's partial goes to LDS and the workgroup merges.
+    const int us = blockIdx.x / Hkv, ukvh = blockIdx.x - us * Hkv;
+    const int n = __builtin_amdgcn_readfirstlane(pref[us + 1] - pref[us]);
+    const int q = (n + kWaves - 1) / kWaves;
+    const int64_t u0 = static_cast<int64_t>(Hkv) * __builtin_amdgcn_readfirstlane(pref[us]) +
+                       static_cast<int64_t>(ukvh) * n;
+    lo = u0 + min(n, wave * q);
+    hi = u0 + min(n, (wave + 1) * q);
+  } else {
+    const int64_t total = static_cast<int64_t>(Hkv) * pref[a.B];
+    const int64_t share = (total + a.NW - 1) / a.NW;
+    lo = static_cast<int64_t>(v) * share;
+    hi = min(total, lo + share);
+  }
+  if (lo >= hi) return;  // no barrier follows (one workgroup per unit: the caller's barrier)
   const int n_tiles = static_cast<int>(hi - lo);
   if constexpr (FUSED) {  // weights: lanes 0-15 q_weight, 16-31 k_weight (32-63 repeat them)
     const T* wsrc = static_cast<const T*>((lane & 16) ? a.kw : a.qw) + 8 * (lane & 15);
@@ -386,6 +460,17 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
     slot = tok - lb * a.BS;
     return phys >= 0 && phys < a.NB;
   };
+  // The page of a tile's first token (tok wave-uniform).
+  auto tile_page = [&](const int32_t* bt_row, int64_t tok, int64_t& phys, int64_t& slot) -> bool {
+    if constexpr (UNIT && PAGE16) {
+      const int lb = static_cast<int>(tok / a.BS);
+      phys = __builtin_amdgcn_readlane(btv, lb);
+      slot = tok - static_cast<int64_t>(lb) * a.BS;
+      return phys >= 0 && phys < a.NB;
+    } else {
+      return page_of(bt_row, tok, phys, slot);
+    }
+  };
 
   // One tile's operands: Q^T (lane (g, c): head c, dims 8(g + 4j)..+8), the K
   // operand (token c of the tile, same dims) and V rows (tokens 4g..4g+3).
@@ -410,7 +495,7 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
     const int64_t tok0 = static_cast<int64_t>(tc.t) * 16;
     if constexpr (PAGE16) {
       int64_t phys, slot0;
-      if (!page_of(bt_row, tok0, phys, slot0)) phys = 0;
+      if (!tile_page(bt_row, tok0, phys, slot0)) phys = 0;
       const T* kp = kbase + phys * a.kc_b + (slot0 + c) * ks + 8 * g;
 #pragma unroll
       for (int j = 0; j < KJ; ++j) ko[j] = load_stream<NT>(kp + 32 * j);
@@ -451,7 +536,7 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
     int64_t lim = tc.t + 1 < tc.n ? tok0 + 16 : clamp_len(a, tc.s);
     if constexpr (PAGE16) {
       int64_t phys, slot0;
-      if (!page_of(a.bt + tc.s * a.bt_s0, tok0, phys, slot0)) lim = tok0;
+      if (!tile_page(a.bt + tc.s * a.bt_s0, tok0, phys, slot0)) lim = tok0;
     }
     if (tok0 + 16 > lim) {
 #pragma unroll
@@ -470,8 +555,9 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
       sv[r] = tb + r < lim ? sc[r] * a.scale_log2 : kNegInf;
       tmax = fmaxf(tmax, sv[r]);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    // (across the 4 row groups: lane swaps, no LDS round trip)
+    tmax = fmaxf(tmax, __builtin_bit_cast(float, xor_lane32<16>(__builtin_bit_cast(uint32_t, tmax), lane)));
+    tmax = fmaxf(tmax, __builtin_bit_cast(float, xor_lane32<32>(__builtin_bit_cast(uint32_t, tmax), lane)));
     const float m_new = fmaxf(m, tmax);
     if (__any(m_new > m)) {
       const float alpha = m_new == kNegInf ? 1.f : fast_exp2(m - m_new);  // 0 on the first tile
@@ -521,7 +607,9 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
     float lt = l;
     lt += __shfl_xor(lt, 16, 64);
     lt += __shfl_xor(lt, 32, 64);
-    float* slot = a.part + (static_cast<int64_t>(tc.s) * Hkv + tc.kvh + v) * slot_floats;
+    float* slot;
+    if constexpr (UNIT) slot = unit_slot<FUSED>(a, lds_i, wave);
+    else slot = a.part + (static_cast<int64_t>(tc.s) * Hkv + tc.kvh + v) * slot_floats;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int hd = 4 * g + r;
@@ -670,16 +758,23 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
       }
     }
   };
-  if (n_tiles >= (FUSED ? kFusedNtMin : kStreamNtMin)) stream(std::true_type{});
+  // One workgroup per unit (small batches) streams with ordinary loads: the
+  // ring's repeats of the wave's last tile then hit L2 rather than HBM, and
+  // the merge's registers wait for them.
+  if (!UNIT && n_tiles >= (FUSED ? kFusedNtMin : kStreamNtMin)) stream(std::true_type{});
   else stream(std::false_type{});
 }
 
-template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED, bool GPREF>
+template <typename T, int D, bool PAGE16, bool CONTIG, bool FUSED, bool GPREF, bool UNIT = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TSA_DECODE_WAVES_PER_EU)))
 void paged_decode_stream(DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ sl,
                          float* __restrict__ part) {
   extern __shared__ int lds_i[];
-  decode_stream_body<T, D, PAGE16, CONTIG, FUSED, GPREF>(a, bt, sl, part, lds_i);
+  decode_stream_body<T, D, PAGE16, CONTIG, FUSED, GPREF, UNIT>(a, bt, sl, part, lds_i);
+  if constexpr (UNIT) {
+    unit_barrier();
+    unit_merge<T, FUSED>(a, lds_i);
+  }
 }
 
 // The exclusive tile prefix over the sequences (pref_out[0..B], pref_out[B]
@@ -875,6 +970,7 @@ static int default_workgroups() {
 
 struct DecodePlan {
   int W;
+  bool unit;
   size_t part_bytes, pref_bytes, total;
 };
 
@@ -888,6 +984,16 @@ struct DecodePlan {
 // (Qwen3-0.6B batch of 4, 1024-tile tables: 11.5 us replayed at 128
 // workgroups against 12.6 at 256; a 56-tile batch 10.7 us at any grid).
 constexpr int kMinAutoWG = 64;
+// With no grid asked for, a batch of at most kUnitMaxUnits (sequence, kv
+// head) units whose block tables hold at most kUnitMaxTiles tiles per unit
+// takes one workgroup per unit instead: its four waves split the unit's
+// tiles, merge in LDS and write the output, so the call is one launch with
+// no merge launch after it. Such a call streams each unit's K/V through
+// one CU (about 1 us per 32 KB tile round of a workgroup, measured), so it
+// pays only while the units are few and short: the Qwen3-0.6B batch of 4
+// (32 units, 32-tile tables) went from 11.7 to 10.3-10.5 us replayed.
+constexpr int64_t kUnitMaxUnits = 64;
+constexpr int64_t kUnitMaxTiles = 32;
 static DecodePlan make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_blocks, int64_t BS,
                             int32_t num_workgroups) {
   DecodePlan p{};
@@ -895,12 +1001,18 @@ static DecodePlan make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64
   constexpr int64_t k31 = int64_t(1) << 31;
   if (num_workgroups == 0 && max_blocks > 0 && BS > 0 && max_blocks < k31 && BS < k31 && max_blocks * BS < k31 &&
       B < k31 && Hkv < k31 && B * Hkv < k31) {
-    const int64_t cap_tiles = Hkv * B * ((max_blocks * BS + 15) / 16);
+    const int64_t unit_tiles = (max_blocks * BS + 15) / 16;
+    const int64_t cap_tiles = Hkv * B * unit_tiles;
     const int64_t want = (cap_tiles + 2 * kWaves - 1) / (2 * kWaves);
     if (want < p.W) p.W = static_cast<int>(want < kMinAutoWG ? kMinAutoWG : want);
+    if (B > 0 && B * Hkv <= kUnitMaxUnits && unit_tiles <= kUnitMaxTiles) {
+      p.unit = true;
+      p.W = static_cast<int>(B * Hkv);
+    }
   }
   const int64_t G = Hq / Hkv;
-  const int64_t slots = B * Hkv + static_cast<int64_t>(kWaves) * p.W;
+  // (one workgroup per unit keeps its partials in LDS: no slots)
+  const int64_t slots = p.unit ? 0 : B * Hkv + static_cast<int64_t>(kWaves) * p.W;
   p.part_bytes = align256(static_cast<size_t>(slots) * G * (D + 2) * sizeof(float));
   p.pref_bytes = align256(static_cast<size_t>(B + 1) * sizeof(int32_t));
   p.total = p.part_bytes + p.pref_bytes;
@@ -944,6 +1056,28 @@ static int launch_decode(DecodeArgs& a, bool mfma, hipStream_t stream, bool fuse
     const bool page16 = a.BS % 16 == 0;
     const bool contig = a.kc_s == a.D && a.vc_s == a.D;
     const dim3 grid(a.W);
+    if (a.unit) {  // one workgroup per unit (the plan keeps such batches' prefixes in LDS), no merge launch
+      if (fused) {
+        paged_decode_stream<T, 128, true, true, true, false, true><<<grid, dim3(kThreads), fused_lds_bytes(a.B),
+                                                                    stream>>>(a, a.bt, a.seq_lens, a.part);
+        return check_launch("tsa_paged_decode");
+      }
+      const size_t lds_u = prefix_lds_bytes16(a.B) + static_cast<size_t>(kWaves) * unit_slot_floats(a.G, a.D) * 4;
+#define TSA_UNIT_LAUNCH(DD, P16, CT)                                                                       \
+  paged_decode_stream<T, DD, P16, CT, false, false, true><<<grid, dim3(kThreads), lds_u, stream>>>(a, a.bt, \
+                                                                                             a.seq_lens, a.part)
+      if (a.D == 128) {
+        if (page16 && contig) TSA_UNIT_LAUNCH(128, true, true);
+        else if (page16) TSA_UNIT_LAUNCH(128, true, false);
+        else TSA_UNIT_LAUNCH(128, false, false);
+      } else {
+        if (page16 && contig) TSA_UNIT_LAUNCH(64, true, true);
+        else if (page16) TSA_UNIT_LAUNCH(64, true, false);
+        else TSA_UNIT_LAUNCH(64, false, false);
+      }
+#undef TSA_UNIT_LAUNCH
+      return check_launch("tsa_paged_decode");
+    }
     if (gpref) {
       decode_tile_prefix<<<dim3(1), dim3(kPrefixThreads), 0, stream>>>(a);
       if (int rc = check_launch("tsa_paged_decode")) return rc;
@@ -1045,6 +1179,7 @@ static int check_decode(const tsa_view* out, const tsa_view* query, const tsa_vi
     plan = make_plan(B, Hq, Hkv, D, block_tables->size[1], BS, num_workgroups);
     a.W = plan.W;
     a.NW = kWaves * plan.W;
+    a.unit = plan.unit ? 1 : 0;
   }
   return TSA_OK;
 }
@@ -1189,6 +1324,8 @@ constexpr int kMixedLds = gqa_smem_bytes<128, 4>();
 constexpr int64_t kMixedAutoMaxTokens = 512;
 constexpr int64_t kMixedAutoMaxDecodeTokens = 131072;
 static_assert(kMixedLds >= 64 * 1024, "the mixed kernel's LDS also holds the decode tile prefixes (at most 64 KB)");
+static_assert(kMixedLds >= kWaves * (kUnitMaxUnits + 1) * 4 + 16 + kWaves * 16 * (128 + 2) * 4,
+              "the mixed kernel's LDS holds a unit-mode decode workgroup's prefixes and wave partials");
 static_assert(kThreads == 64 * 4 && TSA_DECODE_WAVES_PER_EU == 2,
               "the decode and prefill roles share a 4-wave workgroup compiled for two waves per SIMD");
 
@@ -1197,10 +1334,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     DecodeArgs d, const int32_t* __restrict__ bt, const int32_t* __restrict__ sl, float* __restrict__ part,
     PrefillArgs p, const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
   __shared__ __align__(16) char lds_m[kMixedLds];
-  if (static_cast<int>(blockIdx.x) < d.W)
-    decode_stream_body<T, 128, true, true, false>(d, bt, sl, part, reinterpret_cast<int*>(lds_m));
-  else
+  if (static_cast<int>(blockIdx.x) < d.W) {
+    if (d.unit) {  // one workgroup per decode unit, merged here (as tsa_paged_decode's plan takes it)
+      decode_stream_body<T, 128, true, true, false, false, true>(d, bt, sl, part, reinterpret_cast<int*>(lds_m));
+      unit_barrier();
+      unit_merge<T, false>(d, reinterpret_cast<int*>(lds_m));
+    } else {
+      decode_stream_body<T, 128, true, true, false>(d, bt, sl, part, reinterpret_cast<int*>(lds_m));
+    }
+  } else {
     prefill_gqa_body<T, 128, 4>(p, cu_q, cu_k, lds_m, d.W);
+  }
 }
 
 static int device_cus() {
@@ -1260,11 +1404,11 @@ extern "C" int tsa_mixed_attention(const tsa_view* prefill_out, const tsa_view* 
     mixed_attention_kernel<bf16_t><<<grid, dim3(kThreads), 0, st>>>(a, a.bt, a.seq_lens, a.part, pa, pa.cu_q,
                                                                      pa.cu_k);
     if (int rc = check_launch("tsa_mixed_attention")) return rc;
-    return launch_merge<bf16_t>(a, st);
+    return a.unit ? TSA_OK : launch_merge<bf16_t>(a, st);
   }
   mixed_attention_kernel<f16_t><<<grid, dim3(kThreads), 0, st>>>(a, a.bt, a.seq_lens, a.part, pa, pa.cu_q, pa.cu_k);
   if (int rc = check_launch("tsa_mixed_attention")) return rc;
-  return launch_merge<f16_t>(a, st);
+  return a.unit ? TSA_OK : launch_merge<f16_t>(a, st);
 }
 
 // ---------------------------------------------------------------------------

@@ -249,4 +249,75 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Inclusive scan over a wave's 64 lanes on DPP moves (no LDS round trip):
+// sums within rows of 16 lanes (row shifts by 1, 2, 4, 8; a lane whose
+// source lies before its row's start reads 0), then lane 15's sum added to
+// row 1 and lane 47's to row 3 (row_bcast:15), then lane 31's to rows 2
+// and 3 (row_bcast:31). These lane mappings were checked on the GPU. Every
+// lane of the wave must take part.
+template <int CTRL, int ROWS, bool BC>
+__device__ __forceinline__ uint32_t dpp32(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, ROWS, 0xf, BC));
+}
+template <int CTRL, int ROWS, bool BC>
+__device__ __forceinline__ uint64_t dpp64(uint64_t x) {
+  const uint32_t lo = dpp32<CTRL, ROWS, BC>(static_cast<uint32_t>(x));
+  const uint32_t hi = dpp32<CTRL, ROWS, BC>(static_cast<uint32_t>(x >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x) {
+  x += dpp32<0x111, 0xf, true>(x);
+  x += dpp32<0x112, 0xf, true>(x);
+  x += dpp32<0x114, 0xf, true>(x);
+  x += dpp32<0x118, 0xf, true>(x);
+  x += dpp32<0x142, 0xa, false>(x);
+  x += dpp32<0x143, 0xc, false>(x);
+  return x;
+}
+__device__ __forceinline__ uint64_t wave_scan_u64(uint64_t x) {
+  x += dpp64<0x111, 0xf, true>(x);
+  x += dpp64<0x112, 0xf, true>(x);
+  x += dpp64<0x114, 0xf, true>(x);
+  x += dpp64<0x118, 0xf, true>(x);
+  x += dpp64<0x142, 0xa, false>(x);
+  x += dpp64<0x143, 0xc, false>(x);
+  return x;
+}
+
+// The value held by lane (lane ^ J), for J a power of two below 64, without
+// an LDS round trip: quad permutes [1,0,3,2] and [2,3,0,1] for 1 and 2, a
+// row rotation by 8 for 8, rotations by 4 and 12 with a per-lane choice for
+// 4, and the half-row and half-wave swaps (v_permlane16_swap,
+// v_permlane32_swap, whose second result is the partner's value in the
+// lower half and whose first is it in the upper half) for 16 and 32. These
+// lane mappings were checked on the GPU. Every lane of the wave must take
+// part.
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane32(uint32_t v, int lane) {
+  if constexpr (J == 1) {
+    return dpp32<0xB1, 0xf, false>(v);
+  } else if constexpr (J == 2) {
+    return dpp32<0x4E, 0xf, false>(v);
+  } else if constexpr (J == 4) {
+    // (row_ror:n: lane l reads lane (l - n) mod 16 of its row.)
+    const uint32_t up = dpp32<0x12C, 0xf, false>(v), down = dpp32<0x124, 0xf, false>(v);
+    return (lane & 4) ? down : up;
+  } else if constexpr (J == 8) {
+    return dpp32<0x128, 0xf, false>(v);
+  } else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    static_assert(J == 32, "xor_lane32: J in {1, 2, 4, 8, 16, 32}");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+template <int J>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v, int lane) {
+  const uint32_t lo = xor_lane32<J>(static_cast<uint32_t>(v), lane);
+  const uint32_t hi = xor_lane32<J>(static_cast<uint32_t>(v >> 32), lane);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 }  // namespace tsa

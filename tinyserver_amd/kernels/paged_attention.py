@@ -67,8 +67,10 @@ def paged_attention_forward(
     ``seq_lens[s]`` tokens gathered through ``block_tables[s]``; q-head h reads
     kv head ``h // (Hq / Hkv)``. query: (B, Hq, D); caches (NB, Hkv, BS, D);
     block_tables (B, max_blocks) int32; seq_lens (B,) int32.
-    ``num_workgroups`` (workgroups sharing the tile list, 0 = one per CU) and
-    ``out`` are extensions; the defaults reproduce the reference call.
+    ``num_workgroups`` (workgroups sharing the tile list; 0 = the library's
+    choice, which for at most 64 (sequence, kv head) units with tables of at
+    most 512 tokens is one workgroup per unit and no merge launch) and ``out``
+    are extensions; the defaults reproduce the reference call.
     """
     if query.dim() != 3:
         raise ValueError(f"query must be a 3D tensor, but got shape {query.shape}")
