@@ -256,6 +256,19 @@ def _decode_pools(w, copies):
     return [(w.k_cache, w.v_cache)] + [(w.k_cache.clone(), w.v_cache.clone()) for _ in range(copies - 1)]
 
 
+def _decode_kernels(w, page, num_workgroups):
+    """The launches of one decode call: a workspace of the tile prefix alone
+    (no partial slots) is the library's one-workgroup-per-unit form."""
+    from tinyserver_amd.kernels.paged_attention import decode_workspace_bytes
+
+    B = len(w.ctx_lens)
+    ws = decode_workspace_bytes(B, w.num_heads, w.num_kv_heads, w.q.shape[-1], w.block_tables.shape[1], page,
+                                num_workgroups)
+    if ws <= (4 * (B + 1) + 255) // 256 * 256:
+        return "paged_decode_stream (one workgroup per unit, no merge launch)"
+    return "paged_decode_stream + paged_decode_stream_merge"
+
+
 def bench_decode(name, steps, warmup, num_workgroups=0, copies=3, with_block=False, **make_kw):
     from tinyserver_amd import workloads as W
     from tinyserver_amd.kernels import paged_attention_forward, paged_decode_step, qk_norm_rope_store
@@ -288,7 +301,7 @@ def bench_decode(name, steps, warmup, num_workgroups=0, copies=3, with_block=Fal
         "us_per_call": us, "us_per_call_median": spread["median"], "us_per_call_p10": spread["p10"],
         "us_per_call_p90": spread["p90"], "wall_ms_per_step": wall_ms,
         "achieved_gbs": nbytes / (us * 1e-6) / 1e9, "tokens_per_s": B / (us * 1e-6),
-        "roofline": {**_roof_hbm(nbytes, us), "kernel": "paged_decode_stream + paged_decode_stream_merge"},
+        "roofline": {**_roof_hbm(nbytes, us), "kernel": _decode_kernels(w, page, num_workgroups)},
     }
     res["pct_peak_hbm"] = 100.0 * res["achieved_gbs"] / HBM_PEAK_GBS
     if with_block:
