@@ -1397,30 +1397,37 @@ struct RowSampler {
     // bucket's count is the step to the next bucket's prefix (the last
     // bucket's to V: every element is in one bucket).
     const size_t base = static_cast<size_t>(srow) * a.S * kBuckets;
-    for (int b = tid; b < kBuckets; b += kSampThreads) {
-      uint32_t c = 0;
-      uint64_t m = 0;
-      // Eight segments per step, every load (at a clamped segment) issued
-      // before any is summed: one step for the usual 8 segments.
-      for (int w0 = 0; w0 < a.S; w0 += 8) {
-        uint32_t cw[8];
-        uint64_t mw[8];
+    static_assert(kBuckets == 2 * kSampThreads, "two buckets per thread");
+    // Thread t takes buckets 2t and 2t + 1: one 8-byte count load and one
+    // 16-byte mass load per segment. Eight segments per step, every load (at
+    // a clamped segment) issued before any is summed: one round trip for
+    // the usual 8 segments.
+    u32x2 c = {0u, 0u};
+    uint64_t m0 = 0, m1 = 0;
+    for (int w0 = 0; w0 < a.S; w0 += 8) {
+      u32x2 cw[8];
+      u32x4 mw[8];
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
-          const size_t at = base + static_cast<size_t>(min(w0 + w, a.S - 1)) * kBuckets + b;
-          cw[w] = a.plp[at];
-          mw[w] = a.pmass[at];
-        }
-        __builtin_amdgcn_sched_barrier(0);
+      for (int w = 0; w < 8; ++w) {
+        const size_t at = base + static_cast<size_t>(min(w0 + w, a.S - 1)) * kBuckets + 2 * tid;
+        cw[w] = *reinterpret_cast<const u32x2*>(a.plp + at);
+        mw[w] = *reinterpret_cast<const u32x4*>(a.pmass + at);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
-          c += w0 + w < a.S ? cw[w] : 0u;
-          m += w0 + w < a.S ? mw[w] : uint64_t{0};
+      for (int w = 0; w < 8; ++w) {
+        if (w0 + w < a.S) {
+          c[0] += cw[w][0];
+          c[1] += cw[w][1];
+          m0 += (static_cast<uint64_t>(mw[w][1]) << 32) | mw[w][0];
+          m1 += (static_cast<uint64_t>(mw[w][3]) << 32) | mw[w][2];
         }
       }
-      s.pcnt[b] = c;
-      s.wsum[b] = m;
     }
+    s.pcnt[2 * tid] = c[0];
+    s.pcnt[2 * tid + 1] = c[1];
+    s.wsum[2 * tid] = m0;
+    s.wsum[2 * tid + 1] = m1;
     __syncthreads();
     for (int b = tid; b < kBuckets; b += kSampThreads)
       s.cnt[b] = (b + 1 < kBuckets ? s.pcnt[b + 1] : static_cast<uint32_t>(a.V)) - s.pcnt[b];
