@@ -47,6 +47,10 @@
 // * A second kernel merges, per unit, the partials of the wave workers whose
 //   runs cover it with a log-sum-exp reduce. The kernel boundary orders the
 //   two, so no cache flushes or atomics are needed; no host sync, no memset.
+// * Small batches (at most 64 units, tables of at most 512 tokens, no grid
+//   asked for) run one workgroup per unit instead: its four waves split the
+//   unit's tiles through the same ring, leave their partials in LDS, and
+//   the workgroup merges them and writes the output. One launch.
 //
 // Tokens past seq_len are scored -inf and their V rows zeroed (the
 // reference's masked loads, :88-105). seq_len is clamped to the block table's
