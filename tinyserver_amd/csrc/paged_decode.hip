@@ -359,8 +359,8 @@ __device__ __forceinline__ void decode_stream_body(DecodeArgs a, const int32_t* 
   // One workgroup per unit, 16-token pages: lane i holds the unit's block-table
   // entry i, loaded beside the sequence lengths, and each tile's page id is a
   // lane read rather than a dependent scalar load. (The plan takes this form
-  // only for tables of at most 64 tiles per unit, so 16-token or larger pages
-  // give at most 64 entries.)
+  // only for tables of at most kUnitMaxTiles = 32 tiles per unit, so 16-token
+  // or larger pages give at most 32 entries, within the wave's 64 lanes.)
   int btv = 0;
   if constexpr (UNIT && PAGE16) {
     const int us = blockIdx.x / Hkv;
@@ -998,6 +998,7 @@ constexpr int kMinAutoWG = 64;
 // (32 units, 32-tile tables) went from 11.7 to 10.3-10.5 us replayed.
 constexpr int64_t kUnitMaxUnits = 64;
 constexpr int64_t kUnitMaxTiles = 32;
+static_assert(kUnitMaxTiles <= 64, "a unit's block-table row (16-token or larger pages) fits one wave's lanes");
 static DecodePlan make_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_blocks, int64_t BS,
                             int32_t num_workgroups) {
   DecodePlan p{};
