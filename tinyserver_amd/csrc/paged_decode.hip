@@ -992,10 +992,10 @@ constexpr int kMinAutoWG = 64;
 // head) units whose block tables hold at most kUnitMaxTiles tiles per unit
 // takes one workgroup per unit instead: its four waves split the unit's
 // tiles, merge in LDS and write the output, so the call is one launch with
-// no merge launch after it. Such a call streams each unit's K/V through
-// one CU (about 1 us per 32 KB tile round of a workgroup, measured), so it
-// pays only while the units are few and short: the Qwen3-0.6B batch of 4
-// (32 units, 32-tile tables) went from 11.7 to 10.3-10.5 us replayed.
+// no merge launch after it. Its waves compute their tiles one after
+// another (about 0.7 us of computation per tile, measured), so it pays only
+// while the units are few and short: the Qwen3-0.6B batch of 4 (32 units,
+// 32-tile tables) went from 11.7 to 10.3-10.5 us replayed.
 constexpr int64_t kUnitMaxUnits = 64;
 constexpr int64_t kUnitMaxTiles = 32;
 static_assert(kUnitMaxTiles <= 64, "a unit's block-table row (16-token or larger pages) fits one wave's lanes");
